@@ -1,0 +1,150 @@
+/*
+ * sketchpad_attn.h — C ABI of the MI355X (gfx950) ragged-batch attention path.
+ *
+ * The library replaces the attention hot path of rhi-zone/sketchpad:
+ *   - the paged KV-cache append      (PagedKvCache::store_kv,  crates/sketchpad-core/src/paged_attention.rs:230-310)
+ *   - the paged KV-cache gather      (PagedKvCache::gather_kv, crates/sketchpad-core/src/paged_attention.rs:313-378)
+ *   - cached decode attention         (MultiHeadAttention::forward_cached with Sq == 1,
+ *                                      crates/sketchpad-core/src/transformer.rs:184-271)
+ *   - causal / windowed prefill        (flash_attention, crates/sketchpad-cubecl/src/attention.rs:97-178,
+ *                                      and the dense masked path, transformer.rs:103-168, :415-451)
+ *   - chunked prefill against a cache  (forward_cached with Sq > 1 and prefill_causal_mask,
+ *                                      crates/sketchpad-llm/src/llama.rs:250-260, :374-388)
+ *
+ * Conventions (all entry points):
+ *   - Plain pointers and sizes only. Device pointers are HIP device addresses; the stream is a
+ *     hipStream_t passed as void* (NULL = the default stream). Work is enqueued on that stream
+ *     and nothing synchronises the host.
+ *   - Return SP_OK (0) on success, a nonzero sp_status otherwise; sp_last_error() then returns a
+ *     thread-local message. Nothing is thrown, aborted or exited across the ABI.
+ *   - No entry point allocates device memory. Scratch space is caller-owned (workspace).
+ *   - Calls are stateless and re-entrant; two calls that share a workspace must not overlap.
+ *
+ * Paged pool layout (the reference's, paged_attention.rs:152-155):
+ *   pool[num_blocks][num_layers][num_kv_heads][block_size][head_dim], one pool for K, one for V.
+ *   A position `pos` of a sequence with block table `table` lives at
+ *   block = table[pos / block_size], slot = pos % block_size (BlockTable::get_block/get_slot,
+ *   paged_attention.rs:124-132). A slot-mapping entry is block * block_size + slot.
+ *
+ * Grouped-query attention (repeat_kv, transformer.rs:257-271): query head h reads KV head
+ * h / (num_q_heads / num_kv_heads).
+ *
+ * Attention window: `window_left` = how many keys before the query's own position stay visible;
+ * -1 means no limit. The reference's two conventions map to it as:
+ *   sliding_window_mask(W)          (transformer.rs:436-451, keys [i-W, i])   -> window_left = W
+ *   sliding_window_prefill_mask(W)  (gemma4.rs:1086-1108, keys [p-W+1, p])    -> window_left = W-1
+ */
+#ifndef SKETCHPAD_ATTN_H
+#define SKETCHPAD_ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SP_ABI_VERSION 1
+
+typedef enum sp_status {
+    SP_OK = 0,
+    SP_EINVAL = 1,        /* a size, pointer or combination of arguments is invalid          */
+    SP_EUNSUPPORTED = 2,  /* valid, but this build has no kernel for it (dtype, head_dim...) */
+    SP_EHIP = 3,          /* the HIP runtime reported an error (launch, device query)          */
+    SP_EOOB = 4,          /* an index addresses memory outside the pool / table               */
+    SP_ENOSPACE = 5       /* the caller's workspace is smaller than required                  */
+} sp_status;
+
+typedef enum sp_dtype {
+    SP_F32 = 0,
+    SP_BF16 = 1,
+    SP_F16 = 2
+} sp_dtype;
+
+/* Causal alignment of the prefill mask when a sequence has Lq queries and Lk keys. */
+typedef enum sp_causal {
+    SP_CAUSAL_NONE = 0,          /* no causal mask (bidirectional)                                  */
+    SP_CAUSAL_BOTTOM_RIGHT = 1,  /* query i sits at position Lk-Lq+i: prefill_causal_mask,
+                                    llama.rs:374-388 (== causal_mask when Lq == Lk)              */
+    SP_CAUSAL_TOP_LEFT = 2       /* query i sits at position i: the flash-attention test oracle,
+                                    sketchpad-cubecl/tests/correctness_cpu.rs:1066-1074         */
+} sp_causal;
+
+/* Geometry of one layer's view into a paged pool (PagedKvCacheConfig, paged_attention.rs:35-86). */
+typedef struct sp_cache_layout {
+    int32_t num_blocks;    /* blocks in the pool                                  */
+    int32_t num_layers;    /* layers interleaved in every block                   */
+    int32_t layer;         /* the layer this call reads or writes (0..num_layers) */
+    int32_t num_kv_heads;  /* Hkv                                                 */
+    int32_t block_size;    /* tokens per block (BS)                               */
+    int32_t head_dim;      /* D                                                   */
+} sp_cache_layout;
+
+/* ABI version (SP_ABI_VERSION) and the message of the last failed call on this thread. */
+int sp_version(void);
+const char* sp_last_error(void);
+
+/*
+ * Cache append: scatter new K/V rows into the paged pools through a slot mapping.
+ * Replaces PagedKvCache::store_kv + store_single_kv (paged_attention.rs:230-310), batched over
+ * any number of sequences: token t of the batch is written to
+ *   pool[slot_mapping[t] / BS][layer][h][slot_mapping[t] % BS][:] = new[t, h, :]
+ * for every KV head h. The copy is bit-exact. A negative slot skips the token; a slot at or past
+ * num_blocks * block_size is skipped by the kernel (never written) — callers validate slots on
+ * the host first (the reference panics "Block not allocated", paged_attention.rs:242).
+ * k_new / v_new element (t, h, d) lives at t*token_stride + h*head_stride + d (elements), so
+ * token-major [T, Hkv, D] input uses (Hkv*D, D) and the reference's head-major [Hkv, T, D] uses
+ * (D, T*D).
+ */
+int sp_kv_append(void* k_pool, void* v_pool, const sp_cache_layout* layout,
+                 const void* k_new, const void* v_new,
+                 int64_t token_stride, int64_t head_stride,
+                 const int32_t* slot_mapping, int32_t num_tokens,
+                 sp_dtype dtype, void* stream);
+
+/*
+ * Cache gather: copy one sequence's first seq_len positions out of the pools into contiguous
+ * k_out / v_out of shape [Hkv, seq_len, D]. Replaces PagedKvCache::gather_kv
+ * (paged_attention.rs:313-378); seq_len == 0 is a no-op (the reference returns [Hkv, 0, D]).
+ * block_table is a device array of num_table_blocks block ids; positions whose block index is
+ * past the table make the call fail with SP_EOOB before any launch.
+ */
+int sp_kv_gather(void* k_out, void* v_out,
+                 const void* k_pool, const void* v_pool, const sp_cache_layout* layout,
+                 const int32_t* block_table, int32_t num_table_blocks, int32_t seq_len,
+                 sp_dtype dtype, void* stream);
+
+/*
+ * Bytes of workspace sp_paged_decode needs for the given batch shape. max_context_len bounds
+ * every context_lens[] entry.
+ */
+size_t sp_paged_decode_workspace_size(int32_t num_seqs, int32_t num_q_heads,
+                                      int32_t max_context_len, int32_t window_left,
+                                      const sp_cache_layout* layout);
+
+/*
+ * Paged decode attention: one query token per sequence against its paged context.
+ * Replaces, for Sq == 1, PagedAttentionCache::update_layer's gather (paged_attention.rs:519-548)
+ * followed by repeat_kv + softmax((q k^T) * scale) v (transformer.rs:227-243). Decode applies
+ * no mask in the reference (llama.rs:255-260); window_left >= 0 restricts sequence s to keys
+ * [context_lens[s]-1-window_left, context_lens[s]) (Mistral window: window_left = W).
+ *   q, out         : [num_seqs, num_q_heads, D] contiguous, dtype
+ *   block_tables   : [num_seqs, max_blocks_per_seq] int32 (device)
+ *   context_lens   : [num_seqs] int32 (device), each in [0, max_context_len]; the count
+ *                    includes the token just appended. A zero-length context yields zeros.
+ *   workspace      : device scratch of at least sp_paged_decode_workspace_size() bytes.
+ * Softmax and accumulation are fp32 for every dtype.
+ */
+int sp_paged_decode(void* out, const void* q,
+                    const void* k_pool, const void* v_pool, const sp_cache_layout* layout,
+                    const int32_t* block_tables, int32_t max_blocks_per_seq,
+                    const int32_t* context_lens, int32_t max_context_len,
+                    int32_t num_seqs, int32_t num_q_heads,
+                    float scale, int32_t window_left, sp_dtype dtype,
+                    void* workspace, size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SKETCHPAD_ATTN_H */

@@ -1,0 +1,239 @@
+"""ctypes front end of the C oracle (oracle/sp_oracle.c).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() (as the checker) and
+bench.py's cpu_baseline leg. The product never imports it. Each function names the reference
+item it restates; sp_oracle.h lists the check that pins it.
+"""
+from __future__ import annotations
+
+import ctypes
+from ctypes import POINTER, c_double, c_float, c_int, c_int32, c_int64, c_void_p
+from pathlib import Path
+
+import numpy as np
+
+LIB_PATH = Path(__file__).resolve().parent / "build" / "libsp_oracle.so"
+
+F32, BF16, F16 = 0, 1, 2
+
+
+class Layout(ctypes.Structure):
+    _fields_ = [("num_blocks", c_int32), ("num_layers", c_int32), ("layer", c_int32),
+                ("num_kv_heads", c_int32), ("block_size", c_int32), ("head_dim", c_int32)]
+
+
+_SIG = {
+    "spo_get_block": (c_int64, [c_void_p, c_int64, c_int64, c_int]),
+    "spo_get_slot": (c_int64, [c_int64, c_int]),
+    "spo_needs_new_block": (c_int, [c_int64, c_int]),
+    "spo_blocks_needed": (c_int64, [c_int64, c_int]),
+    "spo_blocks_from_memory_budget": (c_int64, [c_int64, c_int64, c_int64, c_int64, c_int64]),
+    "spo_slot_mapping": (c_int, [c_void_p, c_int64, c_int64, c_int64, c_int, c_void_p]),
+    "spo_store_kv": (c_int, [c_void_p, c_void_p, POINTER(Layout), c_void_p, c_int64, c_void_p,
+                             c_void_p, c_int64, c_int64, c_int]),
+    "spo_gather_kv": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, POINTER(Layout), c_void_p,
+                              c_int64, c_int64, c_int]),
+    "spo_causal_mask": (None, [c_int64, c_void_p]),
+    "spo_prefill_causal_mask": (None, [c_int64, c_int64, c_void_p]),
+    "spo_sliding_window_mask": (None, [c_int64, c_int64, c_void_p]),
+    "spo_sliding_window_prefill_mask": (None, [c_int64, c_int64, c_int64, c_void_p]),
+    "spo_attention_f64": (None, [c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_int64,
+                                 c_int64, c_int64, c_int64, c_int, c_int, c_int, c_double,
+                                 c_void_p, c_int, c_int64, c_int64, c_int, c_void_p]),
+    "spo_attention_f32_refops": (None, [c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_int64,
+                                        c_int64, c_int64, c_int64, c_int, c_int, c_int, c_float,
+                                        c_void_p, c_int, c_int64, c_int64, c_int, c_void_p]),
+    "spo_cpu_decode_baseline": (None, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+                                       c_void_p, POINTER(Layout), c_void_p, c_int64, c_void_p,
+                                       c_int64, c_int, c_float, c_int64, c_int]),
+    "spo_cpu_prefill_baseline": (None, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+                                        c_int64, c_int, c_int, c_int, c_float, c_int]),
+}
+
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(f"{LIB_PATH} missing: run oracle/build.sh")
+        l = ctypes.CDLL(str(LIB_PATH))
+        for name, (res, args) in _SIG.items():
+            fn = getattr(l, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = l
+    return _lib
+
+
+def _p(a: np.ndarray | None):
+    return None if a is None else a.ctypes.data_as(c_void_p)
+
+
+def _c(a, dtype=None):
+    return np.ascontiguousarray(a if dtype is None else np.asarray(a, dtype=dtype))
+
+
+def _dtype_code(a: np.ndarray, dtype: int | None) -> int:
+    if dtype is not None:
+        return dtype
+    if a.dtype == np.float32:
+        return F32
+    if a.dtype == np.uint16:
+        return BF16
+    raise TypeError(f"oracle: unsupported array dtype {a.dtype}")
+
+
+def make_layout(num_blocks, num_layers, layer, num_kv_heads, block_size, head_dim) -> Layout:
+    return Layout(num_blocks, num_layers, layer, num_kv_heads, block_size, head_dim)
+
+
+# --- BlockTable arithmetic (paged_attention.rs:124-137) ---------------------------------------
+
+def get_block(table, pos: int, block_size: int):
+    t = _c(table, np.int32)
+    r = lib().spo_get_block(_p(t), len(t), pos, block_size)
+    return None if r < 0 else int(r)
+
+
+def get_slot(pos: int, block_size: int) -> int:
+    return int(lib().spo_get_slot(pos, block_size))
+
+
+def needs_new_block(seq_len: int, block_size: int) -> bool:
+    return bool(lib().spo_needs_new_block(seq_len, block_size))
+
+
+def blocks_needed(new_len: int, block_size: int) -> int:
+    return int(lib().spo_blocks_needed(new_len, block_size))
+
+
+def blocks_from_memory_budget(memory_bytes, num_kv_heads, head_dim, num_layers, block_size):
+    return int(lib().spo_blocks_from_memory_budget(memory_bytes, num_kv_heads, head_dim,
+                                                   num_layers, block_size))
+
+
+def slot_mapping(table, start_pos: int, count: int, block_size: int) -> np.ndarray | None:
+    t = _c(table, np.int32)
+    out = np.empty(count, dtype=np.int32)
+    rc = lib().spo_slot_mapping(_p(t), len(t), start_pos, count, block_size, _p(out))
+    return None if rc else out
+
+
+# --- store_kv / gather_kv (paged_attention.rs:230-378) ----------------------------------------
+
+def store_kv(k_pool: np.ndarray, v_pool: np.ndarray, lay: Layout, table, k: np.ndarray,
+             v: np.ndarray, start_pos: int) -> int:
+    """In place on the pools. k, v are [Hkv, S, D] (the reference's head-major layout)."""
+    assert k_pool.flags.c_contiguous and v_pool.flags.c_contiguous
+    t = _c(table, np.int32)
+    k, v = _c(k), _c(v)
+    return int(lib().spo_store_kv(_p(k_pool), _p(v_pool), ctypes.byref(lay), _p(t), len(t), _p(k),
+                                  _p(v), k.shape[1], start_pos, k.itemsize))
+
+
+def gather_kv(k_pool: np.ndarray, v_pool: np.ndarray, lay: Layout, table, seq_len: int):
+    t = _c(table, np.int32)
+    shape = (lay.num_kv_heads, seq_len, lay.head_dim)
+    ko = np.zeros(shape, dtype=k_pool.dtype)
+    vo = np.zeros(shape, dtype=v_pool.dtype)
+    rc = lib().spo_gather_kv(_p(ko), _p(vo), _p(_c(k_pool)), _p(_c(v_pool)), ctypes.byref(lay),
+                             _p(t), len(t), seq_len, k_pool.itemsize)
+    if rc:
+        raise IndexError("gather_kv: table does not cover seq_len")
+    return ko, vo
+
+
+# --- masks -------------------------------------------------------------------------------------
+
+def causal_mask(n: int) -> np.ndarray:
+    out = np.empty((n, n), dtype=np.float32)
+    lib().spo_causal_mask(n, _p(out))
+    return out
+
+
+def prefill_causal_mask(new_len: int, total_len: int) -> np.ndarray:
+    out = np.empty((new_len, total_len), dtype=np.float32)
+    lib().spo_prefill_causal_mask(new_len, total_len, _p(out))
+    return out
+
+
+def sliding_window_mask(n: int, window: int) -> np.ndarray:
+    out = np.empty((n, n), dtype=np.float32)
+    lib().spo_sliding_window_mask(n, window, _p(out))
+    return out
+
+
+def sliding_window_prefill_mask(new_len: int, total_len: int, window: int) -> np.ndarray:
+    out = np.empty((new_len, total_len), dtype=np.float32)
+    lib().spo_sliding_window_prefill_mask(new_len, total_len, window, _p(out))
+    return out
+
+
+# --- attention --------------------------------------------------------------------------------
+
+def attention_f64(q, k, v, *, scale: float, mask=None, causal: bool = False, q_pos0: int = 0,
+                  window_left: int = -1, dtype: int | None = None) -> np.ndarray:
+    """q [Sq, Hq, D], k/v [Lk, Hkv, D] (float32, or uint16 bf16 bits) -> float64 [Sq, Hq, D]."""
+    q, k, v = _c(q), _c(k), _c(v)
+    dt = _dtype_code(q, dtype)
+    sq, hq, d = q.shape
+    lk, hkv, _ = k.shape
+    out = np.empty((sq, hq, d), dtype=np.float64)
+    m = None if mask is None else _c(mask, np.float32)
+    lib().spo_attention_f64(_p(q), hq * d, d, _p(k), _p(v), hkv * d, d, sq, lk, hq, hkv, d,
+                            scale, _p(m), int(causal), q_pos0, window_left, dt, _p(out))
+    return out
+
+
+def attention_f32_refops(q, k, v, *, scale: float, mask=None, causal: bool = False,
+                         q_pos0: int = 0, window_left: int = -1,
+                         dtype: int | None = None) -> np.ndarray:
+    """The reference's f32 op order (transformer.rs:234-243) -> float32 [Sq, Hq, D]."""
+    q, k, v = _c(q), _c(k), _c(v)
+    dt = _dtype_code(q, dtype)
+    sq, hq, d = q.shape
+    lk, hkv, _ = k.shape
+    out = np.empty((sq, hq, d), dtype=np.float32)
+    m = None if mask is None else _c(mask, np.float32)
+    lib().spo_attention_f32_refops(_p(q), hq * d, d, _p(k), _p(v), hkv * d, d, sq, lk, hq, hkv,
+                                   d, scale, _p(m), int(causal), q_pos0, window_left, dt, _p(out))
+    return out
+
+
+def paged_decode_f64(q, k_pool, v_pool, lay: Layout, block_tables, context_lens, *, scale: float,
+                     window_left: int = -1, dtype: int | None = None) -> np.ndarray:
+    """Reference decode for a batch: per sequence gather_kv (paged_attention.rs:313-378), then
+    softmax((q k^T) scale) v over all gathered keys (decode has no mask, llama.rs:255-260),
+    optionally restricted to the last window_left+1 keys. -> float64 [B, Hq, D]."""
+    q = _c(q)
+    b, hq, d = q.shape
+    out = np.zeros((b, hq, d), dtype=np.float64)
+    for s in range(b):
+        L = int(context_lens[s])
+        if L == 0:
+            continue
+        kg, vg = gather_kv(k_pool, v_pool, lay, block_tables[s], L)  # [Hkv, L, D]
+        kt = np.ascontiguousarray(kg.transpose(1, 0, 2))               # [L, Hkv, D]
+        vt = np.ascontiguousarray(vg.transpose(1, 0, 2))
+        out[s] = attention_f64(q[s:s + 1], kt, vt, scale=scale, causal=True, q_pos0=L - 1,
+                               window_left=window_left, dtype=dtype)[0]
+    return out
+
+
+def cpu_decode_baseline(out, q, k_new, v_new, k_pool, v_pool, lay: Layout, block_tables,
+                        context_lens, *, scale: float, window_left: int = -1, threads: int = 0):
+    """Timed CPU port of the reference's decode op sequence (all float32 arrays, in place)."""
+    bt = _c(block_tables, np.int32)
+    cl = _c(context_lens, np.int32)
+    lib().spo_cpu_decode_baseline(_p(out), _p(q), _p(k_new), _p(v_new), _p(k_pool), _p(v_pool),
+                                  ctypes.byref(lay), _p(bt), bt.shape[1], _p(cl), len(cl),
+                                  q.shape[1], scale, window_left, threads)
+
+
+def cpu_prefill_baseline(out, q, k, v, cu_seqlens, *, hq: int, hkv: int, d: int, scale: float,
+                         threads: int = 0):
+    cu = _c(cu_seqlens, np.int32)
+    lib().spo_cpu_prefill_baseline(_p(out), _p(q), _p(k), _p(v), _p(cu), len(cu) - 1, hq, hkv, d,
+                                   scale, threads)

@@ -1,0 +1,421 @@
+/*
+ * sp_oracle.c — CPU restatement of the reference's ragged-batch attention path.
+ *
+ * TEST INFRASTRUCTURE ONLY: the checker for tests/, smoke() and bench.py's cpu_baseline leg.
+ * The product never links it. See sp_oracle.h for the reference file:line each function
+ * restates and the check that pins it.
+ */
+#include "sp_oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+/* ------------------------------------------------------------------------------------------ */
+/* element conversion                                                                          */
+/* ------------------------------------------------------------------------------------------ */
+
+static float bf16_to_f32(uint16_t b) {
+  uint32_t u = (uint32_t)b << 16;
+  float f;
+  memcpy(&f, &u, 4);
+  return f;
+}
+
+static float f16_to_f32(uint16_t h) {
+  const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+  uint32_t exp = (h >> 10) & 0x1fu;
+  uint32_t man = h & 0x3ffu;
+  uint32_t u;
+  if (exp == 0) {
+    if (man == 0) {
+      u = sign;
+    } else { /* subnormal: renormalise */
+      exp = 127 - 15 + 1;
+      while ((man & 0x400u) == 0) {
+        man <<= 1;
+        exp--;
+      }
+      man &= 0x3ffu;
+      u = sign | (exp << 23) | (man << 13);
+    }
+  } else if (exp == 31) {
+    u = sign | 0x7f800000u | (man << 13);
+  } else {
+    u = sign | ((exp + 127 - 15) << 23) | (man << 13);
+  }
+  float f;
+  memcpy(&f, &u, 4);
+  return f;
+}
+
+static float load_elem(const void* p, int64_t i, int dtype) {
+  switch (dtype) {
+    case SPO_BF16: return bf16_to_f32(((const uint16_t*)p)[i]);
+    case SPO_F16: return f16_to_f32(((const uint16_t*)p)[i]);
+    default: return ((const float*)p)[i];
+  }
+}
+
+/* ------------------------------------------------------------------------------------------ */
+/* BlockTable / PagedKvCacheConfig arithmetic (paged_attention.rs:67-85, :124-137, :403-404)    */
+/* ------------------------------------------------------------------------------------------ */
+
+int64_t spo_get_block(const int32_t* table, int64_t num_table_blocks, int64_t pos,
+                      int block_size) {
+  const int64_t block_num = pos / block_size; /* paged_attention.rs:125 */
+  if (block_num < 0 || block_num >= num_table_blocks) return -1; /* None (:126) */
+  return table[block_num];
+}
+
+int64_t spo_get_slot(int64_t pos, int block_size) { return pos % block_size; /* :131 */ }
+
+int spo_needs_new_block(int64_t seq_len, int block_size) {
+  return seq_len > 0 && seq_len % block_size == 0; /* :136 */
+}
+
+int64_t spo_blocks_needed(int64_t new_len, int block_size) {
+  return (new_len + block_size - 1) / block_size; /* div_ceil, :404 */
+}
+
+int64_t spo_blocks_from_memory_budget(int64_t memory_bytes, int64_t num_kv_heads,
+                                      int64_t head_dim, int64_t num_layers, int64_t block_size) {
+  /* 2 (K+V) * layers * heads * head_dim * block_size * 4 bytes (f32), :75-76 */
+  const int64_t per_block = 2 * num_layers * num_kv_heads * head_dim * block_size * 4;
+  return per_block > 0 ? memory_bytes / per_block : 0;
+}
+
+/* ------------------------------------------------------------------------------------------ */
+/* store_kv / gather_kv (paged_attention.rs:230-378)                                            */
+/* ------------------------------------------------------------------------------------------ */
+
+int spo_slot_mapping(const int32_t* table, int64_t num_table_blocks, int64_t start_pos,
+                     int64_t count, int block_size, int32_t* out) {
+  for (int64_t i = 0; i < count; ++i) {
+    const int64_t pos = start_pos + i;
+    const int64_t blk = spo_get_block(table, num_table_blocks, pos, block_size);
+    if (blk < 0) return -1; /* "Block not allocated", :242 */
+    out[i] = (int32_t)(blk * block_size + spo_get_slot(pos, block_size));
+  }
+  return 0;
+}
+
+static int64_t pool_offset(const spo_layout* l, int64_t blk, int64_t head, int64_t slot) {
+  /* [num_blocks][num_layers][Hkv][BS][D] element offset of row (blk, layer, head, slot) */
+  return (((blk * l->num_layers + l->layer) * l->num_kv_heads + head) * l->block_size + slot) *
+         l->head_dim;
+}
+
+int spo_store_kv(void* k_pool, void* v_pool, const spo_layout* l, const int32_t* table,
+                 int64_t num_table_blocks, const void* k, const void* v, int64_t seq_len,
+                 int64_t start_pos, int elem_size) {
+  const int64_t row = (int64_t)l->head_dim * elem_size;
+  for (int64_t i = 0; i < seq_len; ++i) { /* :240 */
+    const int64_t pos = start_pos + i;
+    const int64_t blk = spo_get_block(table, num_table_blocks, pos, l->block_size);
+    if (blk < 0 || blk >= l->num_blocks) return -1; /* panic "Block not allocated" */
+    const int64_t slot = spo_get_slot(pos, l->block_size);
+    for (int64_t h = 0; h < l->num_kv_heads; ++h) {
+      /* k is [Hkv, seq_len, D] (:234); cache[blk, layer, h, slot, :] = k[h, i, :] (:289-298) */
+      const int64_t src = (h * seq_len + i) * row;
+      const int64_t dst = pool_offset(l, blk, h, slot) * elem_size;
+      memcpy((char*)k_pool + dst, (const char*)k + src, (size_t)row);
+      memcpy((char*)v_pool + dst, (const char*)v + src, (size_t)row);
+    }
+  }
+  return 0;
+}
+
+int spo_gather_kv(void* k_out, void* v_out, const void* k_pool, const void* v_pool,
+                  const spo_layout* l, const int32_t* table, int64_t num_table_blocks,
+                  int64_t seq_len, int elem_size) {
+  if (seq_len == 0) return 0; /* [Hkv, 0, D], :322-327 */
+  if (spo_blocks_needed(seq_len, l->block_size) > num_table_blocks) return -1;
+  const int64_t row = (int64_t)l->head_dim * elem_size;
+  for (int64_t b = 0; b < num_table_blocks; ++b) { /* :333 */
+    const int64_t start = b * l->block_size;
+    if (start >= seq_len) break;
+    int64_t end = start + l->block_size;
+    if (end > seq_len) end = seq_len; /* :335 */
+    const int64_t blk = table[b];
+    if (blk < 0 || blk >= l->num_blocks) return -1;
+    for (int64_t h = 0; h < l->num_kv_heads; ++h) {
+      for (int64_t t = start; t < end; ++t) { /* slice + reshape + cat along seq (:340-375) */
+        const int64_t src = pool_offset(l, blk, h, t - start) * elem_size;
+        const int64_t dst = (h * seq_len + t) * row;
+        memcpy((char*)k_out + dst, (const char*)k_pool + src, (size_t)row);
+        memcpy((char*)v_out + dst, (const char*)v_pool + src, (size_t)row);
+      }
+    }
+  }
+  return 0;
+}
+
+/* ------------------------------------------------------------------------------------------ */
+/* masks                                                                                       */
+/* ------------------------------------------------------------------------------------------ */
+
+void spo_causal_mask(int64_t n, float* out) { /* transformer.rs:415-424 */
+  for (int64_t i = 0; i < n; ++i)
+    for (int64_t j = 0; j < n; ++j) out[i * n + j] = j > i ? -INFINITY : 0.f;
+}
+
+void spo_prefill_causal_mask(int64_t new_len, int64_t total_len, float* out) {
+  const int64_t start = total_len - new_len; /* llama.rs:379 */
+  for (int64_t i = 0; i < new_len; ++i)
+    for (int64_t j = 0; j < total_len; ++j) out[i * total_len + j] = j > start + i ? -INFINITY : 0.f;
+}
+
+void spo_sliding_window_mask(int64_t n, int64_t window, float* out) { /* transformer.rs:436-451 */
+  for (int64_t i = 0; i < n; ++i)
+    for (int64_t j = 0; j < n; ++j)
+      out[i * n + j] = (j > i || i > j + window) ? -INFINITY : 0.f; /* :445 */
+}
+
+void spo_sliding_window_prefill_mask(int64_t new_len, int64_t total_len, int64_t window,
+                                     float* out) { /* gemma4.rs:1086-1108 */
+  const int64_t start = total_len - new_len;
+  for (int64_t i = 0; i < new_len; ++i) {
+    const int64_t p = start + i;
+    for (int64_t j = 0; j < total_len; ++j) {
+      float m = 0.f;
+      if (j > p) m = -INFINITY;
+      if (p >= window && j < p - window + 1) m = -INFINITY; /* :1102 */
+      out[i * total_len + j] = m;
+    }
+  }
+}
+
+/* ------------------------------------------------------------------------------------------ */
+/* attention                                                                                   */
+/* ------------------------------------------------------------------------------------------ */
+
+static int visible(int causal, int64_t q_pos0, int64_t window_left, int64_t i, int64_t j) {
+  const int64_t p = q_pos0 + i;
+  if (causal && j > p) return 0;
+  if (window_left >= 0 && j < p - window_left) return 0;
+  return 1;
+}
+
+void spo_attention_f64(const void* q, int64_t q_tok, int64_t q_head, const void* k,
+                       const void* v, int64_t kv_tok, int64_t kv_head, int64_t sq, int64_t lk,
+                       int hq, int hkv, int d, double scale, const float* mask, int causal,
+                       int64_t q_pos0, int64_t window_left, int dtype, double* out) {
+  const int rep = hq / hkv; /* repeat_kv: head h reads KV head h / rep (transformer.rs:263-270) */
+  double* s = (double*)malloc(sizeof(double) * (size_t)(lk > 0 ? lk : 1));
+  for (int h = 0; h < hq; ++h) {
+    const int g = h / rep;
+    for (int64_t i = 0; i < sq; ++i) {
+      double m = -INFINITY;
+      for (int64_t j = 0; j < lk; ++j) {
+        double acc = 0.0;
+        for (int c = 0; c < d; ++c)
+          acc += (double)load_elem(q, i * q_tok + h * q_head + c, dtype) *
+                 (double)load_elem(k, j * kv_tok + g * kv_head + c, dtype);
+        acc *= scale; /* scale after the product (transformer.rs:234-235) */
+        if (mask)
+          acc += (double)mask[i * lk + j];
+        else if (!visible(causal, q_pos0, window_left, i, j))
+          acc = -INFINITY;
+        s[j] = acc;
+        if (acc > m) m = acc;
+      }
+      double* o = out + (i * hq + h) * d;
+      for (int c = 0; c < d; ++c) o[c] = 0.0;
+      if (m == -INFINITY) continue; /* no visible key (or no keys): zeros */
+      double sum = 0.0;
+      for (int64_t j = 0; j < lk; ++j) {
+        s[j] = exp(s[j] - m); /* softmax(dim 3), max-subtracted (transformer.rs:242) */
+        sum += s[j];
+      }
+      for (int64_t j = 0; j < lk; ++j) {
+        if (s[j] == 0.0) continue;
+        const double pj = s[j] / sum;
+        for (int c = 0; c < d; ++c) o[c] += pj * (double)load_elem(v, j * kv_tok + g * kv_head + c, dtype);
+      }
+    }
+  }
+  free(s);
+}
+
+void spo_attention_f32_refops(const void* q, int64_t q_tok, int64_t q_head, const void* k,
+                              const void* v, int64_t kv_tok, int64_t kv_head, int64_t sq,
+                              int64_t lk, int hq, int hkv, int d, float scale, const float* mask,
+                              int causal, int64_t q_pos0, int64_t window_left, int dtype,
+                              float* out) {
+  const int rep = hq / hkv;
+  const int64_t lk1 = lk > 0 ? lk : 1;
+  float* s = (float*)malloc(sizeof(float) * (size_t)lk1);
+  float* kr = (float*)malloc(sizeof(float) * (size_t)(lk1 * d)); /* repeat_kv copy, per head */
+  float* vr = (float*)malloc(sizeof(float) * (size_t)(lk1 * d));
+  for (int h = 0; h < hq; ++h) {
+    const int g = h / rep;
+    for (int64_t j = 0; j < lk; ++j)
+      for (int c = 0; c < d; ++c) {
+        kr[j * d + c] = load_elem(k, j * kv_tok + g * kv_head + c, dtype);
+        vr[j * d + c] = load_elem(v, j * kv_tok + g * kv_head + c, dtype);
+      }
+    for (int64_t i = 0; i < sq; ++i) {
+      float m = -INFINITY;
+      for (int64_t j = 0; j < lk; ++j) {
+        float acc = 0.f; /* q.matmul(k^T) */
+        for (int c = 0; c < d; ++c) acc += load_elem(q, i * q_tok + h * q_head + c, dtype) * kr[j * d + c];
+        acc = acc * scale; /* * scale */
+        if (mask)
+          acc = acc + mask[i * lk + j]; /* + mask */
+        else if (!visible(causal, q_pos0, window_left, i, j))
+          acc = -INFINITY;
+        s[j] = acc;
+        if (acc > m) m = acc;
+      }
+      float* o = out + (i * hq + h) * d;
+      for (int c = 0; c < d; ++c) o[c] = 0.f;
+      if (m == -INFINITY) continue;
+      float sum = 0.f; /* softmax: exp(x - max) / sum */
+      for (int64_t j = 0; j < lk; ++j) {
+        s[j] = expf(s[j] - m);
+        sum += s[j];
+      }
+      for (int64_t j = 0; j < lk; ++j) s[j] = s[j] / sum;
+      for (int64_t j = 0; j < lk; ++j) /* attn.matmul(v) */
+        for (int c = 0; c < d; ++c) o[c] += s[j] * vr[j * d + c];
+    }
+  }
+  free(s);
+  free(kr);
+  free(vr);
+}
+
+/* ------------------------------------------------------------------------------------------ */
+/* timed CPU baselines (the reference's op sequence, f32, OpenMP)                              */
+/* ------------------------------------------------------------------------------------------ */
+
+static float dot_f32(const float* a, const float* b, int n) {
+  float acc = 0.f;
+#pragma omp simd reduction(+ : acc)
+  for (int c = 0; c < n; ++c) acc += a[c] * b[c];
+  return acc;
+}
+
+/* softmax over row[0..n), in place, max-subtracted; returns 0 when every entry is -inf */
+static int softmax_row(float* row, int64_t n) {
+  float m = -INFINITY;
+  for (int64_t j = 0; j < n; ++j) m = row[j] > m ? row[j] : m;
+  if (m == -INFINITY) return 0;
+  float sum = 0.f;
+  for (int64_t j = 0; j < n; ++j) {
+    row[j] = expf(row[j] - m);
+    sum += row[j];
+  }
+  const float inv = 1.f / sum;
+  for (int64_t j = 0; j < n; ++j) row[j] *= inv;
+  return 1;
+}
+
+void spo_cpu_decode_baseline(float* out, const float* q, const float* k_new, const float* v_new,
+                             float* k_pool, float* v_pool, const spo_layout* l,
+                             const int32_t* block_tables, int64_t max_blocks_per_seq,
+                             const int32_t* context_lens, int64_t num_seqs, int hq, float scale,
+                             int64_t window_left, int threads) {
+  const int hkv = l->num_kv_heads, d = l->head_dim;
+  const int rep = hq / hkv;
+#ifdef _OPENMP
+  if (threads > 0) omp_set_num_threads(threads);
+#endif
+#pragma omp parallel for schedule(dynamic, 1)
+  for (int64_t s = 0; s < num_seqs; ++s) {
+    const int64_t len = context_lens[s];
+    const int32_t* table = block_tables + s * max_blocks_per_seq;
+    float* o = out + s * hq * d;
+    if (len <= 0) {
+      memset(o, 0, sizeof(float) * (size_t)hq * d);
+      continue;
+    }
+    /* 1. store the new token at position len-1 (store_kv, per head) */
+    spo_store_kv(k_pool, v_pool, l, table, max_blocks_per_seq, k_new + s * hkv * d,
+                 v_new + s * hkv * d, 1, len - 1, 4);
+    /* 2. gather: per-block slices concatenated into [Hkv, len, D] */
+    float* kg = (float*)malloc(sizeof(float) * (size_t)(hkv * len * d));
+    float* vg = (float*)malloc(sizeof(float) * (size_t)(hkv * len * d));
+    spo_gather_kv(kg, vg, k_pool, v_pool, l, table, max_blocks_per_seq, len, 4);
+    /* 3. repeat_kv materialised: [Hq, len, D] */
+    float* kr = (float*)malloc(sizeof(float) * (size_t)(hq * len * d));
+    float* vr = (float*)malloc(sizeof(float) * (size_t)(hq * len * d));
+    for (int h = 0; h < hq; ++h) {
+      memcpy(kr + (int64_t)h * len * d, kg + (int64_t)(h / rep) * len * d, sizeof(float) * (size_t)(len * d));
+      memcpy(vr + (int64_t)h * len * d, vg + (int64_t)(h / rep) * len * d, sizeof(float) * (size_t)(len * d));
+    }
+    /* 4. scores = (q k^T) * scale (+ window mask), softmax, out = p v */
+    float* sc = (float*)malloc(sizeof(float) * (size_t)(hq * len));
+    for (int h = 0; h < hq; ++h) {
+      const float* qh = q + (s * hq + h) * d;
+      float* row = sc + (int64_t)h * len;
+      for (int64_t j = 0; j < len; ++j) row[j] = dot_f32(qh, kr + ((int64_t)h * len + j) * d, d) * scale;
+      if (window_left >= 0)
+        for (int64_t j = 0; j < len; ++j)
+          if (j < len - 1 - window_left) row[j] += -INFINITY;
+      float* oh = o + h * d;
+      for (int c = 0; c < d; ++c) oh[c] = 0.f;
+      if (!softmax_row(row, len)) continue;
+      for (int64_t j = 0; j < len; ++j) {
+        const float pj = row[j];
+        const float* vj = vr + ((int64_t)h * len + j) * d;
+#pragma omp simd
+        for (int c = 0; c < d; ++c) oh[c] += pj * vj[c];
+      }
+    }
+    free(sc);
+    free(kr);
+    free(vr);
+    free(kg);
+    free(vg);
+  }
+}
+
+void spo_cpu_prefill_baseline(float* out, const float* q, const float* k, const float* v,
+                              const int32_t* cu_seqlens, int64_t num_seqs, int hq, int hkv,
+                              int d, float scale, int threads) {
+  const int rep = hq / hkv;
+#ifdef _OPENMP
+  if (threads > 0) omp_set_num_threads(threads);
+#endif
+#pragma omp parallel for collapse(2) schedule(dynamic, 1)
+  for (int64_t s = 0; s < num_seqs; ++s) {
+    for (int h = 0; h < hq; ++h) {
+      const int64_t t0 = cu_seqlens[s], len = cu_seqlens[s + 1] - cu_seqlens[s];
+      if (len <= 0) continue;
+      const int g = h / rep;
+      /* repeat_kv copy of this head's K/V, contiguous [len, D] */
+      float* kh = (float*)malloc(sizeof(float) * (size_t)(len * d));
+      float* vh = (float*)malloc(sizeof(float) * (size_t)(len * d));
+      for (int64_t j = 0; j < len; ++j) {
+        memcpy(kh + j * d, k + ((t0 + j) * hkv + g) * d, sizeof(float) * (size_t)d);
+        memcpy(vh + j * d, v + ((t0 + j) * hkv + g) * d, sizeof(float) * (size_t)d);
+      }
+      /* [len, len] scores, * scale, + causal mask, softmax, matmul */
+      float* sc = (float*)malloc(sizeof(float) * (size_t)(len * len));
+      for (int64_t i = 0; i < len; ++i) {
+        const float* qi = q + ((t0 + i) * hq + h) * d;
+        float* row = sc + i * len;
+        for (int64_t j = 0; j < len; ++j) row[j] = dot_f32(qi, kh + j * d, d) * scale;
+        for (int64_t j = i + 1; j < len; ++j) row[j] += -INFINITY;
+        softmax_row(row, len);
+        float* oi = out + ((t0 + i) * hq + h) * d;
+        for (int c = 0; c < d; ++c) oi[c] = 0.f;
+        for (int64_t j = 0; j < len; ++j) {
+          const float pj = row[j];
+          const float* vj = vh + j * d;
+#pragma omp simd
+          for (int c = 0; c < d; ++c) oi[c] += pj * vj[c];
+        }
+      }
+      free(sc);
+      free(kh);
+      free(vh);
+    }
+  }
+}

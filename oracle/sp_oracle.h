@@ -1,0 +1,120 @@
+/*
+ * sp_oracle.h — CPU restatement of the reference's ragged-batch attention path.
+ *
+ * TEST INFRASTRUCTURE ONLY. Nothing in the product (sketchpad_amd/, include/) links or calls
+ * this code. It is used by tests/ as the checker, by __graft_entry__.smoke() as the checker and
+ * by bench.py's cpu_baseline leg as the timed CPU port of the reference's op sequence.
+ *
+ * Every function restates a reference item (file:line under rhi-zone/sketchpad) and states how
+ * it is pinned (see the test named after it):
+ *   spo_get_block / spo_get_slot / spo_needs_new_block    paged_attention.rs:124-137
+ *       pinned: the reference's test_block_table known answers (paged_attention.rs:568-598)
+ *   spo_blocks_needed                                     paged_attention.rs:403-404, :504-505
+ *       pinned: test_paged_scheduler counts (3 tokens -> 1 block, 5 -> 2; :623-645)
+ *   spo_blocks_from_memory_budget                         paged_attention.rs:67-85
+ *       pinned: test_config_from_memory_budget (1 GiB -> 256 blocks; :648-661)
+ *   spo_store_kv / spo_slot_mapping                       paged_attention.rs:230-310
+ *       pinned: gather(store(x)) == x, untouched slots stay zero, closed-form addresses,
+ *               and the numpy restatement (oracle/np_oracle.py)
+ *   spo_gather_kv                                         paged_attention.rs:313-378
+ *       pinned: empty gather (test_gather_kv_empty, :664-674) + round trip + concat-cache
+ *               equivalence (KvCache::update, kv_cache.rs:108-130)
+ *   spo_causal_mask / spo_sliding_window_mask             transformer.rs:415-451
+ *       pinned: test_causal_mask and test_sliding_window_mask entries (transformer.rs:524-561)
+ *   spo_prefill_causal_mask                               llama.rs:374-388
+ *   spo_sliding_window_prefill_mask                       gemma4.rs:1086-1108
+ *       pinned: reduce to causal_mask when new_len == total_len; brute-force predicate checks
+ *   spo_attention_f64                                     transformer.rs:227-243 (+ repeat_kv :257-271)
+ *       pinned: torch.nn.functional.scaled_dot_product_attention in float64 (a library
+ *               routine), closed forms (one key -> v; equal keys -> mean(v); dominant key -> its v),
+ *               GQA == repeated-head MHA, mask-rule == explicit additive mask
+ *   spo_attention_f32_refops                              transformer.rs:234-243 op order in f32
+ *       pinned: within f32 rounding of spo_attention_f64 on every test case
+ *   spo_cpu_decode_baseline / spo_cpu_prefill_baseline    the reference's whole decode / prefill
+ *       op sequence (store, gather+concat, repeat_kv, matmul, scale, mask, softmax, matmul), f32,
+ *       OpenMP over sequences; pinned against spo_attention_f64.
+ */
+#ifndef SP_ORACLE_H
+#define SP_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Same field order as sp_cache_layout (include/sketchpad_attn.h). */
+typedef struct spo_layout {
+  int32_t num_blocks, num_layers, layer, num_kv_heads, block_size, head_dim;
+} spo_layout;
+
+/* element types of the tensors handed to the oracle */
+enum { SPO_F32 = 0, SPO_BF16 = 1, SPO_F16 = 2 };
+
+int64_t spo_get_block(const int32_t* table, int64_t num_table_blocks, int64_t pos, int block_size);
+int64_t spo_get_slot(int64_t pos, int block_size);
+int spo_needs_new_block(int64_t seq_len, int block_size);
+int64_t spo_blocks_needed(int64_t new_len, int block_size);
+int64_t spo_blocks_from_memory_budget(int64_t memory_bytes, int64_t num_kv_heads, int64_t head_dim,
+                                      int64_t num_layers, int64_t block_size);
+
+int spo_slot_mapping(const int32_t* table, int64_t num_table_blocks, int64_t start_pos,
+                     int64_t count, int block_size, int32_t* out);
+int spo_store_kv(void* k_pool, void* v_pool, const spo_layout* layout, const int32_t* table,
+                 int64_t num_table_blocks, const void* k, const void* v, int64_t seq_len,
+                 int64_t start_pos, int elem_size);
+int spo_gather_kv(void* k_out, void* v_out, const void* k_pool, const void* v_pool,
+                  const spo_layout* layout, const int32_t* table, int64_t num_table_blocks,
+                  int64_t seq_len, int elem_size);
+
+void spo_causal_mask(int64_t n, float* out);
+void spo_prefill_causal_mask(int64_t new_len, int64_t total_len, float* out);
+void spo_sliding_window_mask(int64_t n, int64_t window, float* out);
+void spo_sliding_window_prefill_mask(int64_t new_len, int64_t total_len, int64_t window,
+                                     float* out);
+
+/*
+ * Attention of one sequence. q element (i, h, d) is at q[i*q_tok + h*q_head + d]; k/v (j, g, d)
+ * at [j*kv_tok + g*kv_head + d]. Query head h reads KV head h / (Hq / Hkv). Key j is visible to
+ * query i when mask == NULL and
+ *   (!causal || j <= q_pos0 + i) && (window_left < 0 || j >= q_pos0 + i - window_left)
+ * or, with an explicit mask, the additive mask[i*Lk + j] is added to the scaled score.
+ * out is [Sq, Hq, D] (double for _f64, float for _f32_refops). A row with no visible key is 0.
+ */
+void spo_attention_f64(const void* q, int64_t q_tok, int64_t q_head, const void* k,
+                       const void* v, int64_t kv_tok, int64_t kv_head, int64_t sq, int64_t lk,
+                       int hq, int hkv, int d, double scale, const float* mask, int causal,
+                       int64_t q_pos0, int64_t window_left, int dtype, double* out);
+void spo_attention_f32_refops(const void* q, int64_t q_tok, int64_t q_head, const void* k,
+                              const void* v, int64_t kv_tok, int64_t kv_head, int64_t sq,
+                              int64_t lk, int hq, int hkv, int d, float scale, const float* mask,
+                              int causal, int64_t q_pos0, int64_t window_left, int dtype,
+                              float* out);
+
+/*
+ * Timed CPU baseline of one decode step in the reference's op order, OpenMP over sequences.
+ * For each sequence s: store the new token's k/v ([Hkv, D] at position L_s-1) into the pools,
+ * gather [Hkv, L_s, D], materialise repeat_kv, scores = (q k^T) * scale, softmax, out = p v.
+ * Pools are f32 (the reference's NdArray<f32>); q/k_new/v_new are f32. out is [B, Hq, D].
+ */
+void spo_cpu_decode_baseline(float* out, const float* q, const float* k_new, const float* v_new,
+                             float* k_pool, float* v_pool, const spo_layout* layout,
+                             const int32_t* block_tables, int64_t max_blocks_per_seq,
+                             const int32_t* context_lens, int64_t num_seqs, int hq, float scale,
+                             int64_t window_left, int threads);
+
+/*
+ * Timed CPU baseline of causal prefill over packed sequences in the reference's op order:
+ * per sequence, repeat_kv, [Hq, L, L] f32 scores, scale, + causal mask, softmax, matmul.
+ * q [T, Hq, D], k/v [T, Hkv, D] f32, cu_seqlens [num_seqs+1]; out [T, Hq, D].
+ */
+void spo_cpu_prefill_baseline(float* out, const float* q, const float* k, const float* v,
+                              const int32_t* cu_seqlens, int64_t num_seqs, int hq, int hkv,
+                              int d, float scale, int threads);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -1,0 +1,23 @@
+"""MI355X-native ragged-batch attention for rhi-zone/sketchpad's paged/flash attention path.
+
+The product is the C-ABI library ``lib/libsketchpad_attn.so`` (include/sketchpad_attn.h) built
+from the gfx950 HIP kernels under ``csrc/``, plus the C++ mirror of the reference's paged-cache
+API under ``host/``. This package only binds the library for Python callers (tests, bench).
+"""
+from ._lib import (  # noqa: F401
+    CacheLayout,
+    SketchpadError,
+    SP_BF16,
+    SP_CAUSAL_BOTTOM_RIGHT,
+    SP_CAUSAL_NONE,
+    SP_CAUSAL_TOP_LEFT,
+    SP_F16,
+    SP_F32,
+    alloc_decode_workspace,
+    kv_append,
+    kv_gather,
+    layout,
+    load,
+    paged_decode,
+    paged_decode_workspace_size,
+)

@@ -1,0 +1,176 @@
+"""ctypes binding of the C ABI in include/sketchpad_attn.h.
+
+The shared library is built in-tree by ``python -m sketchpad_amd.build`` (or
+``__graft_entry__.build()``). Loading fails loudly when it is missing: there is no CPU or
+PyTorch fallback for any entry point.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from ctypes import POINTER, c_float, c_int32, c_int64, c_size_t, c_void_p
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "lib" / "libsketchpad_attn.so"
+HEADER = Path(__file__).resolve().parent.parent / "include" / "sketchpad_attn.h"
+
+SP_OK, SP_EINVAL, SP_EUNSUPPORTED, SP_EHIP, SP_EOOB, SP_ENOSPACE = range(6)
+SP_F32, SP_BF16, SP_F16 = 0, 1, 2
+SP_CAUSAL_NONE, SP_CAUSAL_BOTTOM_RIGHT, SP_CAUSAL_TOP_LEFT = 0, 1, 2
+
+STATUS_NAMES = {
+    SP_OK: "SP_OK",
+    SP_EINVAL: "SP_EINVAL",
+    SP_EUNSUPPORTED: "SP_EUNSUPPORTED",
+    SP_EHIP: "SP_EHIP",
+    SP_EOOB: "SP_EOOB",
+    SP_ENOSPACE: "SP_ENOSPACE",
+}
+
+
+class SketchpadError(RuntimeError):
+    """A nonzero sp_status, with the library's message."""
+
+    def __init__(self, code: int, message: str):
+        super().__init__(f"{STATUS_NAMES.get(code, code)}: {message}")
+        self.code = code
+        self.message = message
+
+
+class CacheLayout(ctypes.Structure):
+    """sp_cache_layout: one layer's view of a [num_blocks, num_layers, Hkv, BS, D] pool."""
+
+    _fields_ = [
+        ("num_blocks", c_int32),
+        ("num_layers", c_int32),
+        ("layer", c_int32),
+        ("num_kv_heads", c_int32),
+        ("block_size", c_int32),
+        ("head_dim", c_int32),
+    ]
+
+    def __repr__(self) -> str:
+        return ("CacheLayout(num_blocks={0.num_blocks}, num_layers={0.num_layers}, "
+                "layer={0.layer}, num_kv_heads={0.num_kv_heads}, block_size={0.block_size}, "
+                "head_dim={0.head_dim})").format(self)
+
+
+_SIGNATURES = {
+    "sp_version": (c_int32, []),
+    "sp_last_error": (ctypes.c_char_p, []),
+    "sp_kv_append": (c_int32, [c_void_p, c_void_p, POINTER(CacheLayout), c_void_p, c_void_p,
+                               c_int64, c_int64, c_void_p, c_int32, c_int32, c_void_p]),
+    "sp_kv_gather": (c_int32, [c_void_p, c_void_p, c_void_p, c_void_p, POINTER(CacheLayout),
+                               c_void_p, c_int32, c_int32, c_int32, c_void_p]),
+    "sp_paged_decode_workspace_size": (c_size_t, [c_int32, c_int32, c_int32, c_int32,
+                                                  POINTER(CacheLayout)]),
+    "sp_paged_decode": (c_int32, [c_void_p, c_void_p, c_void_p, c_void_p, POINTER(CacheLayout),
+                                  c_void_p, c_int32, c_void_p, c_int32, c_int32, c_int32,
+                                  c_float, c_int32, c_int32, c_void_p, c_size_t, c_void_p]),
+}
+
+_lib = None
+
+
+def load() -> ctypes.CDLL:
+    """Load libsketchpad_attn.so (once) and bind every entry point's signature."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not LIB_PATH.exists():
+        raise RuntimeError(
+            f"{LIB_PATH} is missing: build it with `python -m sketchpad_amd.build` "
+            "(there is no fallback path)")
+    lib = ctypes.CDLL(str(LIB_PATH))
+    for name, (res, args) in _SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+def check(code: int) -> None:
+    if code != SP_OK:
+        raise SketchpadError(code, load().sp_last_error().decode())
+
+
+def layout(num_blocks: int, num_layers: int, layer: int, num_kv_heads: int, block_size: int,
+           head_dim: int) -> CacheLayout:
+    return CacheLayout(num_blocks, num_layers, layer, num_kv_heads, block_size, head_dim)
+
+
+# ---------------------------------------------------------------------------------------------
+# torch-tensor helpers: torch only supplies device memory and the stream.
+# ---------------------------------------------------------------------------------------------
+
+def _torch():
+    import torch
+    return torch
+
+
+def sp_dtype(t) -> int:
+    torch = _torch()
+    m = {torch.float32: SP_F32, torch.bfloat16: SP_BF16, torch.float16: SP_F16}
+    if t.dtype not in m:
+        raise SketchpadError(SP_EUNSUPPORTED, f"dtype {t.dtype} has no kernel")
+    return m[t.dtype]
+
+
+def _ptr(t) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _stream(stream) -> int | None:
+    if stream is not None:
+        return stream
+    torch = _torch()
+    return torch.cuda.current_stream().cuda_stream
+
+
+def kv_append(k_pool, v_pool, lay: CacheLayout, k_new, v_new, slot_mapping, *,
+              token_stride: int | None = None, head_stride: int | None = None,
+              stream=None) -> None:
+    """sp_kv_append. k_new/v_new default to token-major [T, Hkv, D] contiguous tensors."""
+    if token_stride is None:
+        token_stride = k_new.stride(0)
+    if head_stride is None:
+        head_stride = k_new.stride(1)
+    assert slot_mapping.dtype == _torch().int32
+    check(load().sp_kv_append(_ptr(k_pool), _ptr(v_pool), ctypes.byref(lay), _ptr(k_new),
+                              _ptr(v_new), token_stride, head_stride, _ptr(slot_mapping),
+                              slot_mapping.numel(), sp_dtype(k_pool), _stream(stream)))
+
+
+def kv_gather(k_out, v_out, k_pool, v_pool, lay: CacheLayout, block_table, seq_len: int, *,
+              stream=None) -> None:
+    """sp_kv_gather into [Hkv, seq_len, D] tensors."""
+    check(load().sp_kv_gather(_ptr(k_out), _ptr(v_out), _ptr(k_pool), _ptr(v_pool),
+                              ctypes.byref(lay), _ptr(block_table), block_table.numel(), seq_len,
+                              sp_dtype(k_pool), _stream(stream)))
+
+
+def paged_decode_workspace_size(num_seqs: int, num_q_heads: int, max_context_len: int,
+                                window_left: int, lay: CacheLayout) -> int:
+    return int(load().sp_paged_decode_workspace_size(num_seqs, num_q_heads, max_context_len,
+                                                     window_left, ctypes.byref(lay)))
+
+
+def paged_decode(out, q, k_pool, v_pool, lay: CacheLayout, block_tables, context_lens,
+                 max_context_len: int, scale: float, *, window_left: int = -1, workspace=None,
+                 stream=None) -> None:
+    """sp_paged_decode. q/out are [num_seqs, Hq, D]; block_tables [num_seqs, max_blocks]."""
+    num_seqs, hq = q.shape[0], q.shape[1]
+    ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    check(load().sp_paged_decode(_ptr(out), _ptr(q), _ptr(k_pool), _ptr(v_pool),
+                                 ctypes.byref(lay), _ptr(block_tables), block_tables.shape[1],
+                                 _ptr(context_lens), max_context_len, num_seqs, hq, scale,
+                                 window_left, sp_dtype(q), _ptr(workspace), ws_bytes,
+                                 _stream(stream)))
+
+
+def alloc_decode_workspace(num_seqs: int, num_q_heads: int, max_context_len: int,
+                           window_left: int, lay: CacheLayout, device="cuda"):
+    torch = _torch()
+    n = paged_decode_workspace_size(num_seqs, num_q_heads, max_context_len, window_left, lay)
+    return torch.empty(max(n, 16), dtype=torch.uint8, device=device)

@@ -1,0 +1,214 @@
+// C-ABI entry points (include/sketchpad_attn.h): argument validation, geometry, launches.
+//
+// Every entry point checks its arguments on the host before anything is enqueued, turns each
+// failure into an sp_status plus a thread-local message, and never throws across the ABI.
+#include <stdarg.h>
+#include <math.h>
+#include <stdio.h>
+
+#include <string>
+
+#include "kv_cache.hpp"
+#include "paged_decode.hpp"
+#include "sp_common.hpp"
+
+namespace sp {
+
+static thread_local std::string g_last_error;
+
+void set_error(const std::string& msg) { g_last_error = msg; }
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+int check_launch(const char* what) {
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(SP_EHIP, "%s: launch failed: %s", what, hipGetErrorString(e));
+  return SP_OK;
+}
+
+static int check_dtype(sp_dtype dt, const char* fn) {
+  if (dt != SP_F32 && dt != SP_BF16 && dt != SP_F16)
+    return fail(SP_EINVAL, "%s: unknown dtype %d", fn, (int)dt);
+  return SP_OK;
+}
+
+static int check_layout(const sp_cache_layout* l, const char* fn) {
+  if (!l) return fail(SP_EINVAL, "%s: layout is NULL", fn);
+  if (l->num_blocks <= 0 || l->num_layers <= 0 || l->num_kv_heads <= 0 || l->block_size <= 0 ||
+      l->head_dim <= 0)
+    return fail(SP_EINVAL,
+                "%s: layout sizes must be positive (num_blocks=%d num_layers=%d num_kv_heads=%d "
+                "block_size=%d head_dim=%d)",
+                fn, l->num_blocks, l->num_layers, l->num_kv_heads, l->block_size, l->head_dim);
+  if (l->layer < 0 || l->layer >= l->num_layers)
+    return fail(SP_EOOB, "%s: layer %d outside [0, %d)", fn, l->layer, l->num_layers);
+  return SP_OK;
+}
+
+// Byte strides of the reference pool layout [num_blocks][num_layers][Hkv][BS][D].
+static void pool_strides(const sp_cache_layout* l, int es, int64_t* block_stride_b,
+                         int64_t* layer_off_b) {
+  const int64_t layer_elems = (int64_t)l->num_kv_heads * l->block_size * l->head_dim;
+  *block_stride_b = layer_elems * l->num_layers * es;
+  *layer_off_b = layer_elems * l->layer * es;
+}
+
+}  // namespace sp
+
+using namespace sp;
+
+extern "C" {
+
+int sp_version(void) { return SP_ABI_VERSION; }
+
+const char* sp_last_error(void) { return g_last_error.c_str(); }
+
+int sp_kv_append(void* k_pool, void* v_pool, const sp_cache_layout* layout, const void* k_new,
+                 const void* v_new, int64_t token_stride, int64_t head_stride,
+                 const int32_t* slot_mapping, int32_t num_tokens, sp_dtype dtype, void* stream) {
+  const char* fn = "sp_kv_append";
+  if (int rc = check_layout(layout, fn)) return rc;
+  if (int rc = check_dtype(dtype, fn)) return rc;
+  if (num_tokens < 0) return fail(SP_EINVAL, "%s: num_tokens %d < 0", fn, num_tokens);
+  if (num_tokens == 0) return SP_OK;
+  if (!k_pool || !v_pool || !k_new || !v_new || !slot_mapping)
+    return fail(SP_EINVAL, "%s: NULL pointer argument", fn);
+  if (token_stride < 0 || head_stride < 0)
+    return fail(SP_EINVAL, "%s: negative stride", fn);
+  const int es = dtype_size(dtype);
+  KvAppendArgs a{};
+  a.kpool = (char*)k_pool;
+  a.vpool = (char*)v_pool;
+  a.knew = (const char*)k_new;
+  a.vnew = (const char*)v_new;
+  a.tok_stride_b = token_stride * es;
+  a.head_stride_b = head_stride * es;
+  a.slots = slot_mapping;
+  a.num_tokens = num_tokens;
+  a.hkv = layout->num_kv_heads;
+  a.row_bytes = layout->head_dim * es;
+  a.block_size = layout->block_size;
+  pool_strides(layout, es, &a.block_stride_b, &a.layer_off_b);
+  a.num_slots = (int64_t)layout->num_blocks * layout->block_size;
+  return launch_kv_append(a, (hipStream_t)stream);
+}
+
+int sp_kv_gather(void* k_out, void* v_out, const void* k_pool, const void* v_pool,
+                 const sp_cache_layout* layout, const int32_t* block_table,
+                 int32_t num_table_blocks, int32_t seq_len, sp_dtype dtype, void* stream) {
+  const char* fn = "sp_kv_gather";
+  if (int rc = check_layout(layout, fn)) return rc;
+  if (int rc = check_dtype(dtype, fn)) return rc;
+  if (seq_len < 0) return fail(SP_EINVAL, "%s: seq_len %d < 0", fn, seq_len);
+  if (seq_len == 0) return SP_OK;
+  if (!k_out || !v_out || !k_pool || !v_pool || !block_table)
+    return fail(SP_EINVAL, "%s: NULL pointer argument", fn);
+  const int64_t needed = ((int64_t)seq_len + layout->block_size - 1) / layout->block_size;
+  if (num_table_blocks < needed)
+    return fail(SP_EOOB, "%s: seq_len %d needs %lld blocks, the table holds %d", fn, seq_len,
+                (long long)needed, num_table_blocks);
+  const int es = dtype_size(dtype);
+  KvGatherArgs a{};
+  a.kout = (char*)k_out;
+  a.vout = (char*)v_out;
+  a.kpool = (const char*)k_pool;
+  a.vpool = (const char*)v_pool;
+  a.table = block_table;
+  a.seq_len = seq_len;
+  a.hkv = layout->num_kv_heads;
+  a.row_bytes = layout->head_dim * es;
+  a.block_size = layout->block_size;
+  pool_strides(layout, es, &a.block_stride_b, &a.layer_off_b);
+  a.num_blocks = layout->num_blocks;
+  return launch_kv_gather(a, (hipStream_t)stream);
+}
+
+size_t sp_paged_decode_workspace_size(int32_t num_seqs, int32_t num_q_heads,
+                                      int32_t max_context_len, int32_t window_left,
+                                      const sp_cache_layout* layout) {
+  if (!layout || layout->num_kv_heads <= 0 || num_seqs <= 0 || num_q_heads <= 0 ||
+      max_context_len <= 0)
+    return 0;
+  const DecodePlan p = plan_decode(num_seqs, num_q_heads, layout->num_kv_heads, layout->head_dim,
+                                   max_context_len, window_left);
+  return p.ws_bytes;
+}
+
+int sp_paged_decode(void* out, const void* q, const void* k_pool, const void* v_pool,
+                    const sp_cache_layout* layout, const int32_t* block_tables,
+                    int32_t max_blocks_per_seq, const int32_t* context_lens,
+                    int32_t max_context_len, int32_t num_seqs, int32_t num_q_heads, float scale,
+                    int32_t window_left, sp_dtype dtype, void* workspace, size_t workspace_bytes,
+                    void* stream) {
+  const char* fn = "sp_paged_decode";
+  if (int rc = check_layout(layout, fn)) return rc;
+  if (int rc = check_dtype(dtype, fn)) return rc;
+  if (num_seqs < 0 || num_q_heads <= 0 || max_context_len < 0 || max_blocks_per_seq < 0)
+    return fail(SP_EINVAL,
+                "%s: invalid sizes (num_seqs=%d num_q_heads=%d max_context_len=%d "
+                "max_blocks_per_seq=%d)",
+                fn, num_seqs, num_q_heads, max_context_len, max_blocks_per_seq);
+  if (num_seqs == 0) return SP_OK;
+  if (!out || !q || !k_pool || !v_pool || !block_tables || !context_lens)
+    return fail(SP_EINVAL, "%s: NULL pointer argument", fn);
+  const int hkv = layout->num_kv_heads;
+  if (num_q_heads % hkv != 0)
+    return fail(SP_EINVAL, "%s: num_q_heads %d is not a multiple of num_kv_heads %d", fn,
+                num_q_heads, hkv);
+  const int group = num_q_heads / hkv;
+  if (group > kDecodeMaxGroup)
+    return fail(SP_EUNSUPPORTED, "%s: GQA group %d > %d has no kernel", fn, group,
+                kDecodeMaxGroup);
+  const int D = layout->head_dim;
+  if (D != 64 && D != 128)
+    return fail(SP_EUNSUPPORTED, "%s: head_dim %d has no kernel (64, 128)", fn, D);
+  if (window_left < -1) return fail(SP_EINVAL, "%s: window_left %d < -1", fn, window_left);
+  if ((int64_t)max_context_len > (int64_t)max_blocks_per_seq * layout->block_size)
+    return fail(SP_EOOB, "%s: max_context_len %d exceeds the block tables (%d blocks of %d)", fn,
+                max_context_len, max_blocks_per_seq, layout->block_size);
+  if (!isfinite(scale)) return fail(SP_EINVAL, "%s: scale is not finite", fn);
+  const DecodePlan p =
+      plan_decode(num_seqs, num_q_heads, hkv, D, max_context_len < 1 ? 1 : max_context_len,
+                  window_left);
+  if (layout->block_size % p.tt != 0)
+    return fail(SP_EUNSUPPORTED, "%s: block_size %d is not a multiple of the %d-token tile", fn,
+                layout->block_size, p.tt);
+  if (p.ws_bytes > 0 && (!workspace || workspace_bytes < p.ws_bytes))
+    return fail(SP_ENOSPACE, "%s: workspace of %zu bytes, %zu required", fn, workspace_bytes,
+                p.ws_bytes);
+  if (((uintptr_t)q | (uintptr_t)k_pool | (uintptr_t)v_pool | (uintptr_t)workspace) & 15)
+    return fail(SP_EINVAL, "%s: q, pools and workspace must be 16-byte aligned", fn);
+  const int es = dtype_size(dtype);
+  DecodeArgs a{};
+  a.out = out;
+  a.q = q;
+  a.kpool = (const char*)k_pool;
+  a.vpool = (const char*)v_pool;
+  a.block_tables = block_tables;
+  a.context_lens = context_lens;
+  a.partials = (float*)workspace;
+  pool_strides(layout, es, &a.block_stride_b, &a.layer_off_b);
+  a.max_blocks_per_seq = max_blocks_per_seq;
+  a.max_context_len = max_context_len;
+  a.num_blocks = layout->num_blocks;
+  a.block_size = layout->block_size;
+  a.num_seqs = num_seqs;
+  a.hq = num_q_heads;
+  a.hkv = hkv;
+  a.group = group;
+  a.window_left = window_left;
+  a.tps = p.tps;
+  a.max_splits = p.max_splits;
+  a.scale_log2 = scale * 1.4426950408889634f;
+  return launch_paged_decode(a, dtype, D, p.gp, (hipStream_t)stream);
+}
+
+}  // extern "C"

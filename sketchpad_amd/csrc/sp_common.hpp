@@ -1,0 +1,131 @@
+// Shared helpers for the gfx950 kernels and the C-ABI layer: element conversions, wavefront
+// reductions, error reporting.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <string>
+
+#include "sketchpad_attn.h"
+
+namespace sp {
+
+// ---------------------------------------------------------------------------------------------
+// Error reporting (thread-local message behind sp_last_error()).
+// ---------------------------------------------------------------------------------------------
+void set_error(const std::string& msg);
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int check_launch(const char* what);
+
+inline int dtype_size(sp_dtype dt) {
+  switch (dt) {
+    case SP_F32: return 4;
+    case SP_BF16: return 2;
+    case SP_F16: return 2;
+  }
+  return 0;
+}
+
+inline const char* dtype_name(int dt) {
+  switch (dt) {
+    case SP_F32: return "f32";
+    case SP_BF16: return "bf16";
+    case SP_F16: return "f16";
+  }
+  return "?";
+}
+
+// ---------------------------------------------------------------------------------------------
+// Element types. Storage is raw bits; arithmetic is fp32.
+// ---------------------------------------------------------------------------------------------
+struct bf16_t { uint16_t bits; };
+struct f16_t { uint16_t bits; };
+
+typedef __bf16 bf16x2_v __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2_v __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+// fp32 -> bf16 bits, round to nearest even; NaN stays a quiet NaN.
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+__device__ __forceinline__ float f16_bits_to_f32(uint16_t h) {
+  return (float)__builtin_bit_cast(_Float16, h);
+}
+__device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
+  return __builtin_bit_cast(uint16_t, (_Float16)f);
+}
+
+template <typename T> struct Elem;
+template <> struct Elem<float> {
+  static constexpr int bytes = 4;
+  __device__ static float load(const void* p, int64_t i) { return ((const float*)p)[i]; }
+  __device__ static void store(void* p, int64_t i, float v) { ((float*)p)[i] = v; }
+};
+template <> struct Elem<bf16_t> {
+  static constexpr int bytes = 2;
+  __device__ static float load(const void* p, int64_t i) {
+    return __uint_as_float(((uint32_t)((const uint16_t*)p)[i]) << 16);
+  }
+  __device__ static void store(void* p, int64_t i, float v) { ((uint16_t*)p)[i] = f32_to_bf16_bits(v); }
+};
+template <> struct Elem<f16_t> {
+  static constexpr int bytes = 2;
+  __device__ static float load(const void* p, int64_t i) { return f16_bits_to_f32(((const uint16_t*)p)[i]); }
+  __device__ static void store(void* p, int64_t i, float v) { ((uint16_t*)p)[i] = f32_to_f16_bits(v); }
+};
+
+// Dot product of one packed 32-bit word of two 16-bit elements with the matching word of
+// another, accumulated in fp32 (v_dot2_f32_bf16 / v_dot2_f32_f16).
+template <typename T> struct Dot2;
+template <> struct Dot2<bf16_t> {
+  __device__ __forceinline__ static float fma(uint32_t a, uint32_t b, float c) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_v, a),
+                                           __builtin_bit_cast(bf16x2_v, b), c, false);
+  }
+  __device__ __forceinline__ static float lo(uint32_t w) { return bf16_lo(w); }
+  __device__ __forceinline__ static float hi(uint32_t w) { return bf16_hi(w); }
+};
+template <> struct Dot2<f16_t> {
+  __device__ __forceinline__ static float fma(uint32_t a, uint32_t b, float c) {
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_v, a), __builtin_bit_cast(f16x2_v, b), c,
+                                  false);
+  }
+  __device__ __forceinline__ static float lo(uint32_t w) { return f16_bits_to_f32((uint16_t)(w & 0xffffu)); }
+  __device__ __forceinline__ static float hi(uint32_t w) { return f16_bits_to_f32((uint16_t)(w >> 16)); }
+};
+
+// ---------------------------------------------------------------------------------------------
+// Wavefront helpers (wave64).
+// ---------------------------------------------------------------------------------------------
+// Make LDS writes by any lane of this wave visible to later LDS reads by the same wave.
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Butterfly max / sum over aligned groups of WIDTH lanes (WIDTH a power of two <= 64).
+template <int WIDTH>
+__device__ __forceinline__ float group_max(float v) {
+#pragma unroll
+  for (int o = 1; o < WIDTH; o <<= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+template <int WIDTH>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+  for (int o = 1; o < WIDTH; o <<= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+__device__ __forceinline__ int wave_uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
+
+}  // namespace sp

@@ -1,0 +1,193 @@
+"""Seeded synthetic workloads for the five BASELINE configurations.
+
+Metadata (context lengths, block tables, sequence offsets) comes from numpy's PCG64 with seed
+0x5EED0000 + config index, so it is identical on every machine. Tensor contents are N(0, 1)
+drawn by torch on the target device from the same seed, and handed to the oracle by copying
+them back to the host.
+
+    C1  f32 paged decode, 4 seqs, L = 17/64/129/250, 8 q / 8 kv heads, D 64, BS 16, 64 blocks
+    C2  Llama-3-8B bf16 paged decode, B 64, L ~ U[512, 4096], 32/8 heads, D 128, BS 16
+    C3  ragged causal prefill bf16, 8 seqs L ~ U[256, 2048], 32/8 heads, D 128
+    C4  Qwen2.5-7B mixed: 4 chunks x 512 on context U[1024, 8192] + 128 decode U[256, 4096], 28/4
+    C5  Mistral-7B windowed decode bf16, B 16, L ~ U[8192, 32768], 32/8 heads, W 4096
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+
+import numpy as np
+
+SEED_BASE = 0x5EED0000
+
+
+def seed_for(config_index: int) -> int:
+    return SEED_BASE + config_index
+
+
+@dataclass
+class DecodeWorkload:
+    """One decode step over a ragged batch: append one token per sequence, then attend."""
+
+    name: str
+    seed: int
+    num_seqs: int
+    hq: int
+    hkv: int
+    head_dim: int
+    block_size: int
+    dtype: str                    # "f32" | "bf16"
+    context_lens: np.ndarray      # int32 [B], includes the token appended this step
+    block_tables: np.ndarray      # int32 [B, max_blocks]
+    num_blocks: int               # pool size
+    window_left: int = -1         # -1: no window; Mistral window W -> W
+    num_layers: int = 1
+    layer: int = 0
+    extra: dict = field(default_factory=dict)
+
+    @property
+    def max_context_len(self) -> int:
+        return int(self.context_lens.max()) if self.num_seqs else 0
+
+    @property
+    def max_blocks(self) -> int:
+        return int(self.block_tables.shape[1])
+
+    @property
+    def elem_bytes(self) -> int:
+        return 4 if self.dtype == "f32" else 2
+
+    def slot_mapping(self) -> np.ndarray:
+        """Slot of the appended token of each sequence (position L-1): block * BS + slot."""
+        pos = self.context_lens.astype(np.int64) - 1
+        blk = self.block_tables[np.arange(self.num_seqs), pos // self.block_size]
+        return (blk.astype(np.int64) * self.block_size + pos % self.block_size).astype(np.int32)
+
+    def attended_keys(self) -> np.ndarray:
+        lens = self.context_lens.astype(np.int64)
+        if self.window_left < 0:
+            return lens
+        return np.minimum(lens, self.window_left + 1)
+
+    def decode_bytes(self) -> int:
+        """Algorithmic HBM bytes of the attention launch: each attended K/V row once, q, out,
+        the block-table entries walked and the context lengths."""
+        e = self.elem_bytes
+        kv = int(self.attended_keys().sum()) * 2 * self.hkv * self.head_dim * e
+        qo = self.num_seqs * self.hq * self.head_dim * 2 * e
+        tables = int(((self.attended_keys() + self.block_size - 1) // self.block_size).sum()) * 4
+        return kv + qo + tables + self.num_seqs * 4
+
+    def append_bytes(self) -> int:
+        """Algorithmic bytes of the append: read + write of one K and one V row per sequence
+        and KV head, plus the slot mapping."""
+        e = self.elem_bytes
+        return self.num_seqs * self.hkv * self.head_dim * e * 2 * 2 + self.num_seqs * 4
+
+    def layout(self):
+        from ._lib import layout
+        return layout(self.num_blocks, self.num_layers, self.layer, self.hkv, self.block_size,
+                      self.head_dim)
+
+
+def _tables_from_pool(rng: np.random.Generator, lens: np.ndarray, block_size: int,
+                      num_blocks: int) -> np.ndarray:
+    """Block tables as consecutive slices of one seeded permutation of the pool's block ids."""
+    need = (lens + block_size - 1) // block_size
+    assert need.sum() <= num_blocks
+    perm = rng.permutation(num_blocks).astype(np.int32)
+    tables = np.full((len(lens), max(int(need.max()), 1)), -1, dtype=np.int32)
+    off = 0
+    for s, n in enumerate(need):
+        tables[s, :n] = perm[off:off + n]
+        off += n
+    return tables
+
+
+def decode_c1() -> DecodeWorkload:
+    seed = seed_for(1)
+    rng = np.random.default_rng(seed)
+    lens = np.array([17, 64, 129, 250], dtype=np.int32)
+    tables = _tables_from_pool(rng, lens, 16, 64)
+    return DecodeWorkload("C1-f32-decode", seed, 4, 8, 8, 64, 16, "f32", lens, tables, 64)
+
+
+def decode_c2() -> DecodeWorkload:
+    seed = seed_for(2)
+    rng = np.random.default_rng(seed)
+    lens = rng.integers(512, 4096, size=64, endpoint=True).astype(np.int32)
+    nblk = int(((lens + 15) // 16).sum())
+    tables = _tables_from_pool(rng, lens, 16, nblk)
+    return DecodeWorkload("C2-llama3-8b-decode", seed, 64, 32, 8, 128, 16, "bf16", lens, tables,
+                          nblk)
+
+
+def decode_c4() -> DecodeWorkload:
+    """The decode half of the C4 mixed batch (Qwen2.5-7B heads: 28 q / 4 kv, GQA 7)."""
+    seed = seed_for(4)
+    rng = np.random.default_rng(seed)
+    lens = rng.integers(256, 4096, size=128, endpoint=True).astype(np.int32)
+    nblk = int(((lens + 15) // 16).sum())
+    tables = _tables_from_pool(rng, lens, 16, nblk)
+    return DecodeWorkload("C4-qwen25-7b-decode", seed, 128, 28, 4, 128, 16, "bf16", lens, tables,
+                          nblk)
+
+
+def decode_c5() -> DecodeWorkload:
+    seed = seed_for(5)
+    rng = np.random.default_rng(seed)
+    lens = rng.integers(8192, 32768, size=16, endpoint=True).astype(np.int32)
+    nblk = int(((lens + 15) // 16).sum())
+    tables = _tables_from_pool(rng, lens, 16, nblk)
+    return DecodeWorkload("C5-mistral-7b-window-decode", seed, 16, 32, 8, 128, 16, "bf16", lens,
+                          tables, nblk, window_left=4096)
+
+
+DECODE_CONFIGS = {"C1": decode_c1, "C2": decode_c2, "C4": decode_c4, "C5": decode_c5}
+
+
+def random_decode(seed: int, num_seqs: int, hq: int, hkv: int, head_dim: int, block_size: int,
+                  dtype: str, min_len: int, max_len: int, window_left: int = -1,
+                  spare_blocks: int = 3, num_layers: int = 1, layer: int = 0) -> DecodeWorkload:
+    """A small seeded decode batch for parity tests (lengths may be 0 when min_len is 0)."""
+    rng = np.random.default_rng(seed)
+    lens = rng.integers(min_len, max_len, size=num_seqs, endpoint=True).astype(np.int32)
+    nblk = int(((lens + block_size - 1) // block_size).sum()) + spare_blocks
+    tables = _tables_from_pool(rng, lens, block_size, nblk)
+    return DecodeWorkload(f"random-decode-{seed}", seed, num_seqs, hq, hkv, head_dim, block_size,
+                          dtype, lens, tables, nblk, window_left=window_left,
+                          num_layers=num_layers, layer=layer)
+
+
+# ---------------------------------------------------------------------------------------------
+# device tensors for a decode workload
+# ---------------------------------------------------------------------------------------------
+
+def torch_dtype(name: str):
+    import torch
+    return {"f32": torch.float32, "bf16": torch.bfloat16, "f16": torch.float16}[name]
+
+
+def make_decode_tensors(w: DecodeWorkload, device="cuda") -> dict:
+    """Pools filled with N(0,1) (every slot, so stale data sits past each context end), the
+    step's q / k_new / v_new, and the int32 metadata, all on `device`."""
+    import torch
+    g = torch.Generator(device=device)
+    g.manual_seed(w.seed)
+    dt = torch_dtype(w.dtype)
+    pool_shape = (w.num_blocks, w.num_layers, w.hkv, w.block_size, w.head_dim)
+
+    def randn(*shape):
+        return torch.randn(*shape, generator=g, device=device, dtype=torch.float32).to(dt)
+
+    t = {
+        "k_pool": randn(*pool_shape),
+        "v_pool": randn(*pool_shape),
+        "q": randn(w.num_seqs, w.hq, w.head_dim),
+        "k_new": randn(w.num_seqs, w.hkv, w.head_dim),
+        "v_new": randn(w.num_seqs, w.hkv, w.head_dim),
+        "block_tables": torch.from_numpy(w.block_tables).to(device),
+        "context_lens": torch.from_numpy(w.context_lens).to(device),
+        "slot_mapping": torch.from_numpy(w.slot_mapping()).to(device),
+    }
+    t["out"] = torch.empty_like(t["q"])
+    return t

@@ -1,0 +1,119 @@
+"""The C-ABI library: it loads, exports every entry point include/*.h declares, and rejects
+invalid arguments on the host with a status code and message (no GPU needed: validation runs
+before anything is enqueued)."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from sketchpad_amd import _lib
+
+ROOT = Path(__file__).resolve().parent.parent
+
+
+def _declared_functions():
+    names = []
+    for h in sorted((ROOT / "include").glob("*.h")):
+        text = h.read_text()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        names += re.findall(r"\b(sp_[a-z0-9_]+)\s*\(", text)
+    return sorted(set(names))
+
+
+def test_header_declares_entry_points():
+    names = _declared_functions()
+    for n in ("sp_version", "sp_last_error", "sp_kv_append", "sp_kv_gather",
+              "sp_paged_decode", "sp_paged_decode_workspace_size"):
+        assert n in names
+
+
+def test_library_exports_every_declared_symbol(sp_lib):
+    missing = [n for n in _declared_functions() if not hasattr(sp_lib, n)]
+    assert not missing, missing
+
+
+def test_python_binding_covers_header():
+    assert set(_declared_functions()) <= set(_lib._SIGNATURES), \
+        set(_declared_functions()) - set(_lib._SIGNATURES)
+
+
+def test_version(sp_lib):
+    assert sp_lib.sp_version() == 1
+
+
+def _lay(**kw):
+    d = dict(num_blocks=8, num_layers=1, layer=0, num_kv_heads=2, block_size=16, head_dim=64)
+    d.update(kw)
+    return _lib.CacheLayout(**d)
+
+
+def _expect(code, rc, needle):
+    lib = _lib.load()
+    assert rc == code, (rc, lib.sp_last_error())
+    assert needle in lib.sp_last_error().decode()
+
+
+def test_append_validation(sp_lib):
+    f = sp_lib.sp_kv_append
+    fake = ctypes.c_void_p(0x1000)
+    _expect(_lib.SP_EINVAL, f(fake, fake, None, fake, fake, 128, 64, fake, 1, 0, None), "layout")
+    _expect(_lib.SP_EOOB, f(fake, fake, ctypes.byref(_lay(layer=1)), fake, fake, 128, 64, fake, 1,
+                            0, None), "layer 1")
+    _expect(_lib.SP_EINVAL, f(fake, fake, ctypes.byref(_lay(block_size=0)), fake, fake, 128, 64,
+                              fake, 1, 0, None), "positive")
+    _expect(_lib.SP_EINVAL, f(fake, fake, ctypes.byref(_lay()), fake, fake, 128, 64, fake, 1, 9,
+                              None), "dtype")
+    _expect(_lib.SP_EINVAL, f(None, fake, ctypes.byref(_lay()), fake, fake, 128, 64, fake, 1, 0,
+                              None), "NULL")
+    assert f(None, None, ctypes.byref(_lay()), None, None, 0, 0, None, 0, 0, None) == 0
+
+
+def test_gather_validation(sp_lib):
+    f = sp_lib.sp_kv_gather
+    fake = ctypes.c_void_p(0x1000)
+    _expect(_lib.SP_EOOB, f(fake, fake, fake, fake, ctypes.byref(_lay()), fake, 1, 17, 0, None),
+            "needs 2 blocks")
+    assert f(None, None, None, None, ctypes.byref(_lay()), None, 0, 0, 0, None) == 0
+
+
+def test_decode_validation(sp_lib):
+    f = sp_lib.sp_paged_decode
+    fake = ctypes.c_void_p(0x1000)
+
+    def call(lay, hq=4, max_ctx=32, mbs=2, window=-1, ws=None, ws_bytes=0, dtype=1, scale=0.125):
+        return f(fake, fake, fake, fake, ctypes.byref(lay), fake, mbs, fake, max_ctx, 3, hq, scale,
+                 window, dtype, ws, ws_bytes, None)
+
+    _expect(_lib.SP_EINVAL, call(_lay(), hq=3), "multiple")
+    _expect(_lib.SP_EUNSUPPORTED, call(_lay(), hq=32), "GQA group 16")
+    _expect(_lib.SP_EUNSUPPORTED, call(_lay(head_dim=96)), "head_dim 96")
+    _expect(_lib.SP_EOOB, call(_lay(), max_ctx=33), "exceeds the block tables")
+    _expect(_lib.SP_EINVAL, call(_lay(), window=-2), "window_left")
+    _expect(_lib.SP_EINVAL, call(_lay(), scale=float("inf")), "scale")
+    _expect(_lib.SP_EUNSUPPORTED, call(_lay(block_size=8), mbs=4), "block_size 8")
+    # a batch needing split-K partials refuses a missing workspace
+    lay = _lay(num_blocks=4096)
+    need = sp_lib.sp_paged_decode_workspace_size(3, 4, 4096, -1, ctypes.byref(lay))
+    assert need > 0
+    _expect(_lib.SP_ENOSPACE, call(lay, max_ctx=4096, mbs=256), "workspace")
+    _expect(_lib.SP_ENOSPACE, call(lay, max_ctx=4096, mbs=256, ws=fake, ws_bytes=need - 1),
+            "workspace")
+
+
+def test_workspace_size_monotone(sp_lib):
+    lay = _lay(num_blocks=100000, num_kv_heads=8, head_dim=128)
+    sizes = [sp_lib.sp_paged_decode_workspace_size(64, 32, L, -1, ctypes.byref(lay))
+             for L in (16, 512, 4096, 32768)]
+    assert sizes == sorted(sizes)
+    # a window bounds the split count whatever the context length
+    w1 = sp_lib.sp_paged_decode_workspace_size(16, 32, 32768, 4096, ctypes.byref(lay))
+    w2 = sp_lib.sp_paged_decode_workspace_size(16, 32, 8192, 4096, ctypes.byref(lay))
+    assert w1 == w2 > 0
+
+
+def test_missing_library_fails_loudly(monkeypatch, tmp_path):
+    monkeypatch.setattr(_lib, "_lib", None)
+    monkeypatch.setattr(_lib, "LIB_PATH", tmp_path / "nope.so")
+    with pytest.raises(RuntimeError, match="no fallback"):
+        _lib.load()
