@@ -132,8 +132,10 @@ size_t sp_paged_decode_workspace_size(int32_t num_seqs, int32_t num_q_heads,
  *   block_tables   : [num_seqs, max_blocks_per_seq] int32 (device)
  *   context_lens   : [num_seqs] int32 (device), each in [0, max_context_len]; the count
  *                    includes the token just appended. A zero-length context yields zeros.
- *   workspace      : device scratch of at least sp_paged_decode_workspace_size() bytes.
- * Softmax and accumulation are fp32 for every dtype.
+ *   workspace      : device scratch of at least sp_paged_decode_workspace_size() bytes (no
+ *                    initialisation needed). Calls that share a workspace must not overlap.
+ * Softmax and accumulation are fp32 for every dtype. GQA groups (Hq / Hkv) up to 16, head_dim
+ * 64 or 128, block_size a multiple of 16.
  */
 int sp_paged_decode(void* out, const void* q,
                     const void* k_pool, const void* v_pool, const sp_cache_layout* layout,

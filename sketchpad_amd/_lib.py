@@ -171,6 +171,7 @@ def paged_decode(out, q, k_pool, v_pool, lay: CacheLayout, block_tables, context
 
 def alloc_decode_workspace(num_seqs: int, num_q_heads: int, max_context_len: int,
                            window_left: int, lay: CacheLayout, device="cuda"):
+    """Allocate a decode workspace of sp_paged_decode_workspace_size() bytes."""
     torch = _torch()
     n = paged_decode_workspace_size(num_seqs, num_q_heads, max_context_len, window_left, lay)
-    return torch.empty(max(n, 16), dtype=torch.uint8, device=device)
+    return torch.empty(max(n, 256), dtype=torch.uint8, device=device)

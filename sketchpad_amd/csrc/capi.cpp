@@ -208,7 +208,7 @@ int sp_paged_decode(void* out, const void* q, const void* k_pool, const void* v_
   a.tps = p.tps;
   a.max_splits = p.max_splits;
   a.scale_log2 = scale * 1.4426950408889634f;
-  return launch_paged_decode(a, dtype, D, p.gp, (hipStream_t)stream);
+  return launch_paged_decode(a, dtype, D, (hipStream_t)stream);
 }
 
 }  // extern "C"

@@ -1,4 +1,4 @@
-// Split-K paged decode attention for gfx950.
+// Split-K paged decode attention for gfx950, on MFMA.
 //
 // Semantics (reference: MultiHeadAttention::forward_cached with one new token,
 // crates/sketchpad-core/src/transformer.rs:227-243, fed by PagedAttentionCache::update_layer,
@@ -6,70 +6,105 @@
 //   out[s,h,:] = softmax_j( (q[s,h,:] . K[s, h/G, j, :]) * scale ) @ V[s, h/G, j, :]
 // over keys j in [start, L_s), start = 0 or L_s-1-window_left; fp32 softmax and accumulation.
 //
-// Work decomposition: one workgroup of four waves per (split, KV head, sequence). A split is
-// `tps` consecutive tiles of TT tokens (TT = 16 for GQA groups up to 4). The GQA group's query
-// heads are all served by the same workgroup, so every K/V byte is read from HBM exactly once.
-// Each wave takes every fourth tile of the split and runs its own online softmax:
-//   1. the tile's K and V rows (TT x D each, contiguous inside one pool block) are loaded with
-//      16-byte per-lane loads (a wave instruction covers 1 KiB contiguous) into registers, one
-//      tile ahead of the compute, then staged in LDS with a 16-byte row pad (bank-conflict free);
-//   2. lane (head g, token t[, part]) computes the full q_g . k_t from LDS (v_dot2_f32_bf16 for
-//      16-bit types), so no cross-lane reduction is needed for the scores;
-//   3. per-head tile max/exp2 with shuffles inside the head's lane group, p written to LDS;
-//   4. lane (head g, dim chunk) accumulates p_t * V[t, chunk] over the tile's tokens.
-// The four waves are merged in LDS at the end. A sequence that fits in one split writes its
-// output directly; otherwise each split writes (m, l, acc[D]) and decode_combine_kernel merges.
+// Work decomposition: one workgroup of four waves per (split, KV head, sequence); a split is
+// `tps` consecutive 16-token tiles and the waves take every fourth tile. All query heads of the
+// GQA group (up to 16) ride in the N = 16 columns of the MFMA tiles, so each K/V byte is read
+// from HBM once. Per tile, per wave:
+//   S^T[16 tok, 16 heads]  = K[16 tok, D] . Q^T[D, 16 heads]     MFMA 16x16x32 (16-bit) / 16x16x4 (f32)
+//     K is the A operand loaded straight from the pool: lane (g, n) loads 16 bytes of token n,
+//     so no LDS trip for K. Lane (g, n) then holds scores of tokens 4g..4g+3 for head n.
+//   online softmax per head column (two cross-row shuffles per tile), fp32.
+//   O^T[D, 16 heads]     += V^T[D, 16 tok] . P^T[16 tok, 16 heads] MFMA 16x16x16 / 16x16x4
+//     The score registers are already the B-operand layout of P^T; V is staged in LDS with
+//     coalesced 16-byte stores and read back column-wise (padded pitch, conflict-free).
+// The next tile's loads are issued as soon as the current K has entered the MFMAs and V is in
+// LDS, so they stay in flight through the softmax and PV of the current tile.
+// The four waves merge in LDS. A sequence that needs one split writes its output directly;
+// otherwise each split stores (m, l, acc[D]) and decode_combine_kernel merges them. (Merging in
+// the last-arriving split instead needs an agent-scope release/acquire per split, which on
+// gfx950 is an L2 writeback + invalidate per workgroup: measured 10x slower.)
 #include "paged_decode.hpp"
 
 #include <math.h>
 
 namespace sp {
 
-template <int GP> struct DecodeShape {
-  static constexpr int TT = GP <= 4 ? 16 : 64 / GP;  // tokens per tile
-  static constexpr int LPH = 64 / GP;                // lanes per head
-  static constexpr int LPS = LPH / TT;               // lanes per score
+typedef __bf16 bf16x8_v __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_v __attribute__((ext_vector_type(8)));
+typedef short s16x4_v __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x4_v __attribute__((ext_vector_type(4)));
+typedef float f32x4_v __attribute__((ext_vector_type(4)));
+
+constexpr int kTile = 16;  // tokens per tile
+
+template <typename T> struct DecodeMfma;
+template <> struct DecodeMfma<bf16_t> {
+  __device__ __forceinline__ static f32x4_v qk(uint4 k, uint4 q, f32x4_v c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_v, k),
+                                                   __builtin_bit_cast(bf16x8_v, q), c, 0, 0, 0);
+  }
+  __device__ __forceinline__ static f32x4_v pv(uint2 v, uint2 p, f32x4_v c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4_v, v),
+                                                     __builtin_bit_cast(s16x4_v, p), c, 0, 0, 0);
+  }
+  __device__ __forceinline__ static uint32_t pack(float lo, float hi) {
+    return (uint32_t)f32_to_bf16_bits(lo) | ((uint32_t)f32_to_bf16_bits(hi) << 16);
+  }
+};
+template <> struct DecodeMfma<f16_t> {
+  __device__ __forceinline__ static f32x4_v qk(uint4 k, uint4 q, f32x4_v c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_v, k),
+                                                  __builtin_bit_cast(f16x8_v, q), c, 0, 0, 0);
+  }
+  __device__ __forceinline__ static f32x4_v pv(uint2 v, uint2 p, f32x4_v c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4_v, v),
+                                                 __builtin_bit_cast(f16x4_v, p), c, 0, 0, 0);
+  }
+  __device__ __forceinline__ static uint32_t pack(float lo, float hi) {
+    return (uint32_t)f32_to_f16_bits(lo) | ((uint32_t)f32_to_f16_bits(hi) << 16);
+  }
 };
 
-// Copy BYTES (4, 8 or 16) from LDS into 32-bit words.
-template <int BYTES>
-__device__ __forceinline__ void lds_words(const char* p, uint32_t* w) {
-  if constexpr (BYTES == 16) {
-    const uint4 v = *(const uint4*)p;
-    w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
-  } else if constexpr (BYTES == 8) {
-    const uint2 v = *(const uint2*)p;
-    w[0] = v.x; w[1] = v.y;
-  } else {
-    static_assert(BYTES == 4, "LDS chunk must be 4, 8 or 16 bytes");
-    w[0] = *(const uint32_t*)p;
-  }
+__device__ __forceinline__ f32x4_v mfma_f32(float a, float b, f32x4_v c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
-template <typename T, int D, int GP>
-__global__ void __launch_bounds__(64 * kDecodeWaves) paged_decode_kernel(DecodeArgs a) {
-  using S = DecodeShape<GP>;
-  constexpr int TT = S::TT, LPH = S::LPH, LPS = S::LPS;
-  constexpr int ES = Elem<T>::bytes;
-  constexpr bool kF32 = (ES == 4);
-  constexpr int RB = D * ES;              // bytes per K/V row
-  constexpr int RBP = RB + 16;            // LDS row pitch (pad breaks the 256-byte bank stride)
-  constexpr int NL = TT * RB / 1024;      // 16-byte loads per lane per tile (K or V)
-  constexpr int SEG = D / LPS;            // dims per score lane
-  constexpr int QW = SEG * ES / 4;        // 32-bit words of q held per lane
-  constexpr int DPL = D / LPH;            // dims per accumulation lane
-  constexpr int PVB = DPL * ES;           // bytes of one V row read by one lane
-  constexpr int WAVE_LDS = 2 * TT * RBP + GP * TT * 4;
-  static_assert(TT * RB % 1024 == 0 && NL >= 1, "tile must be a whole number of wave loads");
-  static_assert(SEG * ES % 16 == 0, "score segment must be 16-byte aligned");
-  static_assert(DPL >= 1, "head_dim too small for this group");
-  static_assert(kDecodeWaves * GP * (D + 2) * 4 <= kDecodeWaves * WAVE_LDS, "merge area");
+template <typename T, int D>
+struct DecodeCfg {
+  static constexpr int ES = Elem<T>::bytes;
+  static constexpr bool kF32 = (ES == 4);
+  static constexpr int RB = D * ES;                    // bytes per K/V row
+  static constexpr int NL = RB / 64;                   // 16-byte loads per lane per tile (K or V)
+  static constexpr int VP = RB + (kF32 ? 16 : 8);      // V staging pitch (4-row stride hits new banks)
+  static constexpr int WAVE_LDS = kTile * VP;
+  static constexpr int ND = D / 16;                    // 16-dim output blocks
+  static constexpr int MERGE_LDS = kDecodeWaves * (2 * 16 + 16 * D) * 4;
+  static constexpr int LDS = (kDecodeWaves * WAVE_LDS > MERGE_LDS) ? kDecodeWaves * WAVE_LDS : MERGE_LDS;
+};
 
-  __shared__ __attribute__((aligned(16))) char smem[kDecodeWaves * WAVE_LDS];
+// 16-bit kernels fit four waves per SIMD (<= 128 VGPRs, no spills); f32 D=128 would spill.
+template <typename T>
+constexpr int decode_min_waves() { return Elem<T>::bytes == 4 ? 1 : 4; }
+
+template <typename T, int D>
+__global__ void __launch_bounds__(64 * kDecodeWaves, decode_min_waves<T>())
+    paged_decode_kernel(DecodeArgs a) {
+  using C = DecodeCfg<T, D>;
+  constexpr int ES = C::ES, RB = C::RB, NL = C::NL, VP = C::VP, ND = C::ND;
+  constexpr bool kF32 = C::kF32;
+  static_assert(RB % 64 == 0, "row must split into 64-byte MFMA K chunks");
+
+  __shared__ __attribute__((aligned(16))) char smem[C::LDS];
 
   const int lane = threadIdx.x & 63;
   const int wave = wave_uniform(threadIdx.x >> 6);
-  const int split = blockIdx.x, kvh = blockIdx.y, seq = blockIdx.z;
+  const int g = lane >> 4, n = lane & 15;
+  // blockIdx.x enumerates (sequence, KV head) units, blockIdx.y the split. Workgroups are handed
+  // to the eight XCDs round-robin in id order, so the unit must vary fastest: with the split
+  // fastest, split s always lands on XCD s % 8 and the early splits (present in every sequence)
+  // pile up on a few XCDs.
+  const int unit = blockIdx.x, split = blockIdx.y;
+  const int seq = unit / a.hkv, kvh = unit - seq * a.hkv;
   const int G = a.group;
 
   int L = a.context_lens[seq];
@@ -82,288 +117,294 @@ __global__ void __launch_bounds__(64 * kDecodeWaves) paged_decode_kernel(DecodeA
     return;
   }
   const int start_tok = a.window_left >= 0 ? max(0, L - 1 - a.window_left) : 0;
-  const int first_tile = start_tok / TT, last_tile = (L - 1) / TT;
+  const int first_tile = start_tok / kTile, last_tile = (L - 1) / kTile;
   const int nsplit = (last_tile - first_tile + a.tps) / a.tps;
   if (split >= nsplit) return;
   const int t_begin = first_tile + split * a.tps;
   const int t_end = min(t_begin + a.tps, last_tile + 1);
 
-  // Lane roles: score lane (head hs, token tok_s, part) and accumulation lane (head hs, chunk dc).
-  const int hs = lane / LPH;
-  const int rem = lane % LPH;
-  const int tok_s = rem / LPS;
-  const int part = rem % LPS;
-  const int dc = rem;
-  const int hq_lane = kvh * G + min(hs, G - 1);
-
-  // q segment of this score lane, as raw 32-bit words.
-  uint32_t qw[QW];
+  // Q^T operand: lane (g, n) holds head n's bytes [c*64 + g*16, +16) for every chunk c.
+  uint4 qv[NL];
   {
-    const char* qp = (const char*)a.q + (((int64_t)seq * a.hq + hq_lane) * D + part * SEG) * ES;
+    const bool real = n < G;
+    const char* qp = (const char*)a.q + ((int64_t)seq * a.hq + kvh * G + (real ? n : 0)) * RB;
 #pragma unroll
-    for (int i = 0; i < QW / 4; ++i) {
-      const uint4 v = ((const uint4*)qp)[i];
-      qw[4 * i + 0] = v.x; qw[4 * i + 1] = v.y; qw[4 * i + 2] = v.z; qw[4 * i + 3] = v.w;
-    }
+    for (int c = 0; c < NL; ++c)
+      qv[c] = real ? *(const uint4*)(qp + c * 64 + g * 16) : make_uint4(0, 0, 0, 0);
   }
-
-  char* lds_k = smem + wave * WAVE_LDS;
-  char* lds_v = lds_k + TT * RBP;
-  float* lds_p = (float*)(lds_v + TT * RBP);
 
   const int32_t* table = a.block_tables + (int64_t)seq * a.max_blocks_per_seq;
   const int64_t head_off = a.layer_off_b + (int64_t)kvh * a.block_size * RB;
+  char* vst = smem + wave * C::WAVE_LDS;
 
-  uint4 kr[NL], vr[NL];
-  bool next_ok = false;
-  auto load_tile = [&](int t) {
-    const int pos0 = t * TT;
+  // Tile loads. K in MFMA A-operand order (token n, 16 bytes at c*64 + g*16); V coalesced
+  // (lane-linear 16-byte chunks of the contiguous 16 x RB tile).
+  // K/V are streamed once: nontemporal loads keep them from displacing reusable L2 lines.
+  typedef unsigned u32x4_v __attribute__((ext_vector_type(4)));
+  auto ldnt = [](const char* p) {
+    return __builtin_bit_cast(uint4, __builtin_nontemporal_load((const u32x4_v*)p));
+  };
+  auto load_tile = [&](int t, uint4* kr, uint4* vr, bool& ok) {
+    const int pos0 = t * kTile;
     const int blk = table[pos0 / a.block_size];
-    next_ok = blk >= 0 && blk < a.num_blocks;
-    const int64_t base = (int64_t)(next_ok ? blk : 0) * a.block_stride_b + head_off +
+    ok = blk >= 0 && blk < a.num_blocks;
+    const int64_t base = (int64_t)(ok ? blk : 0) * a.block_stride_b + head_off +
                          (int64_t)(pos0 % a.block_size) * RB;
+    const int kpos = pos0 + n;
+    const bool kval = ok && kpos >= start_tok && kpos < L;
+#pragma unroll
+    for (int c = 0; c < NL; ++c)
+      kr[c] = kval ? ldnt(a.kpool + base + n * RB + c * 64 + g * 16) : make_uint4(0, 0, 0, 0);
 #pragma unroll
     for (int i = 0; i < NL; ++i) {
       const int off = (i * 64 + lane) * 16;
-      const int pos = pos0 + off / RB;
-      if (next_ok && pos >= start_tok && pos < L) {
-        kr[i] = *(const uint4*)(a.kpool + base + off);
-        vr[i] = *(const uint4*)(a.vpool + base + off);
-      } else {
-        kr[i] = make_uint4(0, 0, 0, 0);
-        vr[i] = make_uint4(0, 0, 0, 0);
-      }
+      const int vpos = pos0 + off / RB;
+      vr[i] = (ok && vpos >= start_tok && vpos < L) ? ldnt(a.vpool + base + off)
+                                                    : make_uint4(0, 0, 0, 0);
     }
   };
 
   float m_run = -INFINITY, l_run = 0.f;
-  float acc[DPL];
+  f32x4_v acc[ND];
 #pragma unroll
-  for (int e = 0; e < DPL; ++e) acc[e] = 0.f;
+  for (int i = 0; i < ND; ++i) acc[i] = f32x4_v{0.f, 0.f, 0.f, 0.f};
 
+  uint4 kc[NL], vc[NL];
+  bool ok_c = false;
   int t = t_begin + wave;
-  if (t < t_end) load_tile(t);
+  if (t < t_end) load_tile(t, kc, vc, ok_c);
   for (; t < t_end; t += kDecodeWaves) {
-    const bool tile_ok = next_ok;
-    // Stage the tile in LDS, then start fetching the next one.
+    const bool tile_ok = ok_c;
+
+    // Stage V rows in LDS (two 8-byte stores per 16-byte chunk: the pitch is 8-byte aligned).
 #pragma unroll
     for (int i = 0; i < NL; ++i) {
       const int off = (i * 64 + lane) * 16;
-      const int lds_off = (off / RB) * RBP + off % RB;
-      *(uint4*)(lds_k + lds_off) = kr[i];
-      *(uint4*)(lds_v + lds_off) = vr[i];
+      char* dst = vst + (off / RB) * VP + off % RB;
+      *(uint2*)dst = make_uint2(vc[i].x, vc[i].y);
+      *(uint2*)(dst + 8) = make_uint2(vc[i].z, vc[i].w);
     }
-    wave_lds_sync();
-    if (t + kDecodeWaves < t_end) load_tile(t + kDecodeWaves);
 
-    // Score of (head hs, token tok_s) over this lane's dims.
-    float s = 0.f;
-    {
-      const char* kp = lds_k + tok_s * RBP + part * SEG * ES;
+    // S^T = K Q^T
+    f32x4_v s = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int i = 0; i < QW / 4; ++i) {
-        uint32_t kw[4];
-        lds_words<16>(kp + 16 * i, kw);
+    for (int c = 0; c < NL; ++c) {
+      if constexpr (kF32) {
+        s = mfma_f32(__uint_as_float(kc[c].x), __uint_as_float(qv[c].x), s);
+        s = mfma_f32(__uint_as_float(kc[c].y), __uint_as_float(qv[c].y), s);
+        s = mfma_f32(__uint_as_float(kc[c].z), __uint_as_float(qv[c].z), s);
+        s = mfma_f32(__uint_as_float(kc[c].w), __uint_as_float(qv[c].w), s);
+      } else {
+        s = DecodeMfma<T>::qk(kc[c], qv[c], s);
+      }
+    }
+    // K went into the MFMAs and V into LDS: the registers take the next tile's loads, which
+    // stay in flight through this tile's softmax and PV.
+    if (t + kDecodeWaves < t_end) load_tile(t + kDecodeWaves, kc, vc, ok_c);
+
+    // Online softmax for head column n over tokens 4g..4g+3 of this tile.
+    const int pos = t * kTile + 4 * g;
+    float sv[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const bool valid = tile_ok && pos + j >= start_tok && pos + j < L;
+      sv[j] = valid ? s[j] * a.scale_log2 : -INFINITY;
+    }
+    float mt = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
+    mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
+    mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+    const float m_new = fmaxf(m_run, mt);
+    const float alpha = (m_run == -INFINITY) ? 0.f : exp2f(m_run - m_new);
+    float p[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) p[j] = (sv[j] == -INFINITY) ? 0.f : exp2f(sv[j] - m_new);
+    l_run = l_run * alpha + ((p[0] + p[1]) + (p[2] + p[3]));
+    m_run = m_new;
+#pragma unroll
+    for (int i = 0; i < ND; ++i) acc[i] *= alpha;
+
+    wave_lds_sync();  // V staging visible to the whole wave
+
+    // O^T += V^T P^T
+    if constexpr (kF32) {
+#pragma unroll
+      for (int db = 0; db < ND; ++db) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          if constexpr (kF32)
-            s = fmaf(__uint_as_float(qw[4 * i + j]), __uint_as_float(kw[j]), s);
-          else
-            s = Dot2<T>::fma(qw[4 * i + j], kw[j], s);
+          const float v = *(const float*)(vst + (4 * g + j) * VP + (db * 16 + n) * 4);
+          acc[db] = mfma_f32(v, p[j], acc[db]);
         }
       }
-    }
-    if constexpr (LPS > 1) s = group_sum<LPS>(s);
-    const int pos = t * TT + tok_s;
-    const bool valid = tile_ok && pos >= start_tok && pos < L;
-    s = valid ? s * a.scale_log2 : -INFINITY;
-
-    const float m_tile = group_max<LPH>(s);
-    const float m_new = fmaxf(m_run, m_tile);
-    const float alpha = (m_run == -INFINITY) ? 0.f : exp2f(m_run - m_new);
-    const float p = valid ? exp2f(s - m_new) : 0.f;
-    l_run = l_run * alpha + (part == 0 ? p : 0.f);
-    m_run = m_new;
-    if (part == 0) lds_p[hs * TT + tok_s] = p;
-    wave_lds_sync();
-
-    // acc[hs, dc*DPL ..] = alpha * acc + sum_t p_t * V[t, dc*DPL ..]
+    } else {
+      const uint2 pp = make_uint2(DecodeMfma<T>::pack(p[0], p[1]), DecodeMfma<T>::pack(p[2], p[3]));
 #pragma unroll
-    for (int e = 0; e < DPL; ++e) acc[e] *= alpha;
-#pragma unroll
-    for (int t4 = 0; t4 < TT; t4 += 4) {
-      const float4 p4 = *(const float4*)(lds_p + hs * TT + t4);
-      const float pv[4] = {p4.x, p4.y, p4.z, p4.w};
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const char* vp = lds_v + (t4 + j) * RBP + dc * PVB;
-        if constexpr (kF32) {
-          constexpr int NW = DPL;  // one word per element
-          uint32_t w[NW];
-          if constexpr (PVB >= 16) {
-#pragma unroll
-            for (int c = 0; c < PVB / 16; ++c) lds_words<16>(vp + 16 * c, w + 4 * c);
-          } else {
-            lds_words<PVB>(vp, w);
-          }
-#pragma unroll
-          for (int e = 0; e < DPL; ++e) acc[e] = fmaf(pv[j], __uint_as_float(w[e]), acc[e]);
-        } else if constexpr (PVB >= 4) {
-          constexpr int NW = PVB / 4;
-          uint32_t w[NW];
-          if constexpr (PVB >= 16) {
-#pragma unroll
-            for (int c = 0; c < PVB / 16; ++c) lds_words<16>(vp + 16 * c, w + 4 * c);
-          } else {
-            lds_words<PVB>(vp, w);
-          }
-#pragma unroll
-          for (int e = 0; e < NW; ++e) {
-            acc[2 * e] = fmaf(pv[j], Dot2<T>::lo(w[e]), acc[2 * e]);
-            acc[2 * e + 1] = fmaf(pv[j], Dot2<T>::hi(w[e]), acc[2 * e + 1]);
-          }
-        } else {
-          acc[0] = fmaf(pv[j], Elem<T>::load(vp, 0), acc[0]);
-        }
+      for (int db = 0; db < ND; ++db) {
+        const char* col = vst + (4 * g) * VP + (db * 16 + n) * ES;
+        const uint32_t v0 = *(const uint16_t*)(col);
+        const uint32_t v1 = *(const uint16_t*)(col + VP);
+        const uint32_t v2 = *(const uint16_t*)(col + 2 * VP);
+        const uint32_t v3 = *(const uint16_t*)(col + 3 * VP);
+        acc[db] = DecodeMfma<T>::pv(make_uint2(v0 | (v1 << 16), v2 | (v3 << 16)), pp, acc[db]);
       }
     }
-    wave_lds_sync();
+    wave_lds_sync();  // reads done before the next tile overwrites the staging area
   }
 
-  // Merge the four waves' (m, l, acc) in LDS.
-  l_run = group_sum<LPH>(l_run);
+  // Per-head sums over the four token groups of the wave, then merge the four waves in LDS.
+  l_run += __shfl_xor(l_run, 16, 64);
+  l_run += __shfl_xor(l_run, 32, 64);
   __syncthreads();
-  float* cm = (float*)smem;                  // [waves][GP]
-  float* cl = cm + kDecodeWaves * GP;        // [waves][GP]
-  float* ca = cl + kDecodeWaves * GP;        // [waves][GP][D]
-  if (rem == 0) {
-    cm[wave * GP + hs] = m_run;
-    cl[wave * GP + hs] = l_run;
+  float* cm = (float*)smem;             // [waves][16]
+  float* cl = cm + kDecodeWaves * 16;   // [waves][16]
+  float* ca = cl + kDecodeWaves * 16;   // [waves][16][D]
+  if (g == 0) {
+    cm[wave * 16 + n] = m_run;
+    cl[wave * 16 + n] = l_run;
   }
 #pragma unroll
-  for (int e = 0; e < DPL; ++e) ca[(wave * GP + hs) * D + dc * DPL + e] = acc[e];
+  for (int db = 0; db < ND; ++db)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) ca[(wave * 16 + n) * D + db * 16 + 4 * g + r] = acc[db][r];
   __syncthreads();
 
   for (int i = threadIdx.x; i < G * D; i += blockDim.x) {
     const int h = i / D, d = i % D;
     float M = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < kDecodeWaves; ++w) M = fmaxf(M, cm[w * GP + h]);
-    float lsum = 0.f, accsum = 0.f;
+    for (int w = 0; w < kDecodeWaves; ++w) M = fmaxf(M, cm[w * 16 + h]);
+    float lsum = 0.f, asum = 0.f;
     if (M != -INFINITY) {
 #pragma unroll
       for (int w = 0; w < kDecodeWaves; ++w) {
-        const float mw = cm[w * GP + h];
+        const float mw = cm[w * 16 + h];
         const float f = (mw == -INFINITY) ? 0.f : exp2f(mw - M);
-        lsum = fmaf(cl[w * GP + h], f, lsum);
-        accsum = fmaf(ca[(w * GP + h) * D + d], f, accsum);
+        lsum = fmaf(cl[w * 16 + h], f, lsum);
+        asum = fmaf(ca[(w * 16 + h) * D + d], f, asum);
       }
     }
     const int hq = kvh * G + h;
     if (nsplit == 1) {
-      Elem<T>::store(a.out, ((int64_t)seq * a.hq + hq) * D + d, lsum > 0.f ? accsum / lsum : 0.f);
+      Elem<T>::store(a.out, ((int64_t)seq * a.hq + hq) * D + d, lsum > 0.f ? asum / lsum : 0.f);
     } else {
       float* pp = a.partials + (((int64_t)seq * a.hq + hq) * a.max_splits + split) * (D + 4);
       if (d == 0) {
         pp[0] = M;
         pp[1] = lsum;
       }
-      pp[4 + d] = accsum;
+      pp[4 + d] = asum;
     }
   }
 }
 
-// Merge the per-split partials of sequences that needed more than one split.
-template <typename T, int D, int TT>
-__global__ void __launch_bounds__(D) decode_combine_kernel(DecodeArgs a) {
-  const int hq = blockIdx.x, seq = blockIdx.y, d = threadIdx.x;
+// Merge the per-split partials (m, l, acc[D]) of sequences that needed more than one split.
+// One wave per (query head, sequence): lane s reads split s's (m, l); the weights
+// 2^(m_s - M) are shared through LDS and every lane accumulates D/64 output dims.
+template <typename T, int D>
+__global__ void __launch_bounds__(64) decode_combine_kernel(DecodeArgs a) {
+  constexpr int DPL = D / 64;
+  __shared__ float w_lds[64];
+  const int hq = blockIdx.x, seq = blockIdx.y, lane = threadIdx.x;
   int L = a.context_lens[seq];
   L = min(L, min(a.max_context_len, a.max_blocks_per_seq * a.block_size));
   if (L <= 0) return;
   const int start_tok = a.window_left >= 0 ? max(0, L - 1 - a.window_left) : 0;
-  const int nsplit = ((L - 1) / TT - start_tok / TT + a.tps) / a.tps;
+  const int nsplit = ((L - 1) / kTile - start_tok / kTile + a.tps) / a.tps;
   if (nsplit <= 1) return;
   const float* pp = a.partials + ((int64_t)seq * a.hq + hq) * a.max_splits * (D + 4);
   float M = -INFINITY;
-  for (int s = 0; s < nsplit; ++s) M = fmaxf(M, pp[s * (D + 4)]);
-  float lsum = 0.f, accsum = 0.f;
-  if (M != -INFINITY) {
-    for (int s = 0; s < nsplit; ++s) {
+  for (int s = lane; s < nsplit; s += 64) M = fmaxf(M, pp[s * (D + 4)]);
+  M = group_max<64>(M);
+  float acc[DPL];
+#pragma unroll
+  for (int e = 0; e < DPL; ++e) acc[e] = 0.f;
+  float lsum = 0.f;
+  for (int s0 = 0; s0 < nsplit; s0 += 64) {
+    const int s = s0 + lane;
+    float w = 0.f;
+    if (s < nsplit && M != -INFINITY) {
       const float ms = pp[s * (D + 4)];
-      const float f = (ms == -INFINITY) ? 0.f : exp2f(ms - M);
-      lsum = fmaf(pp[s * (D + 4) + 1], f, lsum);
-      accsum = fmaf(pp[s * (D + 4) + 4 + d], f, accsum);
+      w = (ms == -INFINITY) ? 0.f : exp2f(ms - M);
+      lsum = fmaf(pp[s * (D + 4) + 1], w, lsum);
     }
+    w_lds[lane] = w;
+    __syncthreads();
+    const int cnt = min(64, nsplit - s0);
+    // Batches of 8 partial rows: the loads of a batch are all in flight before the FMAs.
+    for (int j0 = 0; j0 < cnt; j0 += 8) {
+      float v[8][DPL];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const float* src = pp + (s0 + min(j0 + u, cnt - 1)) * (D + 4) + 4 + lane * DPL;
+#pragma unroll
+        for (int e = 0; e < DPL; ++e) v[u][e] = src[e];
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const float wj = (j0 + u < cnt) ? w_lds[j0 + u] : 0.f;
+#pragma unroll
+        for (int e = 0; e < DPL; ++e) acc[e] = fmaf(v[u][e], wj, acc[e]);
+      }
+    }
+    __syncthreads();
   }
-  Elem<T>::store(a.out, ((int64_t)seq * a.hq + hq) * D + d, lsum > 0.f ? accsum / lsum : 0.f);
+  lsum = group_sum<64>(lsum);
+  const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
+#pragma unroll
+  for (int e = 0; e < DPL; ++e)
+    Elem<T>::store(a.out, ((int64_t)seq * a.hq + hq) * D + lane * DPL + e, acc[e] * inv);
 }
 
 DecodePlan plan_decode(int num_seqs, int hq, int hkv, int head_dim, int max_context_len,
                        int window_left) {
   DecodePlan p{};
   p.group = hkv > 0 ? hq / hkv : 0;
-  p.gp = decode_group_pow2(p.group < 1 ? 1 : p.group);
-  p.tt = decode_tile_tokens(p.gp);
-  int max_tiles = (max_context_len + p.tt - 1) / p.tt;
+  p.tt = kTile;
+  int max_tiles = (max_context_len + kTile - 1) / kTile;
   if (window_left >= 0) {
-    const int wt = (window_left + 1 + p.tt - 1) / p.tt + 1;  // a window straddles one extra tile
+    const int wt = (window_left + 1 + kTile - 1) / kTile + 1;  // a window straddles one extra tile
     if (wt < max_tiles) max_tiles = wt;
   }
   p.max_tiles = max_tiles < 1 ? 1 : max_tiles;
-  // Tiles per split: 16 (4 per wave) unless the batch is too small to fill 256 CUs.
-  int tps = 16;
+  int tps = 24;  // 384 tokens per split, 6 tiles per wave
   const char* env = getenv("SP_DECODE_TPS");
   if (env && atoi(env) > 0) {
     tps = atoi(env);
   } else {
     const int64_t units = (int64_t)num_seqs * (hkv > 0 ? hkv : 1);
-    while (tps > kDecodeWaves && units * ((p.max_tiles + tps - 1) / tps) < 2048) tps >>= 1;
+    while (tps > kDecodeWaves && units * ((p.max_tiles + tps - 1) / tps) < 2048)
+      tps = tps / 2 < kDecodeWaves ? kDecodeWaves : tps / 2;
   }
   p.tps = tps;
   p.max_splits = (p.max_tiles + tps - 1) / tps;
-  p.ws_bytes = p.max_splits > 1
-                   ? (size_t)num_seqs * hq * p.max_splits * (head_dim + 4) * sizeof(float)
-                   : 0;
+  if (p.max_splits > 1)
+    p.ws_bytes = (size_t)num_seqs * hq * p.max_splits * (head_dim + 4) * sizeof(float);
   return p;
 }
 
-template <typename T, int D, int GP>
-static void launch_typed(const DecodeArgs& a, int nsplit_grid, hipStream_t stream) {
-  const dim3 grid(nsplit_grid, a.hkv, a.num_seqs);
-  hipLaunchKernelGGL((paged_decode_kernel<T, D, GP>), grid, dim3(64 * kDecodeWaves), 0, stream, a);
-  if (a.max_splits > 1) {
-    hipLaunchKernelGGL((decode_combine_kernel<T, D, DecodeShape<GP>::TT>), dim3(a.hq, a.num_seqs),
-                       dim3(D), 0, stream, a);
-  }
-}
-
 template <typename T, int D>
-static int launch_d(const DecodeArgs& a, int gp, hipStream_t stream) {
-  switch (gp) {
-    case 1: launch_typed<T, D, 1>(a, a.max_splits, stream); break;
-    case 2: launch_typed<T, D, 2>(a, a.max_splits, stream); break;
-    case 4: launch_typed<T, D, 4>(a, a.max_splits, stream); break;
-    case 8: launch_typed<T, D, 8>(a, a.max_splits, stream); break;
-    default: return fail(SP_EUNSUPPORTED, "paged decode: GQA group %d has no kernel", a.group);
-  }
+static int launch_typed(const DecodeArgs& a, hipStream_t stream) {
+  const dim3 grid(a.num_seqs * a.hkv, a.max_splits);
+  hipLaunchKernelGGL((paged_decode_kernel<T, D>), grid, dim3(64 * kDecodeWaves), 0, stream, a);
+  if (a.max_splits > 1)
+    hipLaunchKernelGGL((decode_combine_kernel<T, D>), dim3(a.hq, a.num_seqs), dim3(64), 0, stream,
+                       a);
   return check_launch("paged_decode_kernel");
 }
 
 template <typename T>
-static int launch_t(const DecodeArgs& a, int head_dim, int gp, hipStream_t stream) {
+static int launch_t(const DecodeArgs& a, int head_dim, hipStream_t stream) {
   switch (head_dim) {
-    case 64: return launch_d<T, 64>(a, gp, stream);
-    case 128: return launch_d<T, 128>(a, gp, stream);
+    case 64: return launch_typed<T, 64>(a, stream);
+    case 128: return launch_typed<T, 128>(a, stream);
     default: return fail(SP_EUNSUPPORTED, "paged decode: head_dim %d has no kernel", head_dim);
   }
 }
 
-int launch_paged_decode(const DecodeArgs& a, sp_dtype dtype, int head_dim, int gp,
-                        hipStream_t stream) {
+int launch_paged_decode(const DecodeArgs& a, sp_dtype dtype, int head_dim, hipStream_t stream) {
   switch (dtype) {
-    case SP_F32: return launch_t<float>(a, head_dim, gp, stream);
-    case SP_BF16: return launch_t<bf16_t>(a, head_dim, gp, stream);
-    case SP_F16: return launch_t<f16_t>(a, head_dim, gp, stream);
+    case SP_F32: return launch_t<float>(a, head_dim, stream);
+    case SP_BF16: return launch_t<bf16_t>(a, head_dim, stream);
+    case SP_F16: return launch_t<f16_t>(a, head_dim, stream);
   }
   return fail(SP_EUNSUPPORTED, "paged decode: dtype %d has no kernel", (int)dtype);
 }

@@ -1,30 +1,20 @@
-// Launch interface of the split-K paged decode kernels (paged_decode.hip).
+// Launch interface of the split-K paged decode kernel (paged_decode.hip).
 #pragma once
 
 #include "sp_common.hpp"
 
 namespace sp {
 
-constexpr int kDecodeWaves = 4;        // waves per workgroup
-constexpr int kDecodeMaxGroup = 8;     // largest GQA group (Hq / Hkv) with a kernel
-
-// Tokens per tile for a GQA group padded to GP lanes-groups: a tile is the unit one wave stages
-// through LDS; every lane of the wave then owns one (head, token) score.
-inline int decode_group_pow2(int g) {
-  int gp = 1;
-  while (gp < g) gp <<= 1;
-  return gp;
-}
-inline int decode_tile_tokens(int gp) { return gp <= 4 ? 16 : 64 / gp; }
+constexpr int kDecodeWaves = 4;      // waves per workgroup
+constexpr int kDecodeMaxGroup = 16;  // largest GQA group (Hq / Hkv): the MFMA N extent
 
 struct DecodePlan {
-  int group;       // Hq / Hkv
-  int gp;          // group rounded up to a power of two
-  int tt;          // tokens per tile
-  int tps;         // tiles per split (one workgroup)
-  int max_tiles;   // tiles a sequence can span
-  int max_splits;  // splits a sequence can span
-  size_t ws_bytes; // fp32 partials: [num_seqs][Hq][max_splits][D + 4]
+  int group;            // Hq / Hkv
+  int tt;               // tokens per tile
+  int tps;              // tiles per split (one workgroup)
+  int max_tiles;        // tiles a sequence can span
+  int max_splits;       // splits a sequence can span
+  size_t ws_bytes;      // fp32 partials [num_seqs][Hq][max_splits][D + 4]
 };
 
 DecodePlan plan_decode(int num_seqs, int hq, int hkv, int head_dim, int max_context_len,
@@ -54,7 +44,6 @@ struct DecodeArgs {
   float scale_log2;  // softmax scale * log2(e)
 };
 
-int launch_paged_decode(const DecodeArgs& a, sp_dtype dtype, int head_dim, int gp,
-                        hipStream_t stream);
+int launch_paged_decode(const DecodeArgs& a, sp_dtype dtype, int head_dim, hipStream_t stream);
 
 }  // namespace sp

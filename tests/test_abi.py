@@ -86,7 +86,7 @@ def test_decode_validation(sp_lib):
                  window, dtype, ws, ws_bytes, None)
 
     _expect(_lib.SP_EINVAL, call(_lay(), hq=3), "multiple")
-    _expect(_lib.SP_EUNSUPPORTED, call(_lay(), hq=32), "GQA group 16")
+    _expect(_lib.SP_EUNSUPPORTED, call(_lay(), hq=34), "GQA group 17")
     _expect(_lib.SP_EUNSUPPORTED, call(_lay(head_dim=96)), "head_dim 96")
     _expect(_lib.SP_EOOB, call(_lay(), max_ctx=33), "exceeds the block tables")
     _expect(_lib.SP_EINVAL, call(_lay(), window=-2), "window_left")
