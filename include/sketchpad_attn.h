@@ -145,6 +145,52 @@ int sp_paged_decode(void* out, const void* q,
                     float scale, int32_t window_left, sp_dtype dtype,
                     void* workspace, size_t workspace_bytes, void* stream);
 
+/*
+ * Prefill attention over packed variable-length sequences (FlashAttention-2 style, MFMA).
+ * Replaces MultiHeadAttention::forward with causal_mask / sliding_window_mask
+ * (transformer.rs:103-168, :415-451) and flash_attention (sketchpad-cubecl attention.rs:97-178),
+ * for a ragged batch packed into one token stream:
+ *   q, out : [total_q, Hq, D] contiguous;  k, v : [total_k, Hkv, D] contiguous
+ *   sequence s owns queries cu_seqlens_q[s]..cu_seqlens_q[s+1] and keys
+ *   cu_seqlens_k[s]..cu_seqlens_k[s+1] (device int32 arrays of num_seqs + 1 entries; pass the same
+ *   array twice for self-attention). max_seqlen_q must bound every sequence's query count.
+ *   causal : sp_causal; window_left >= 0 adds the sliding window (see above).
+ * Softmax and accumulation are fp32; a query that sees no key gets zeros. bf16 and f16,
+ * head_dim 64 or 128, GQA groups of any size.
+ */
+int sp_varlen_prefill(void* out, const void* q, const void* k, const void* v,
+                      const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+                      int32_t num_seqs, int32_t max_seqlen_q,
+                      int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                      float scale, int32_t causal, int32_t window_left,
+                      sp_dtype dtype, void* stream);
+
+/*
+ * Chunked prefill against a paged cache: the new tokens of every sequence attend to that
+ * sequence's whole paged context, which already holds them (append first with sp_kv_append).
+ * Replaces forward_cached with seq_len > 1 and prefill_causal_mask (llama.rs:250-260, :374-388):
+ * sequence s has context_lens[s] keys in the pools and cu_seqlens_q[s+1] - cu_seqlens_q[s] new
+ * queries, which sit at the last positions of the context (bottom-right causal).
+ *   q, out : [total_q, Hq, D] contiguous; block_tables [num_seqs, max_blocks_per_seq] (device).
+ */
+int sp_paged_prefill(void* out, const void* q,
+                     const void* k_pool, const void* v_pool, const sp_cache_layout* layout,
+                     const int32_t* block_tables, int32_t max_blocks_per_seq,
+                     const int32_t* cu_seqlens_q, const int32_t* context_lens,
+                     int32_t num_seqs, int32_t max_seqlen_q, int32_t num_q_heads,
+                     float scale, int32_t window_left, sp_dtype dtype, void* stream);
+
+/*
+ * Dense attention on [batch, heads, seq, head_dim] tensors: flash_attention(q, k, v,
+ * FlashAttentionOptions{causal}) (sketchpad-cubecl attention.rs:97-178). Equal head counts for
+ * q and k/v (the reference has no GQA there). causal uses the reference's test-oracle mask
+ * j > i (top-left, correctness_cpu.rs:1066-1074). The reference scales by head_dim^-0.5.
+ */
+int sp_flash_attention(void* out, const void* q, const void* k, const void* v,
+                       int32_t batch, int32_t num_heads, int32_t seq_q, int32_t seq_k,
+                       int32_t head_dim, float scale, int32_t causal, sp_dtype dtype,
+                       void* stream);
+
 #ifdef __cplusplus
 }
 #endif

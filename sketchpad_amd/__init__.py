@@ -14,10 +14,13 @@ from ._lib import (  # noqa: F401
     SP_F16,
     SP_F32,
     alloc_decode_workspace,
+    flash_attention,
     kv_append,
     kv_gather,
     layout,
     load,
     paged_decode,
     paged_decode_workspace_size,
+    paged_prefill,
+    varlen_prefill,
 )

@@ -67,6 +67,15 @@ _SIGNATURES = {
     "sp_paged_decode": (c_int32, [c_void_p, c_void_p, c_void_p, c_void_p, POINTER(CacheLayout),
                                   c_void_p, c_int32, c_void_p, c_int32, c_int32, c_int32,
                                   c_float, c_int32, c_int32, c_void_p, c_size_t, c_void_p]),
+    "sp_varlen_prefill": (c_int32, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+                                    c_int32, c_int32, c_int32, c_int32, c_int32, c_float,
+                                    c_int32, c_int32, c_int32, c_void_p]),
+    "sp_paged_prefill": (c_int32, [c_void_p, c_void_p, c_void_p, c_void_p, POINTER(CacheLayout),
+                                   c_void_p, c_int32, c_void_p, c_void_p, c_int32, c_int32,
+                                   c_int32, c_float, c_int32, c_int32, c_void_p]),
+    "sp_flash_attention": (c_int32, [c_void_p, c_void_p, c_void_p, c_void_p, c_int32, c_int32,
+                                     c_int32, c_int32, c_int32, c_float, c_int32, c_int32,
+                                     c_void_p]),
 }
 
 _lib = None
@@ -175,3 +184,31 @@ def alloc_decode_workspace(num_seqs: int, num_q_heads: int, max_context_len: int
     torch = _torch()
     n = paged_decode_workspace_size(num_seqs, num_q_heads, max_context_len, window_left, lay)
     return torch.empty(max(n, 256), dtype=torch.uint8, device=device)
+
+
+def varlen_prefill(out, q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q: int, scale: float, *,
+                   causal: int = SP_CAUSAL_BOTTOM_RIGHT, window_left: int = -1,
+                   stream=None) -> None:
+    """sp_varlen_prefill. q/out [total_q, Hq, D], k/v [total_k, Hkv, D] contiguous."""
+    check(load().sp_varlen_prefill(_ptr(out), _ptr(q), _ptr(k), _ptr(v), _ptr(cu_seqlens_q),
+                                   _ptr(cu_seqlens_k), cu_seqlens_q.numel() - 1, max_seqlen_q,
+                                   q.shape[1], k.shape[1], q.shape[2], scale, causal,
+                                   window_left, sp_dtype(q), _stream(stream)))
+
+
+def paged_prefill(out, q, k_pool, v_pool, lay: CacheLayout, block_tables, cu_seqlens_q,
+                  context_lens, max_seqlen_q: int, scale: float, *, window_left: int = -1,
+                  stream=None) -> None:
+    """sp_paged_prefill. q/out [total_q, Hq, D]; the new tokens are already in the pools."""
+    check(load().sp_paged_prefill(_ptr(out), _ptr(q), _ptr(k_pool), _ptr(v_pool),
+                                  ctypes.byref(lay), _ptr(block_tables), block_tables.shape[1],
+                                  _ptr(cu_seqlens_q), _ptr(context_lens),
+                                  cu_seqlens_q.numel() - 1, max_seqlen_q, q.shape[1], scale,
+                                  window_left, sp_dtype(q), _stream(stream)))
+
+
+def flash_attention(out, q, k, v, scale: float, *, causal: bool = False, stream=None) -> None:
+    """sp_flash_attention on [B, H, S, D] tensors."""
+    b, h, sq, d = q.shape
+    check(load().sp_flash_attention(_ptr(out), _ptr(q), _ptr(k), _ptr(v), b, h, sq, k.shape[2],
+                                    d, scale, int(bool(causal)), sp_dtype(q), _stream(stream)))

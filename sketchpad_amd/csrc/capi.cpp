@@ -10,6 +10,7 @@
 
 #include "kv_cache.hpp"
 #include "paged_decode.hpp"
+#include "prefill.hpp"
 #include "sp_common.hpp"
 
 namespace sp {
@@ -209,6 +210,143 @@ int sp_paged_decode(void* out, const void* q, const void* k_pool, const void* v_
   a.max_splits = p.max_splits;
   a.scale_log2 = scale * 1.4426950408889634f;
   return launch_paged_decode(a, dtype, D, (hipStream_t)stream);
+}
+
+static int check_prefill_common(const char* fn, int32_t num_seqs, int32_t max_seqlen_q,
+                                int32_t hq, int32_t hkv, int32_t D, float scale,
+                                int32_t causal, int32_t window_left, sp_dtype dtype) {
+  if (int rc = check_dtype(dtype, fn)) return rc;
+  if (dtype == SP_F32) return fail(SP_EUNSUPPORTED, "%s: f32 prefill has no kernel yet", fn);
+  if (num_seqs < 0 || max_seqlen_q < 0 || hq <= 0 || hkv <= 0)
+    return fail(SP_EINVAL, "%s: invalid sizes (num_seqs=%d max_seqlen_q=%d hq=%d hkv=%d)", fn,
+                num_seqs, max_seqlen_q, hq, hkv);
+  if (hq % hkv != 0)
+    return fail(SP_EINVAL, "%s: num_q_heads %d is not a multiple of num_kv_heads %d", fn, hq, hkv);
+  if (D != 64 && D != 128)
+    return fail(SP_EUNSUPPORTED, "%s: head_dim %d has no kernel (64, 128)", fn, D);
+  if (causal < SP_CAUSAL_NONE || causal > SP_CAUSAL_TOP_LEFT)
+    return fail(SP_EINVAL, "%s: unknown causal mode %d", fn, causal);
+  if (window_left < -1) return fail(SP_EINVAL, "%s: window_left %d < -1", fn, window_left);
+  if (!isfinite(scale)) return fail(SP_EINVAL, "%s: scale is not finite", fn);
+  return SP_OK;
+}
+
+static bool misaligned16(const void* p) { return ((uintptr_t)p & 15) != 0; }
+
+int sp_varlen_prefill(void* out, const void* q, const void* k, const void* v,
+                      const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k, int32_t num_seqs,
+                      int32_t max_seqlen_q, int32_t num_q_heads, int32_t num_kv_heads,
+                      int32_t head_dim, float scale, int32_t causal, int32_t window_left,
+                      sp_dtype dtype, void* stream) {
+  const char* fn = "sp_varlen_prefill";
+  if (int rc = check_prefill_common(fn, num_seqs, max_seqlen_q, num_q_heads, num_kv_heads,
+                                    head_dim, scale, causal, window_left, dtype))
+    return rc;
+  if (num_seqs == 0 || max_seqlen_q == 0) return SP_OK;
+  if (!out || !q || !k || !v || !cu_seqlens_q || !cu_seqlens_k)
+    return fail(SP_EINVAL, "%s: NULL pointer argument", fn);
+  if (misaligned16(out) || misaligned16(q) || misaligned16(k) || misaligned16(v))
+    return fail(SP_EINVAL, "%s: q, k, v and out must be 16-byte aligned", fn);
+  PrefillArgs a{};
+  a.out = out;
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.q_tok = a.o_tok = (int64_t)num_q_heads * head_dim;
+  a.q_head = a.o_head = head_dim;
+  a.kv_tok = (int64_t)num_kv_heads * head_dim;
+  a.kv_head = head_dim;
+  a.cu_q = cu_seqlens_q;
+  a.cu_k = cu_seqlens_k;
+  a.num_seqs = num_seqs;
+  a.hq = num_q_heads;
+  a.hkv = num_kv_heads;
+  a.group = num_q_heads / num_kv_heads;
+  a.num_qblocks = (max_seqlen_q + kPrefillBM - 1) / kPrefillBM;
+  a.causal = causal;
+  a.window_left = window_left;
+  a.scale_log2 = scale * 1.4426950408889634f;
+  return launch_prefill(a, dtype, head_dim, false, (hipStream_t)stream);
+}
+
+int sp_paged_prefill(void* out, const void* q, const void* k_pool, const void* v_pool,
+                     const sp_cache_layout* layout, const int32_t* block_tables,
+                     int32_t max_blocks_per_seq, const int32_t* cu_seqlens_q,
+                     const int32_t* context_lens, int32_t num_seqs, int32_t max_seqlen_q,
+                     int32_t num_q_heads, float scale, int32_t window_left, sp_dtype dtype,
+                     void* stream) {
+  const char* fn = "sp_paged_prefill";
+  if (int rc = check_layout(layout, fn)) return rc;
+  if (int rc = check_prefill_common(fn, num_seqs, max_seqlen_q, num_q_heads,
+                                    layout->num_kv_heads, layout->head_dim, scale,
+                                    SP_CAUSAL_BOTTOM_RIGHT, window_left, dtype))
+    return rc;
+  if (num_seqs == 0 || max_seqlen_q == 0) return SP_OK;
+  if (!out || !q || !k_pool || !v_pool || !block_tables || !cu_seqlens_q || !context_lens)
+    return fail(SP_EINVAL, "%s: NULL pointer argument", fn);
+  if (max_blocks_per_seq <= 0) return fail(SP_EINVAL, "%s: max_blocks_per_seq must be > 0", fn);
+  if (misaligned16(out) || misaligned16(q) || misaligned16(k_pool) || misaligned16(v_pool))
+    return fail(SP_EINVAL, "%s: q, out and pools must be 16-byte aligned", fn);
+  const int D = layout->head_dim;
+  PrefillArgs a{};
+  a.out = out;
+  a.q = q;
+  a.q_tok = a.o_tok = (int64_t)num_q_heads * D;
+  a.q_head = a.o_head = D;
+  a.cu_q = cu_seqlens_q;
+  a.num_seqs = num_seqs;
+  a.hq = num_q_heads;
+  a.hkv = layout->num_kv_heads;
+  a.group = num_q_heads / layout->num_kv_heads;
+  a.num_qblocks = (max_seqlen_q + kPrefillBM - 1) / kPrefillBM;
+  a.causal = SP_CAUSAL_BOTTOM_RIGHT;
+  a.window_left = window_left;
+  a.scale_log2 = scale * 1.4426950408889634f;
+  a.kpool = (const char*)k_pool;
+  a.vpool = (const char*)v_pool;
+  a.block_tables = block_tables;
+  a.context_lens = context_lens;
+  a.max_blocks_per_seq = max_blocks_per_seq;
+  a.block_size = layout->block_size;
+  a.num_blocks = layout->num_blocks;
+  pool_strides(layout, dtype_size(dtype), &a.block_stride_b, &a.layer_off_b);
+  return launch_prefill(a, dtype, D, true, (hipStream_t)stream);
+}
+
+int sp_flash_attention(void* out, const void* q, const void* k, const void* v, int32_t batch,
+                       int32_t num_heads, int32_t seq_q, int32_t seq_k, int32_t head_dim,
+                       float scale, int32_t causal, sp_dtype dtype, void* stream) {
+  const char* fn = "sp_flash_attention";
+  if (int rc = check_prefill_common(fn, batch, seq_q, num_heads, num_heads, head_dim, scale,
+                                    causal ? SP_CAUSAL_TOP_LEFT : SP_CAUSAL_NONE, -1, dtype))
+    return rc;
+  if (seq_k < 0) return fail(SP_EINVAL, "%s: seq_k %d < 0", fn, seq_k);
+  if (batch == 0 || seq_q == 0) return SP_OK;
+  if (!out || !q || !k || !v) return fail(SP_EINVAL, "%s: NULL pointer argument", fn);
+  if (misaligned16(out) || misaligned16(q) || misaligned16(k) || misaligned16(v))
+    return fail(SP_EINVAL, "%s: q, k, v and out must be 16-byte aligned", fn);
+  PrefillArgs a{};
+  a.out = out;
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  // [B, H, S, D]: token stride D, head stride S*D, batch stride H*S*D
+  a.q_tok = a.o_tok = head_dim;
+  a.q_head = a.o_head = (int64_t)seq_q * head_dim;
+  a.q_batch = a.o_batch = (int64_t)num_heads * seq_q * head_dim;
+  a.kv_tok = head_dim;
+  a.kv_head = (int64_t)seq_k * head_dim;
+  a.kv_batch = (int64_t)num_heads * seq_k * head_dim;
+  a.lq = seq_q;
+  a.lk = seq_k;
+  a.num_seqs = batch;
+  a.hq = a.hkv = num_heads;
+  a.group = 1;
+  a.num_qblocks = (seq_q + kPrefillBM - 1) / kPrefillBM;
+  a.causal = causal ? SP_CAUSAL_TOP_LEFT : SP_CAUSAL_NONE;
+  a.window_left = -1;
+  a.scale_log2 = scale * 1.4426950408889634f;
+  return launch_prefill(a, dtype, head_dim, false, (hipStream_t)stream);
 }
 
 }  // extern "C"

@@ -1,0 +1,44 @@
+// Launch interface of the causal / windowed prefill kernels (prefill.hip).
+#pragma once
+
+#include "sp_common.hpp"
+
+namespace sp {
+
+constexpr int kPrefillBM = 128;  // queries per workgroup (four waves x 32)
+constexpr int kPrefillBN = 64;   // keys per step
+
+struct PrefillArgs {
+  void* out;
+  const void* q;
+  const void* k;  // packed / dense K (unused when paged)
+  const void* v;
+  // element strides
+  int64_t q_tok, q_head, q_batch;
+  int64_t o_tok, o_head, o_batch;
+  int64_t kv_tok, kv_head, kv_batch;
+  const int32_t* cu_q;  // [num_seqs + 1] token offsets, or nullptr for dense batches
+  const int32_t* cu_k;  // [num_seqs + 1] key offsets (packed K/V), or nullptr
+  int lq, lk;           // dense lengths (cu_q / cu_k == nullptr)
+  int num_seqs;
+  int hq, hkv, group;
+  int num_qblocks;      // ceil(max_seqlen_q / kPrefillBM)
+  int causal;           // sp_causal
+  int window_left;      // -1: none
+  float scale_log2;     // softmax scale * log2(e)
+  // paged K/V source
+  const char* kpool;
+  const char* vpool;
+  const int32_t* block_tables;
+  const int32_t* context_lens;
+  int max_blocks_per_seq;
+  int block_size;
+  int num_blocks;
+  int64_t block_stride_b;
+  int64_t layer_off_b;
+};
+
+int launch_prefill(const PrefillArgs& a, sp_dtype dtype, int head_dim, bool paged,
+                   hipStream_t stream);
+
+}  // namespace sp

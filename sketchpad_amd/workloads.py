@@ -191,3 +191,181 @@ def make_decode_tensors(w: DecodeWorkload, device="cuda") -> dict:
     }
     t["out"] = torch.empty_like(t["q"])
     return t
+
+
+# ---------------------------------------------------------------------------------------------
+# prefill workloads
+# ---------------------------------------------------------------------------------------------
+
+@dataclass
+class PrefillWorkload:
+    """Causal self-attention prefill of a ragged batch packed into one token stream. The step
+    also appends every token's K/V into a paged pool (block size 16) through a slot mapping."""
+
+    name: str
+    seed: int
+    lens: np.ndarray          # int32 [num_seqs] tokens per sequence
+    hq: int
+    hkv: int
+    head_dim: int
+    dtype: str
+    block_size: int = 16
+
+    @property
+    def num_seqs(self) -> int:
+        return len(self.lens)
+
+    @property
+    def cu_seqlens(self) -> np.ndarray:
+        return np.concatenate([[0], np.cumsum(self.lens)]).astype(np.int32)
+
+    @property
+    def total_tokens(self) -> int:
+        return int(self.lens.sum())
+
+    @property
+    def max_seqlen(self) -> int:
+        return int(self.lens.max())
+
+    def flops(self) -> int:
+        """4 * Hq * D per visible (query, key) pair; causal: L(L+1)/2 pairs per sequence."""
+        L = self.lens.astype(np.int64)
+        return int(4 * self.hq * self.head_dim * (L * (L + 1) // 2).sum())
+
+    def pool_tables(self):
+        rng = np.random.default_rng(self.seed + 1)
+        nblk = int(((self.lens + self.block_size - 1) // self.block_size).sum())
+        return _tables_from_pool(rng, self.lens, self.block_size, nblk), nblk
+
+    def slot_mapping(self) -> np.ndarray:
+        tables, _ = self.pool_tables()
+        out = []
+        for s, L in enumerate(self.lens):
+            pos = np.arange(L)
+            out.append(tables[s, pos // self.block_size] * self.block_size + pos % self.block_size)
+        return np.concatenate(out).astype(np.int32)
+
+
+def prefill_c3() -> PrefillWorkload:
+    seed = seed_for(3)
+    rng = np.random.default_rng(seed)
+    lens = rng.integers(256, 2048, size=8, endpoint=True).astype(np.int32)
+    return PrefillWorkload("C3-llama3-8b-ragged-prefill", seed, lens, 32, 8, 128, "bf16")
+
+
+def make_prefill_tensors(w: PrefillWorkload, device="cuda", with_pool: bool = True) -> dict:
+    import torch
+    g = torch.Generator(device=device)
+    g.manual_seed(w.seed)
+    dt = torch_dtype(w.dtype)
+
+    def randn(*shape):
+        return torch.randn(*shape, generator=g, device=device, dtype=torch.float32).to(dt)
+
+    T = w.total_tokens
+    t = {
+        "q": randn(T, w.hq, w.head_dim),
+        "k": randn(T, w.hkv, w.head_dim),
+        "v": randn(T, w.hkv, w.head_dim),
+        "cu_seqlens": torch.from_numpy(w.cu_seqlens).to(device),
+    }
+    t["out"] = torch.empty_like(t["q"])
+    if with_pool:
+        tables, nblk = w.pool_tables()
+        t["k_pool"] = torch.zeros(nblk, 1, w.hkv, w.block_size, w.head_dim, dtype=dt, device=device)
+        t["v_pool"] = torch.zeros_like(t["k_pool"])
+        t["block_tables"] = torch.from_numpy(tables).to(device)
+        t["slot_mapping"] = torch.from_numpy(w.slot_mapping()).to(device)
+        t["num_blocks"] = nblk
+    return t
+
+
+@dataclass
+class ChunkedPrefillWorkload:
+    """New-token chunks attending to a paged context that already holds them (bottom-right
+    causal), i.e. forward_cached with seq_len > 1 and prefill_causal_mask."""
+
+    name: str
+    seed: int
+    chunk_lens: np.ndarray     # int32 [S] new tokens per sequence
+    ctx_before: np.ndarray     # int32 [S] cached tokens before the chunk
+    hq: int
+    hkv: int
+    head_dim: int
+    dtype: str
+    block_size: int = 16
+    window_left: int = -1
+
+    @property
+    def num_seqs(self) -> int:
+        return len(self.chunk_lens)
+
+    @property
+    def context_lens(self) -> np.ndarray:
+        return (self.ctx_before + self.chunk_lens).astype(np.int32)
+
+    @property
+    def cu_seqlens_q(self) -> np.ndarray:
+        return np.concatenate([[0], np.cumsum(self.chunk_lens)]).astype(np.int32)
+
+    @property
+    def max_seqlen_q(self) -> int:
+        return int(self.chunk_lens.max())
+
+    def flops(self) -> int:
+        c = self.chunk_lens.astype(np.int64)
+        b = self.ctx_before.astype(np.int64)
+        pairs = (c * b + c * (c + 1) // 2).sum()
+        return int(4 * self.hq * self.head_dim * pairs)
+
+    def tables(self):
+        rng = np.random.default_rng(self.seed + 1)
+        lens = self.context_lens
+        nblk = int(((lens + self.block_size - 1) // self.block_size).sum())
+        return _tables_from_pool(rng, lens, self.block_size, nblk), nblk
+
+    def slot_mapping(self) -> np.ndarray:
+        tables, _ = self.tables()
+        out = []
+        for s in range(self.num_seqs):
+            pos = np.arange(self.ctx_before[s], self.context_lens[s])
+            out.append(tables[s, pos // self.block_size] * self.block_size + pos % self.block_size)
+        return np.concatenate(out).astype(np.int32)
+
+
+def chunked_prefill_c4() -> ChunkedPrefillWorkload:
+    """The prefill half of C4: 4 chunks of 512 new tokens on contexts U[1024, 8192]."""
+    seed = seed_for(4) + 100
+    rng = np.random.default_rng(seed)
+    ctx = rng.integers(1024, 8192, size=4, endpoint=True).astype(np.int32)
+    chunks = np.full(4, 512, dtype=np.int32)
+    return ChunkedPrefillWorkload("C4-qwen25-7b-chunked-prefill", seed, chunks, ctx, 28, 4, 128,
+                                  "bf16")
+
+
+def make_chunked_tensors(w: ChunkedPrefillWorkload, device="cuda") -> dict:
+    """Pools with random cached context, the chunk's q/k/v, metadata."""
+    import torch
+    g = torch.Generator(device=device)
+    g.manual_seed(w.seed)
+    dt = torch_dtype(w.dtype)
+    tables, nblk = w.tables()
+
+    def randn(*shape):
+        return torch.randn(*shape, generator=g, device=device, dtype=torch.float32).to(dt)
+
+    T = int(w.chunk_lens.sum())
+    t = {
+        "k_pool": randn(nblk, 1, w.hkv, w.block_size, w.head_dim),
+        "v_pool": randn(nblk, 1, w.hkv, w.block_size, w.head_dim),
+        "q": randn(T, w.hq, w.head_dim),
+        "k_new": randn(T, w.hkv, w.head_dim),
+        "v_new": randn(T, w.hkv, w.head_dim),
+        "block_tables": torch.from_numpy(tables).to(device),
+        "context_lens": torch.from_numpy(w.context_lens).to(device),
+        "cu_seqlens_q": torch.from_numpy(w.cu_seqlens_q).to(device),
+        "slot_mapping": torch.from_numpy(w.slot_mapping()).to(device),
+        "num_blocks": nblk,
+    }
+    t["out"] = torch.empty_like(t["q"])
+    return t

@@ -1,0 +1,226 @@
+"""GPU parity of the prefill paths against the f64 oracle (attention per sequence with the
+reference's masks: causal_mask / prefill_causal_mask / sliding_window_mask, transformer.rs:415-451,
+llama.rs:374-388) and, at the full C3 / C4 sizes, against a float32 torch reference on the GPU plus
+oracle rows sampled from every sequence."""
+import numpy as np
+import pytest
+import torch
+
+import sketchpad_amd as sp
+from oracle import oracle as O
+from sketchpad_amd import workloads as W
+from tests.helpers import announce, assert_attention_close, host_array, oracle_dtype
+
+pytestmark = pytest.mark.gpu
+
+DT = {"bf16": torch.bfloat16, "f16": torch.float16}
+
+
+def _rand(g, *shape, dt):
+    return torch.randn(*shape, generator=g, device="cuda", dtype=torch.float32).to(dt)
+
+
+def _oracle_varlen(q, k, v, cu_q, cu_k, scale, causal_mode, window):
+    """Per-sequence f64 oracle over packed q [Tq, Hq, D], k/v [Tk, Hkv, D] (host arrays)."""
+    out = np.zeros(q.shape, dtype=np.float64)
+    dt = O.BF16 if q.dtype == np.uint16 else O.F32
+    for s in range(len(cu_q) - 1):
+        qa, qb, ka, kb = cu_q[s], cu_q[s + 1], cu_k[s], cu_k[s + 1]
+        lq, lk = qb - qa, kb - ka
+        if lq == 0:
+            continue
+        causal = causal_mode != sp.SP_CAUSAL_NONE
+        pos0 = 0 if causal_mode == sp.SP_CAUSAL_TOP_LEFT else lk - lq
+        out[qa:qb] = O.attention_f64(q[qa:qb], k[ka:kb], v[ka:kb], scale=scale, causal=causal,
+                                     q_pos0=pos0, window_left=window, dtype=dt)
+    return out
+
+
+def _as_f64(t):
+    return t.float().cpu().numpy().astype(np.float64)
+
+
+def run_varlen(lens_q, lens_k, hq, hkv, d, dtype, causal, window, seed):
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    dt = DT[dtype]
+    cu_q = np.concatenate([[0], np.cumsum(lens_q)]).astype(np.int32)
+    cu_k = np.concatenate([[0], np.cumsum(lens_k)]).astype(np.int32)
+    q = _rand(g, int(cu_q[-1]), hq, d, dt=dt)
+    k = _rand(g, int(cu_k[-1]), hkv, d, dt=dt)
+    v = _rand(g, int(cu_k[-1]), hkv, d, dt=dt)
+    out = torch.full_like(q, float("nan"))
+    announce(f"varlen prefill lens_q={list(lens_q)} lens_k={list(lens_k)} hq={hq} hkv={hkv} "
+             f"d={d} {dtype} causal={causal} window={window}")
+    sp.varlen_prefill(out, q, k, v, torch.from_numpy(cu_q).cuda(), torch.from_numpy(cu_k).cuda(),
+                      int(max(lens_q)), d ** -0.5, causal=causal, window_left=window)
+    torch.cuda.synchronize()
+    # the oracle reads 16-bit tensors as bf16 bits; f16 inputs are handed over as float32
+    to_host = host_array if dtype == "bf16" else (lambda t: t.float().cpu().numpy())
+    ref = _oracle_varlen(to_host(q), to_host(k), to_host(v), cu_q, cu_k, d ** -0.5, causal, window)
+    assert_attention_close(_as_f64(out), ref, dtype, "varlen prefill")
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f16"])
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("hq,hkv", [(4, 4), (8, 2), (7, 1)])
+def test_varlen_causal_self(dtype, d, hq, hkv):
+    lens = [1, 5, 16, 17, 64, 65, 127, 128, 129, 200, 300]
+    run_varlen(lens, lens, hq, hkv, d, dtype, sp.SP_CAUSAL_BOTTOM_RIGHT, -1, seed=hq * 10 + d)
+
+
+def test_varlen_llama_heads():
+    lens = [256, 33, 513, 130]
+    run_varlen(lens, lens, 32, 8, 128, "bf16", sp.SP_CAUSAL_BOTTOM_RIGHT, -1, seed=3)
+
+
+@pytest.mark.parametrize("causal", [sp.SP_CAUSAL_NONE, sp.SP_CAUSAL_BOTTOM_RIGHT,
+                                    sp.SP_CAUSAL_TOP_LEFT])
+def test_varlen_cross_lengths(causal):
+    """Lq != Lk: the bottom-right mask is prefill_causal_mask (queries are the last positions)."""
+    lens_q = [3, 40, 130, 64, 1]
+    lens_k = [10, 200, 130, 300, 77]
+    run_varlen(lens_q, lens_k, 8, 4, 128, "bf16", causal, -1, seed=11 + causal)
+
+
+@pytest.mark.parametrize("window", [0, 1, 31, 64, 100])
+def test_varlen_sliding_window(window):
+    """Mistral's sliding_window_mask(W): keys [i - W, i] (window_left = W)."""
+    lens = [7, 150, 300, 65]
+    run_varlen(lens, lens, 8, 2, 128, "bf16", sp.SP_CAUSAL_BOTTOM_RIGHT, window, seed=21 + window)
+
+
+def test_varlen_empty_sequences():
+    lens = [0, 50, 0, 3]
+    run_varlen(lens, lens, 4, 2, 64, "bf16", sp.SP_CAUSAL_BOTTOM_RIGHT, -1, seed=31)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("sq,sk", [(16, 16), (64, 64), (130, 70), (33, 200)])
+def test_flash_attention_dense(causal, sq, sk):
+    """flash_attention on [B, H, S, D]; causal is the reference test oracle's j > i mask."""
+    B, H, D = 2, 4, 64
+    g = torch.Generator(device="cuda").manual_seed(sq + sk + causal)
+    q = _rand(g, B, H, sq, D, dt=torch.bfloat16)
+    k = _rand(g, B, H, sk, D, dt=torch.bfloat16)
+    v = _rand(g, B, H, sk, D, dt=torch.bfloat16)
+    out = torch.empty_like(q)
+    announce(f"flash_attention dense sq={sq} sk={sk} causal={causal}")
+    sp.flash_attention(out, q, k, v, D ** -0.5, causal=causal)
+    torch.cuda.synchronize()
+    qh, kh, vh = host_array(q), host_array(k), host_array(v)
+    ref = np.zeros((B, H, sq, D))
+    for bi in range(B):
+        r = O.attention_f64(qh[bi].transpose(1, 0, 2), kh[bi].transpose(1, 0, 2),
+                            vh[bi].transpose(1, 0, 2), scale=D ** -0.5, causal=causal, q_pos0=0,
+                            dtype=O.BF16)
+        ref[bi] = r.transpose(1, 0, 2)
+    assert_attention_close(_as_f64(out), ref, "bf16", "flash_attention")
+
+
+def run_chunked(w: W.ChunkedPrefillWorkload, sample_rows=None):
+    t = W.make_chunked_tensors(w)
+    lay = sp.layout(t["num_blocks"], 1, 0, w.hkv, w.block_size, w.head_dim)
+    announce(f"chunked prefill {w.name} chunks={list(w.chunk_lens)} ctx={list(w.ctx_before)}")
+    sp.kv_append(t["k_pool"], t["v_pool"], lay, t["k_new"], t["v_new"], t["slot_mapping"])
+    sp.paged_prefill(t["out"], t["q"], t["k_pool"], t["v_pool"], lay, t["block_tables"],
+                     t["cu_seqlens_q"], t["context_lens"], w.max_seqlen_q, w.head_dim ** -0.5,
+                     window_left=w.window_left)
+    torch.cuda.synchronize()
+    olay = O.make_layout(t["num_blocks"], 1, 0, w.hkv, w.block_size, w.head_dim)
+    kp, vp, q = host_array(t["k_pool"]), host_array(t["v_pool"]), host_array(t["q"])
+    got = _as_f64(t["out"])
+    cu = w.cu_seqlens_q
+    rng = np.random.default_rng(0)
+    for s in range(w.num_seqs):
+        L = int(w.context_lens[s])
+        kg, vg = O.gather_kv(kp, vp, olay, w.block_tables_np[s] if hasattr(w, "block_tables_np")
+                             else t["block_tables"][s].cpu().numpy(), L)
+        kt = np.ascontiguousarray(kg.transpose(1, 0, 2))
+        vt = np.ascontiguousarray(vg.transpose(1, 0, 2))
+        lq = int(w.chunk_lens[s])
+        rows = np.arange(lq) if sample_rows is None else np.unique(
+            np.concatenate([[0, lq - 1], rng.choice(lq, size=min(lq, sample_rows), replace=False)]))
+        for i in rows:
+            pos = L - lq + i
+            ref = O.attention_f64(q[cu[s] + i:cu[s] + i + 1], kt[:pos + 1], vt[:pos + 1],
+                                  scale=w.head_dim ** -0.5, causal=True, q_pos0=pos,
+                                  window_left=w.window_left, dtype=O.BF16)
+            assert_attention_close(got[cu[s] + i:cu[s] + i + 1], ref, w.dtype,
+                                   f"{w.name} seq {s} row {i}")
+    return t
+
+
+def test_paged_prefill_small():
+    w = W.ChunkedPrefillWorkload("chunked-small", 41, np.array([1, 17, 130, 64], np.int32),
+                                 np.array([0, 40, 300, 5], np.int32), 8, 2, 128, "bf16")
+    run_chunked(w)
+
+
+def test_paged_prefill_window():
+    w = W.ChunkedPrefillWorkload("chunked-window", 42, np.array([50, 129], np.int32),
+                                 np.array([200, 90], np.int32), 8, 2, 64, "bf16", window_left=70)
+    run_chunked(w)
+
+
+def test_paged_prefill_block_size_32():
+    w = W.ChunkedPrefillWorkload("chunked-bs32", 43, np.array([65, 100], np.int32),
+                                 np.array([77, 31], np.int32), 4, 4, 128, "bf16", block_size=32)
+    run_chunked(w)
+
+
+def test_chunked_prefill_c4_sampled_rows():
+    run_chunked(W.chunked_prefill_c4(), sample_rows=24)
+
+
+def _torch_ref_causal(q, k, v, cu, scale):
+    """float32 torch reference for causal self-attention over packed sequences (GPU)."""
+    out = torch.empty(q.shape, dtype=torch.float32, device=q.device)
+    hq, hkv = q.shape[1], k.shape[1]
+    for s in range(len(cu) - 1):
+        a, b = int(cu[s]), int(cu[s + 1])
+        qf = q[a:b].float().permute(1, 0, 2).contiguous()                       # [Hq, L, D]
+        kf = k[a:b].float().permute(1, 0, 2).repeat_interleave(hq // hkv, 0)   # [Hq, L, D]
+        vf = v[a:b].float().permute(1, 0, 2).repeat_interleave(hq // hkv, 0)
+        sc = torch.matmul(qf, kf.transpose(1, 2).contiguous()) * scale
+        L = b - a
+        mask = torch.ones(L, L, dtype=torch.bool, device=q.device).triu(1)
+        sc.masked_fill_(mask, float("-inf"))
+        out[a:b] = torch.matmul(torch.softmax(sc, dim=-1), vf.contiguous()).permute(1, 0, 2)
+    return out
+
+
+def test_prefill_c3_full_size():
+    """C3 at full size: every row against a float32 torch reference, sampled rows against the
+    f64 oracle, and the appended pool rows bit-exact."""
+    w = W.prefill_c3()
+    t = W.make_prefill_tensors(w)
+    lay = sp.layout(t["num_blocks"], 1, 0, w.hkv, w.block_size, w.head_dim)
+    announce(f"prefill {w.name} lens={list(w.lens)}")
+    sp.kv_append(t["k_pool"], t["v_pool"], lay, t["k"], t["v"], t["slot_mapping"])
+    sp.varlen_prefill(t["out"], t["q"], t["k"], t["v"], t["cu_seqlens"], t["cu_seqlens"],
+                      w.max_seqlen, w.head_dim ** -0.5)
+    torch.cuda.synchronize()
+    ref = _torch_ref_causal(t["q"], t["k"], t["v"], w.cu_seqlens, w.head_dim ** -0.5)
+    err = (t["out"].float() - ref).abs().max().item()
+    assert err <= 2e-2, f"C3 vs fp32 torch: {err}"
+    # oracle rows
+    q, k, v = host_array(t["q"]), host_array(t["k"]), host_array(t["v"])
+    rng = np.random.default_rng(1)
+    got = _as_f64(t["out"])
+    cu = w.cu_seqlens
+    for s in range(w.num_seqs):
+        L = int(w.lens[s])
+        for i in np.unique(np.concatenate([[0, L - 1], rng.choice(L, 6, replace=False)])):
+            r = O.attention_f64(q[cu[s] + i:cu[s] + i + 1], k[cu[s]:cu[s] + i + 1],
+                                v[cu[s]:cu[s] + i + 1], scale=w.head_dim ** -0.5, causal=True,
+                                q_pos0=i, dtype=O.BF16)
+            assert_attention_close(got[cu[s] + i:cu[s] + i + 1], r, "bf16", f"C3 seq {s} row {i}")
+    # the append wrote every token's rows exactly
+    tables, _ = w.pool_tables()
+    kp = t["k_pool"]
+    for s in range(w.num_seqs):
+        L = int(w.lens[s])
+        pos = torch.arange(L, device="cuda")
+        blk = torch.from_numpy(tables[s]).cuda()[pos // w.block_size].long()
+        rows = kp[blk, 0, :, pos % w.block_size, :]             # [L, Hkv, D]
+        assert torch.equal(rows, t["k"][cu[s]:cu[s + 1]])
