@@ -1,6 +1,8 @@
 """Benchmark of the ragged-batch attention path on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config C2] [--no-cpu-baseline]
+                    [--no-prefill] [--secondary]
+    python bench.py --calibrate-copy    # plain 512 MiB device copies (HBM counter calibration)
 
 A step is one decode step of the BASELINE headline workload (C2, Llama-3-8B shape): append the
 step's new K/V row of each of the 64 sequences into the paged pool (sp_kv_append), then paged
@@ -11,6 +13,9 @@ before the timed region starts. Prints one JSON line:
              launch stream) against MI355X's 8 TB/s HBM peak
   cpu_baseline  the oracle's C port of the reference's decode op sequence (f32, OpenMP) timed
              on this host on the same workload
+  prefill    the C3 ragged causal prefill (sp_varlen_prefill, bf16 MFMA): average launch time,
+             TFLOP/s over the unmasked (query, key) pairs and the fraction of the 2.5 PFLOP/s
+             dense bf16 peak, the C3 append, and the oracle's prefill port on a bounded sample
 """
 from __future__ import annotations
 
@@ -28,6 +33,7 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0
 METRIC = "paged-decode HBM GB/s (% of peak) + ragged-prefill TFLOP/s, Llama-3-8B shape"
 
 
@@ -40,6 +46,10 @@ def parse_args():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="approximate CPU time budget of the cpu_baseline leg")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only run 10 plain 512 MiB device-to-device copies and exit")
+    ap.add_argument("--no-prefill", action="store_true",
+                    help="skip the C3 ragged-prefill leg")
     ap.add_argument("--secondary", action="store_true",
                     help="also time the other decode configs (C4, C5) and report them")
     return ap.parse_args()
@@ -142,6 +152,128 @@ def cpu_baseline(w, t, budget_s: float):
     }
 
 
+def _event_times(stream, fn, reps: int):
+    """Average / min milliseconds of fn() with HIP events recorded on the launch stream."""
+    import torch
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(reps)]
+    for a, b in ev:
+        a.record(stream)
+        fn()
+        b.record(stream)
+    torch.cuda.synchronize()
+    ms = [a.elapsed_time(b) for a, b in ev]
+    return float(np.mean(ms)), float(np.min(ms))
+
+
+def time_prefill_c3(steps: int, warmup: int):
+    """C3: append every token's K/V into the paged pool, then ragged causal prefill over the
+    packed stream (sp_varlen_prefill). Returns per-launch times of both."""
+    import torch
+    import sketchpad_amd as sp
+    from sketchpad_amd import workloads as W
+
+    w = W.prefill_c3()
+    t = W.make_prefill_tensors(w)
+    lay = sp.layout(t["num_blocks"], 1, 0, w.hkv, w.block_size, w.head_dim)
+    stream = torch.cuda.current_stream()
+    s = stream.cuda_stream
+
+    def append():
+        sp.kv_append(t["k_pool"], t["v_pool"], lay, t["k"], t["v"], t["slot_mapping"], stream=s)
+
+    def prefill():
+        sp.varlen_prefill(t["out"], t["q"], t["k"], t["v"], t["cu_seqlens"], t["cu_seqlens"],
+                          w.max_seqlen, w.head_dim ** -0.5, stream=s)
+
+    for _ in range(warmup):
+        append()
+        prefill()
+    torch.cuda.synchronize()
+    pf_ms, pf_min = _event_times(stream, prefill, steps)
+    ap_ms, _ = _event_times(stream, append, steps)
+    flops = w.flops()
+    tflops = flops / (pf_ms * 1e-3) / 1e12
+    e = 2
+    append_bytes = w.total_tokens * w.hkv * w.head_dim * e * 2 * 2 + w.total_tokens * 4
+    return w, {
+        "workload": f"{w.name}: B={w.num_seqs}, lens={[int(x) for x in w.lens]} "
+                    f"(sum {w.total_tokens}), Hq={w.hq}, Hkv={w.hkv}, D={w.head_dim}, causal, "
+                    f"seed {w.seed:#x}",
+        "ms": round(pf_ms, 5),
+        "ms_min": round(pf_min, 5),
+        "tflops": round(tflops, 2),
+        "roofline": {
+            "bound": "mfma",
+            "achieved": round(tflops, 2),
+            "peak": MFMA_BF16_PEAK_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
+            "kernel": "prefill_kernel<bf16,128,false> (one sp_varlen_prefill call)",
+            "algorithmic_flops": flops,
+        },
+        "append": {"ms": round(ap_ms, 5), "bytes": append_bytes,
+                   "GBs": round(append_bytes / (ap_ms * 1e-3) / 1e9, 2)},
+    }
+
+
+def time_chunked_c4(steps: int, warmup: int):
+    """C4 prefill half: 4 chunks of 512 new tokens against paged contexts (sp_paged_prefill)."""
+    import torch
+    import sketchpad_amd as sp
+    from sketchpad_amd import workloads as W
+
+    w = W.chunked_prefill_c4()
+    t = W.make_chunked_tensors(w)
+    lay = sp.layout(t["num_blocks"], 1, 0, w.hkv, w.block_size, w.head_dim)
+    stream = torch.cuda.current_stream()
+    s = stream.cuda_stream
+    sp.kv_append(t["k_pool"], t["v_pool"], lay, t["k_new"], t["v_new"], t["slot_mapping"],
+                 stream=s)
+
+    def prefill():
+        sp.paged_prefill(t["out"], t["q"], t["k_pool"], t["v_pool"], lay, t["block_tables"],
+                         t["cu_seqlens_q"], t["context_lens"], w.max_seqlen_q,
+                         w.head_dim ** -0.5, stream=s)
+
+    for _ in range(warmup):
+        prefill()
+    torch.cuda.synchronize()
+    ms, _ = _event_times(stream, prefill, steps)
+    tflops = w.flops() / (ms * 1e-3) / 1e12
+    return {"ms": round(ms, 5), "tflops": round(tflops, 2),
+            "frac_mfma": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4)}
+
+
+def cpu_prefill_baseline(w, budget_s: float):
+    """The oracle's C port of the reference's prefill op sequence ([Hq, L, L] f32 scores per
+    sequence) on a bounded sample: the two shortest C3 sequences."""
+    import torch
+    from oracle import oracle as O
+    from sketchpad_amd import workloads as W
+
+    threads = min(16, os.cpu_count() or 1)
+    idx = np.argsort(w.lens)[:2]
+    lens = w.lens[idx]
+    sub = W.PrefillWorkload(w.name + "-sample", w.seed, lens, w.hq, w.hkv, w.head_dim, w.dtype)
+    t = W.make_prefill_tensors(sub, device="cpu", with_pool=False)
+    q, k, v = (t[n].float().numpy() for n in ("q", "k", "v"))
+    out = np.empty_like(q)
+    reps, spent = 0, 0.0
+    while spent < budget_s and reps < 50:
+        t0 = time.perf_counter()
+        O.cpu_prefill_baseline(out, q, k, v, sub.cu_seqlens, hq=w.hq, hkv=w.hkv, d=w.head_dim,
+                               scale=w.head_dim ** -0.5, threads=threads)
+        spent += time.perf_counter() - t0
+        reps += 1
+    per = spent / reps
+    return {"value": round(sub.flops() / per / 1e12, 5), "unit": "TFLOP/s", "cores": threads,
+            "kind": "port",
+            "sample": f"C3 sequences of length {[int(x) for x in lens]}: {reps} causal prefills "
+                      f"(repeat_kv + [Hq,L,L] f32 scores + mask + softmax + matmul), "
+                      f"{per * 1e3:.1f} ms each"}
+
+
 def main():
     args = parse_args()
     if args.gpus != 1:
@@ -154,6 +286,14 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py: no GPU visible", file=sys.stderr)
         sys.exit(1)
+    if args.calibrate_copy:
+        src = torch.ones(512 << 20, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(10):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"calibrate_copy_bytes": src.numel(), "copies": 10}), flush=True)
+        return
     w = W.DECODE_CONFIGS[args.config]()
     r = time_decode_config(w, args.steps, args.warmup)
     step_bytes = r["decode_bytes"] + r["append_bytes"]
@@ -195,6 +335,13 @@ def main():
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(w, r["tensors"], args.cpu_seconds)
     del r
+    if not args.no_prefill:
+        wp, pf = time_prefill_c3(max(10, args.steps // 2), 3)
+        if not args.no_cpu_baseline:
+            pf["cpu_baseline"] = cpu_prefill_baseline(wp, args.cpu_seconds / 2)
+        line["prefill"] = pf
+    if args.secondary:
+        line.setdefault("secondary", {})["C4-chunked-prefill"] = time_chunked_c4(10, 2)
     if args.secondary:
         sec = {}
         for name in ("C4", "C5", "C1"):
@@ -206,7 +353,7 @@ def main():
             sec[name] = {"decode_ms": round(rx["decode_ms_avg"], 5), "decode_GBs": round(gbs, 2),
                          "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
             del rx
-        line["secondary"] = sec
+        line.setdefault("secondary", {}).update(sec)
     print(json.dumps(line), flush=True)
 
 
