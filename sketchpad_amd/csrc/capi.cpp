@@ -227,7 +227,10 @@ static int check_prefill_common(const char* fn, int32_t num_seqs, int32_t max_se
   if (causal < SP_CAUSAL_NONE || causal > SP_CAUSAL_TOP_LEFT)
     return fail(SP_EINVAL, "%s: unknown causal mode %d", fn, causal);
   if (window_left < -1) return fail(SP_EINVAL, "%s: window_left %d < -1", fn, window_left);
-  if (!isfinite(scale)) return fail(SP_EINVAL, "%s: scale is not finite", fn);
+  // The kernel folds the scale into the exponent after taking the row maximum of the raw
+  // scores, which needs scale > 0 (the reference always uses head_dim^-0.5).
+  if (!isfinite(scale) || !(scale > 0.f))
+    return fail(SP_EINVAL, "%s: scale must be finite and > 0 (got %g)", fn, (double)scale);
   return SP_OK;
 }
 

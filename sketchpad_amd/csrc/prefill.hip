@@ -7,17 +7,21 @@
 // Lk keys, sitting at position p = i + (Lk - Lq) (bottom-right) or p = i (top-left),
 //   out[i, h, :] = softmax_j((q[i,h,:] . k[j, h/G, :]) * scale) @ v[j, h/G, :]
 // over keys j < Lk with j <= p when causal and j >= p - window_left when windowed; fp32 softmax
-// and accumulation; a query with no visible key gets zeros.
+// and accumulation (FlashAttention-2 online softmax, Dao 2023); a query with no visible key gets
+// zeros.
 //
-// Tiling: a workgroup of four waves owns 128 queries of one head (32 per wave, two 16-query MFMA
-// column blocks) and walks the keys in steps of 64. Each step's K and V tiles (64 x D) are loaded
-// cooperatively with 16-byte coalesced loads one step ahead into registers and staged in a double
-// buffer in LDS. Per wave and step:
-//   S^T[64 keys, 32 q]  = K Q^T        MFMA 16x16x32; K from LDS (A operand, 16-byte reads),
-//                                      Q^T held in registers for the whole kernel (B operand)
-//   online softmax per query column: the 16 keys of a lane are local, two shuffles per step
-//   O^T[D, 32 q]       += V^T P^T      MFMA 16x16x16; P^T is the S^T accumulator layout as is,
-//                                      V^T comes from row-major V in LDS through ds_read_tr16_b64
+// Tiling: a workgroup of four waves owns 128 queries of one head (32 per wave) and walks the keys
+// in tiles of 64. Both products run on v_mfma_f32_32x32x16 (bf16 / f16):
+//   S^T[32 keys, 32 q] = K Q^T   A = K rows from LDS (16 bytes per lane), B = Q^T in registers
+//                                (loaded once). Lane l ends up holding 16 scores of query l%32, so
+//                                the softmax max / sum are in-lane plus one permlane32 swap.
+//   O^T[32 d, 32 q]   += V^T P^T B = P^T straight from the S^T registers (the 16 tokens of one
+//                                MFMA are taken in the order the S^T layout hands them out); A = V^T
+//                                from row-major V in LDS through ds_read_tr16_b64.
+// K/V tiles go HBM -> LDS with global_load_lds_dwordx4 (no register staging) into a double
+// buffer; the load of tile t+1 is issued right after the barrier that opens tile t. Rows are
+// stored with the 16-byte chunks XOR-swizzled so that the K reads (16 rows x one chunk) and the
+// V transpose reads (4 rows x 64 bytes) are bank-conflict free.
 // Only tiles that cross the causal diagonal, the window edge or the sequence end are masked.
 // Workgroups are ordered with the KV head fastest (all query heads of one KV head share an XCD's
 // L2) and the heaviest causal query blocks first.
@@ -29,59 +33,73 @@ namespace sp {
 
 typedef __bf16 pf_bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 pf_f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 pf_bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 pf_f16x2 __attribute__((ext_vector_type(2)));
+typedef float pf_f32x2 __attribute__((ext_vector_type(2)));
+typedef float pf_f32x16 __attribute__((ext_vector_type(16)));
 typedef short pf_s16x4 __attribute__((ext_vector_type(4)));
-typedef _Float16 pf_f16x4 __attribute__((ext_vector_type(4)));
-typedef float pf_f32x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) pf_s16x4 lds_s16x4;
+typedef __attribute__((address_space(3))) void lds_void;
 
 template <typename T> struct PrefillMfma;
 template <> struct PrefillMfma<bf16_t> {
-  __device__ __forceinline__ static pf_f32x4 qk(uint4 k, uint4 q, pf_f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(pf_bf16x8, k),
-                                                   __builtin_bit_cast(pf_bf16x8, q), c, 0, 0, 0);
+  __device__ __forceinline__ static pf_f32x16 mma(uint4 a, uint4 b, pf_f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(pf_bf16x8, a),
+                                                   __builtin_bit_cast(pf_bf16x8, b), c, 0, 0, 0);
   }
-  __device__ __forceinline__ static pf_f32x4 pv(pf_s16x4 v, uint2 p, pf_f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(v, __builtin_bit_cast(pf_s16x4, p), c, 0, 0, 0);
-  }
-  __device__ __forceinline__ static uint32_t pack(float lo, float hi) {
-    return (uint32_t)f32_to_bf16_bits(lo) | ((uint32_t)f32_to_bf16_bits(hi) << 16);
+  __device__ __forceinline__ static uint32_t pack(float lo, float hi) {  // v_cvt_pk_bf16_f32 (RNE)
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((pf_f32x2){lo, hi}, pf_bf16x2));
   }
 };
 template <> struct PrefillMfma<f16_t> {
-  __device__ __forceinline__ static pf_f32x4 qk(uint4 k, uint4 q, pf_f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(pf_f16x8, k),
-                                                  __builtin_bit_cast(pf_f16x8, q), c, 0, 0, 0);
-  }
-  __device__ __forceinline__ static pf_f32x4 pv(pf_s16x4 v, uint2 p, pf_f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(pf_f16x4, v),
-                                                 __builtin_bit_cast(pf_f16x4, p), c, 0, 0, 0);
+  __device__ __forceinline__ static pf_f32x16 mma(uint4 a, uint4 b, pf_f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(pf_f16x8, a),
+                                                  __builtin_bit_cast(pf_f16x8, b), c, 0, 0, 0);
   }
   __device__ __forceinline__ static uint32_t pack(float lo, float hi) {
-    return (uint32_t)f32_to_f16_bits(lo) | ((uint32_t)f32_to_f16_bits(hi) << 16);
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((pf_f32x2){lo, hi}, pf_f16x2));
   }
 };
 
 template <int D>
 struct PrefillCfg {
-  static constexpr int RB = D * 2;             // bytes per K/V row (16-bit elements)
-  static constexpr int KP = RB + 16;           // K LDS pitch: 16-byte reads of 8 rows hit 8 bank groups
-  static constexpr int VP = RB + 32;           // V LDS pitch: transpose reads of 4 rows hit 4 bank groups
-  static constexpr int KT = kPrefillBN * KP;   // bytes of one K tile
-  static constexpr int VT = kPrefillBN * VP;
-  static constexpr int BUF = KT + VT;
-  static constexpr int LDS = 2 * BUF;          // double buffered
-  static constexpr int CPR = RB / 16;          // 16-byte chunks per row
-  static constexpr int NLD = kPrefillBN * CPR / 256;  // 16-byte loads per thread per tile (K or V)
-  static constexpr int DC = D / 32;            // QK k-chunks
-  static constexpr int DB = D / 16;            // PV output dim blocks
+  static constexpr int RB = D * 2;                 // bytes per K/V row (16-bit elements)
+  static constexpr int CPR = RB / 16;              // 16-byte chunks per row
+  static constexpr int TILE = kPrefillBN * RB;     // bytes of one K (or V) tile
+  static constexpr int BUF = 2 * TILE;             // K tile then V tile
+  static constexpr int NLD = BUF / 1024 / 4;       // 1 KiB global_load_lds per wave per tile
+  static constexpr int KC = D / 16;                // QK k-steps (16 dims each)
+  static constexpr int DB = D / 32;                // PV output blocks (32 dims each)
+  // XOR swizzle of a row's 16-byte chunks (a permutation of 0..CPR-1 that depends on the row's
+  // low four bits). Chosen so that 16 consecutive rows at one logical chunk, and 4 consecutive
+  // rows x 64 logical bytes, land on distinct LDS banks.
+  __device__ __forceinline__ static int swz(int row) {
+    if constexpr (CPR == 16) return ((row & 3) << 2) | ((row >> 2) & 3);
+    else return (((row >> 1) & 1) << 2) | ((row >> 2) & 3);
+  }
 };
+
+__device__ __forceinline__ float max3f(float a, float b, float c) {
+  return __builtin_fmaxf(__builtin_fmaxf(a, b), c);
+}
+
+// Value of the lane's partner in the other half of the wave (lane ^ 32), via v_permlane32_swap.
+__device__ __forceinline__ void swap_halves(float x, float& a, float& b) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  a = __uint_as_float(r[0]);
+  b = __uint_as_float(r[1]);
+}
 
 template <typename T, int D, bool PAGED>
 __global__ void __launch_bounds__(256, 2) prefill_kernel(PrefillArgs a) {
   using C = PrefillCfg<D>;
-  constexpr int BN = kPrefillBN, KP = C::KP, VP = C::VP, DC = C::DC, DB = C::DB;
-  constexpr int CPR = C::CPR, NLD = C::NLD, RB = C::RB;
-  __shared__ __attribute__((aligned(16))) char smem[C::LDS];
+  using M = PrefillMfma<T>;
+  constexpr int BN = kPrefillBN, RB = C::RB, CPR = C::CPR, TILE = C::TILE, NLD = C::NLD;
+  constexpr int KC = C::KC, DB = C::DB;
+  static_assert(BN == 64, "the S^T layout below assumes two 32-key MFMA blocks per tile");
+  __shared__ __attribute__((aligned(1024))) char lds0[C::BUF];
+  __shared__ __attribute__((aligned(1024))) char lds1[C::BUF];
 
   // ---- workgroup -> (kv head, group member, sequence, query block), heavy query blocks first
   int id = blockIdx.x;
@@ -106,16 +124,17 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PrefillArgs a) {
     Lk = a.cu_k ? a.cu_k[seq + 1] - k_begin : a.lk;
   }
   const int pos_off = (a.causal == SP_CAUSAL_TOP_LEFT) ? 0 : Lk - Lq;
-  // keys any query of this workgroup can see
+  // keys any query of this workgroup can see: [kv_lo, kv_hi)
   int kv_lo = 0, kv_hi = Lk;
   if (a.causal != SP_CAUSAL_NONE) kv_hi = min(Lk, qe - 1 + pos_off + 1);
   if (a.window_left >= 0) kv_lo = max(0, qs + pos_off - a.window_left);
-  const int t_first = kv_lo > 0 ? (kv_lo / BN) * BN : 0;
+  const int t_first = (kv_lo / BN) * BN;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = wave_uniform(tid >> 6);
-  const int b = lane >> 4, i16 = lane & 15;
+  const int l32 = lane & 31, hh = lane >> 5;        // MFMA column (query) and half
+  const int i16 = lane & 15, g4 = lane >> 4;        // 16-lane group for the transpose reads
 
   // ---- per-sequence base addresses
   const char* qbase = (const char*)a.q +
@@ -136,190 +155,202 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PrefillArgs a) {
     vbase = (const char*)a.v + kv0 * 2;
   }
 
-  // ---- Q^T operand in registers: wave's queries qs + 32*wave + 16*qb + i16, dims 32c + 8b..+8
+  // ---- Q^T operand (B of the S^T MFMA): query wq0 + l32, dims 16c + 8hh .. +7
   const int wq0 = qs + 32 * wave;
-  uint4 qreg[2][DC];
+  const int my_q = wq0 + l32;
+  uint4 qreg[KC];
+  {
+    const char* qp = qbase + (int64_t)min(my_q, qe - 1) * a.q_tok * 2;
 #pragma unroll
-  for (int qb = 0; qb < 2; ++qb) {
-    const int qi = wq0 + 16 * qb + i16;
-    const char* qp = qbase + (int64_t)qi * a.q_tok * 2;
-#pragma unroll
-    for (int c = 0; c < DC; ++c)
-      qreg[qb][c] = qi < qe ? *(const uint4*)(qp + (32 * c + 8 * b) * 2) : make_uint4(0, 0, 0, 0);
+    for (int c = 0; c < KC; ++c)
+      qreg[c] = my_q < qe ? *(const uint4*)(qp + (16 * c + 8 * hh) * 2) : make_uint4(0, 0, 0, 0);
   }
 
-  // ---- cooperative tile loads (16-byte chunks, rows = keys)
-  uint4 kr[NLD], vr[NLD];
-  auto load_tile = [&](int t0) {
+  // ---- HBM -> LDS tile load: wave instruction g moves 1 KiB = 64 chunks; lane `lane` takes
+  // physical chunk p of row R and fetches the logical chunk that the swizzle puts there. Rows
+  // outside [kv_lo, kv_hi) read a valid row instead (their scores are masked).
+  auto issue_tile = [&](int t0, char* buf) {
 #pragma unroll
     for (int u = 0; u < NLD; ++u) {
-      const int idx = u * 256 + tid;
-      const int r = idx / CPR, c = idx % CPR;
-      const int j = t0 + r;
-      bool ok = j >= kv_lo && j < kv_hi;
-      const char* kp;
-      const char* vp;
+      const int g = wave * NLD + u;             // 0 .. BUF/1024 - 1 (K tiles first)
+      const bool is_v = g * 1024 >= TILE;
+      const int q = ((g * 1024) % TILE) / 16 + lane;
+      const int R = q / CPR, p = q % CPR;
+      const int c = p ^ C::swz(R);
+      const int j = min(max(t0 + R, kv_lo), kv_hi - 1);
+      const char* src;
       if constexpr (PAGED) {
-        const int blk = ok ? table[j / a.block_size] : 0;
-        ok = ok && blk >= 0 && blk < a.num_blocks;
-        const int64_t off = (int64_t)(ok ? blk : 0) * a.block_stride_b + head_off +
+        int blk = table[j / a.block_size];
+        blk = (blk >= 0 && blk < a.num_blocks) ? blk : 0;  // never dereference outside the pool
+        const int64_t off = (int64_t)blk * a.block_stride_b + head_off +
                             (int64_t)(j % a.block_size) * RB + c * 16;
-        kp = a.kpool + off;
-        vp = a.vpool + off;
+        src = (is_v ? a.vpool : a.kpool) + off;
       } else {
-        const int64_t off = (int64_t)j * a.kv_tok * 2 + c * 16;
-        kp = kbase + off;
-        vp = vbase + off;
+        src = (is_v ? vbase : kbase) + (int64_t)j * a.kv_tok * 2 + c * 16;
       }
-      kr[u] = ok ? *(const uint4*)kp : make_uint4(0, 0, 0, 0);
-      vr[u] = ok ? *(const uint4*)vp : make_uint4(0, 0, 0, 0);
-    }
-  };
-  auto store_tile = [&](int buf) {
-    char* kl = smem + buf * C::BUF;
-    char* vl = kl + C::KT;
-#pragma unroll
-    for (int u = 0; u < NLD; ++u) {
-      const int idx = u * 256 + tid;
-      const int r = idx / CPR, c = idx % CPR;
-      *(uint4*)(kl + r * KP + c * 16) = kr[u];
-      *(uint4*)(vl + r * VP + c * 16) = vr[u];
+      __builtin_amdgcn_global_load_lds((const void*)src, (lds_void*)(buf + g * 1024), 16, 0, 0);
     }
   };
 
-  float m_run[2] = {-INFINITY, -INFINITY}, l_run[2] = {0.f, 0.f};
-  pf_f32x4 acc[2][DB];
+  float m_run = -INFINITY, l_run = 0.f;
+  pf_f32x16 acc[DB];
 #pragma unroll
-  for (int qb = 0; qb < 2; ++qb)
+  for (int db = 0; db < DB; ++db)
 #pragma unroll
-    for (int db = 0; db < DB; ++db) acc[qb][db] = pf_f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int r = 0; r < 16; ++r) acc[db][r] = 0.f;
 
-  // query positions of this wave (for masking) and whether the wave has queries at all
-  const int wq_lo = wq0, wq_hi = min(wq0 + 32, qe) - 1;  // inclusive
+  const int wq_lo = wq0, wq_hi = min(wq0 + 32, qe) - 1;  // this wave's queries (inclusive)
   const bool wave_active = wq_lo < qe;
+  const int qpos = my_q + pos_off;
+  const float c2 = a.scale_log2;  // > 0 (checked on the host)
+  const int sw = C::swz(l32);     // swizzle of the K rows this lane reads (row & 15 == l32 & 15)
+
+  auto compute_tile = [&](int t0, const char* kl) {
+    const char* vl = kl + TILE;
+    // S^T = K Q^T: two 32-key blocks, interleaved so that consecutive MFMAs are independent;
+    // the K operands of step c+1 are read while the MFMAs of step c run.
+    pf_f32x16 s[2];
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s[mb][r] = 0.f;
+    const char* krow0 = kl + l32 * RB;
+    const char* krow1 = kl + (32 + l32) * RB;
+    uint4 k0 = *(const uint4*)(krow0 + 16 * (hh ^ sw));
+    uint4 k1 = *(const uint4*)(krow1 + 16 * (hh ^ sw));
+#pragma unroll
+    for (int c = 0; c < KC; ++c) {
+      uint4 n0 = k0, n1 = k1;
+      if (c + 1 < KC) {
+        n0 = *(const uint4*)(krow0 + 16 * ((2 * c + 2 + hh) ^ sw));
+        n1 = *(const uint4*)(krow1 + 16 * ((2 * c + 2 + hh) ^ sw));
+      }
+      s[0] = M::mma(k0, qreg[c], s[0]);
+      s[1] = M::mma(k1, qreg[c], s[1]);
+      k0 = n0;
+      k1 = n1;
+    }
+    // masks: only tiles that cross the sequence end, the window edge or the diagonal
+    bool need_mask = (t0 + BN > Lk) || (t0 < kv_lo);
+    if (a.causal != SP_CAUSAL_NONE) need_mask = need_mask || (t0 + BN - 1 > wq_lo + pos_off);
+    if (a.window_left >= 0) need_mask = need_mask || (t0 < wq_hi + pos_off - a.window_left);
+    if (need_mask) {
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int j = t0 + 32 * mb + (r >> 2) * 8 + hh * 4 + (r & 3);
+          bool ok = j < Lk && j >= kv_lo;
+          if (a.causal != SP_CAUSAL_NONE) ok = ok && j <= qpos;
+          if (a.window_left >= 0) ok = ok && j >= qpos - a.window_left;
+          s[mb][r] = ok ? s[mb][r] : -INFINITY;
+        }
+    }
+    // online softmax for query l32 (scores kept unscaled; the scale folds into the exponent)
+    float mx = -INFINITY;
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+      for (int r = 0; r < 16; r += 2) mx = max3f(mx, s[mb][r], s[mb][r + 1]);
+    {
+      float x0, x1;
+      swap_halves(mx, x0, x1);
+      mx = __builtin_fmaxf(x0, x1);
+    }
+    const float m_new = __builtin_fmaxf(m_run, mx * c2);
+    const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
+    const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
+    m_run = m_new;
+    uint4 pb[4];
+    float lsum = 0.f;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      float p[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        p[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[ks >> 1][(ks & 1) * 8 + e], c2, -m_use));
+        lsum += p[e];
+      }
+      pb[ks] = make_uint4(M::pack(p[0], p[1]), M::pack(p[2], p[3]), M::pack(p[4], p[5]),
+                          M::pack(p[6], p[7]));
+    }
+    l_run = __builtin_fmaf(l_run, alpha, lsum);
+    if (__any(alpha != 1.f)) {  // wave-uniform: skipped once the running maxima settle
+#pragma unroll
+      for (int db = 0; db < DB; ++db) acc[db] *= alpha;
+    }
+    // O^T += V^T P^T: K-step ks covers tile tokens 16ks .. 16ks+15 in the S^T order. Operand
+    // (ks, db) is read one MFMA ahead.
+    auto read_v = [&](int ks, int db) {
+      const int row0 = 16 * ks + (g4 >> 1) * 4 + (i16 >> 2);
+      const int colb = (db * 32 + (g4 & 1) * 16 + 4 * (i16 & 3)) * 2;
+      const int ch = colb >> 4, within = colb & 15;
+      const char* a0 = vl + row0 * RB + 16 * (ch ^ C::swz(row0)) + within;
+      const char* a1 = vl + (row0 + 8) * RB + 16 * (ch ^ C::swz(row0 + 8)) + within;
+      const pf_s16x4 v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(a0));
+      const pf_s16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(a1));
+      const uint2 w0 = __builtin_bit_cast(uint2, v0), w1 = __builtin_bit_cast(uint2, v1);
+      return make_uint4(w0.x, w0.y, w1.x, w1.y);
+    };
+    uint4 vop = read_v(0, 0);
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+#pragma unroll
+      for (int db = 0; db < DB; ++db) {
+        const int nks = db + 1 < DB ? ks : ks + 1, ndb = db + 1 < DB ? db + 1 : 0;
+        uint4 nxt = vop;
+        if (nks < 4) nxt = read_v(nks, ndb);
+        acc[db] = M::mma(vop, pb[ks], acc[db]);
+        vop = nxt;
+      }
+    }
+  };
+
+  // wave-uniform: does this wave see any key of the tile
+  auto visits = [&](int t0) {
+    bool v = wave_active;
+    if (a.causal != SP_CAUSAL_NONE) v = v && t0 <= wq_hi + pos_off;
+    if (a.window_left >= 0) v = v && t0 + BN - 1 >= wq_lo + pos_off - a.window_left;
+    return v;
+  };
+
+  // One pipeline step: wait for this tile's rows (own loads, then everyone's), start the next
+  // tile's loads into the other buffer, compute on this one. The barrier also guarantees every
+  // wave is done reading `nxt` (its previous tile) before the loads overwrite it.
+  auto step = [&](int t0, char* cur, char* nxt) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (t0 + BN < kv_hi) issue_tile(t0 + BN, nxt);
+    if (visits(t0)) compute_tile(t0, cur);
+  };
 
   int t0 = t_first;
-  if (t0 < kv_hi) {
-    load_tile(t0);
-    store_tile(0);
-    if (t0 + BN < kv_hi) load_tile(t0 + BN);
-  }
-  __syncthreads();
-
-  int buf = 0;
-  for (; t0 < kv_hi; t0 += BN, buf ^= 1) {
-    // wave-uniform: does this wave see any key of the tile, and does it need per-element masks
-    bool visit = wave_active;
-    bool need_mask = t0 + BN > Lk;
-    if (a.causal != SP_CAUSAL_NONE) {
-      visit = visit && t0 <= wq_hi + pos_off;
-      need_mask = need_mask || (t0 + BN - 1 > wq_lo + pos_off);
-    }
-    if (a.window_left >= 0) {
-      visit = visit && t0 + BN - 1 >= wq_lo + pos_off - a.window_left;
-      need_mask = need_mask || (t0 < wq_hi + pos_off - a.window_left);
-    }
-    if (visit) {
-      const char* kl = smem + buf * C::BUF;
-      char* vl = smem + buf * C::BUF + C::KT;
-      // S^T = K Q^T
-      pf_f32x4 s[4][2];
-#pragma unroll
-      for (int kb = 0; kb < 4; ++kb) {
-        s[kb][0] = pf_f32x4{0.f, 0.f, 0.f, 0.f};
-        s[kb][1] = pf_f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int c = 0; c < DC; ++c) {
-          const uint4 kop = *(const uint4*)(kl + (16 * kb + i16) * KP + (32 * c + 8 * b) * 2);
-          s[kb][0] = PrefillMfma<T>::qk(kop, qreg[0][c], s[kb][0]);
-          s[kb][1] = PrefillMfma<T>::qk(kop, qreg[1][c], s[kb][1]);
-        }
-      }
-      // online softmax per query column
-      uint2 pb[4][2];
-#pragma unroll
-      for (int qb = 0; qb < 2; ++qb) {
-        const int qpos = wq0 + 16 * qb + i16 + pos_off;
-        float mloc = -INFINITY;
-#pragma unroll
-        for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            float x = s[kb][qb][e] * a.scale_log2;
-            if (need_mask) {
-              const int j = t0 + 16 * kb + 4 * b + e;
-              bool ok = j < Lk && j >= kv_lo;
-              if (a.causal != SP_CAUSAL_NONE) ok = ok && j <= qpos;
-              if (a.window_left >= 0) ok = ok && j >= qpos - a.window_left;
-              x = ok ? x : -INFINITY;
-            }
-            s[kb][qb][e] = x;
-            mloc = fmaxf(mloc, x);
-          }
-        mloc = fmaxf(mloc, __shfl_xor(mloc, 16, 64));
-        mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
-        const float m_new = fmaxf(m_run[qb], mloc);
-        const float alpha = (m_run[qb] == -INFINITY) ? 0.f : exp2f(m_run[qb] - m_new);
-        const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
-        float lsum = 0.f;
-#pragma unroll
-        for (int kb = 0; kb < 4; ++kb) {
-          float p[4];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            p[e] = exp2f(s[kb][qb][e] - m_use);  // exp2(-inf) = 0 for masked keys
-            lsum += p[e];
-          }
-          pb[kb][qb] = make_uint2(PrefillMfma<T>::pack(p[0], p[1]), PrefillMfma<T>::pack(p[2], p[3]));
-        }
-        l_run[qb] = l_run[qb] * alpha + lsum;
-        m_run[qb] = m_new;
-        if (alpha != 1.f) {  // skipped wave-wide once the running max stops moving
-#pragma unroll
-          for (int db = 0; db < DB; ++db) acc[qb][db] *= alpha;
-        }
-      }
-      // O^T += V^T P^T, V^T through the LDS transpose read
-      const int vrow = 4 * b + (i16 >> 2), vcol = 4 * (i16 & 3);
-#pragma unroll
-      for (int kb = 0; kb < 4; ++kb) {
-#pragma unroll
-        for (int db = 0; db < DB; ++db) {
-          lds_s16x4* vptr = (lds_s16x4*)(vl + (16 * kb + vrow) * VP + (16 * db + vcol) * 2);
-          const pf_s16x4 vop = __builtin_amdgcn_ds_read_tr16_b64_v4i16(vptr);
-          acc[0][db] = PrefillMfma<T>::pv(vop, pb[kb][0], acc[0][db]);
-          acc[1][db] = PrefillMfma<T>::pv(vop, pb[kb][1], acc[1][db]);
-        }
-      }
-    }
-    // stage the next tile (loaded one step ahead) and fetch the one after
-    if (t0 + BN < kv_hi) {
-      store_tile(buf ^ 1);
-      if (t0 + 2 * BN < kv_hi) load_tile(t0 + 2 * BN);
-    }
-    __syncthreads();
+  if (t0 < kv_hi) issue_tile(t0, lds0);
+  while (t0 < kv_hi) {
+    step(t0, lds0, lds1);
+    t0 += BN;
+    if (t0 >= kv_hi) break;
+    step(t0, lds1, lds0);
+    t0 += BN;
   }
 
-  // ---- normalise and store: lane (b, i16) holds O^T[16db + 4b + e][query 16qb + i16]
+  // ---- normalise and store: lane holds O^T[d][query l32], d = 32db + 8(r/4) + 4hh + r%4
+  float x0, x1;
+  swap_halves(l_run, x0, x1);
+  const float l = x0 + x1;
+  if (my_q >= qe) return;
+  const float inv = l > 0.f ? 1.f / l : 0.f;
+  char* op = obase + (int64_t)my_q * a.o_tok * 2;
 #pragma unroll
-  for (int qb = 0; qb < 2; ++qb) {
-    float l = l_run[qb];
-    l += __shfl_xor(l, 16, 64);
-    l += __shfl_xor(l, 32, 64);
-    const int qi = wq0 + 16 * qb + i16;
-    if (qi >= qe) continue;
-    const float inv = l > 0.f ? 1.f / l : 0.f;
-    char* op = obase + (int64_t)qi * a.o_tok * 2;
+  for (int db = 0; db < DB; ++db)
 #pragma unroll
-    for (int db = 0; db < DB; ++db) {
+    for (int rg = 0; rg < 4; ++rg) {
+      const int d0 = db * 32 + rg * 8 + hh * 4;
       uint2 w;
-      if constexpr (sizeof(T) == 2) {
-        w.x = PrefillMfma<T>::pack(acc[qb][db][0] * inv, acc[qb][db][1] * inv);
-        w.y = PrefillMfma<T>::pack(acc[qb][db][2] * inv, acc[qb][db][3] * inv);
-      }
-      *(uint2*)(op + (16 * db + 4 * b) * 2) = w;
+      w.x = M::pack(acc[db][rg * 4 + 0] * inv, acc[db][rg * 4 + 1] * inv);
+      w.y = M::pack(acc[db][rg * 4 + 2] * inv, acc[db][rg * 4 + 3] * inv);
+      *(uint2*)(op + d0 * 2) = w;
     }
-  }
 }
 
 template <typename T, int D>
