@@ -48,6 +48,8 @@ def parse_args():
                     help="approximate CPU time budget of the cpu_baseline leg")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run 10 plain 512 MiB device-to-device copies and exit")
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="only the C3 prefill leg (profiling); prints its JSON object")
     ap.add_argument("--no-prefill", action="store_true",
                     help="skip the C3 ragged-prefill leg")
     ap.add_argument("--secondary", action="store_true",
@@ -293,6 +295,10 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         print(json.dumps({"calibrate_copy_bytes": src.numel(), "copies": 10}), flush=True)
+        return
+    if args.prefill_only:
+        _, pf = time_prefill_c3(args.steps, args.warmup)
+        print(json.dumps({"prefill": pf}), flush=True)
         return
     w = W.DECODE_CONFIGS[args.config]()
     r = time_decode_config(w, args.steps, args.warmup)

@@ -38,6 +38,7 @@ typedef _Float16 pf_f16x2 __attribute__((ext_vector_type(2)));
 typedef float pf_f32x2 __attribute__((ext_vector_type(2)));
 typedef float pf_f32x16 __attribute__((ext_vector_type(16)));
 typedef short pf_s16x4 __attribute__((ext_vector_type(4)));
+typedef short pf_s16x8 __attribute__((ext_vector_type(8)));
 typedef __attribute__((address_space(3))) pf_s16x4 lds_s16x4;
 typedef __attribute__((address_space(3))) void lds_void;
 
@@ -47,12 +48,20 @@ template <> struct PrefillMfma<bf16_t> {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(pf_bf16x8, a),
                                                    __builtin_bit_cast(pf_bf16x8, b), c, 0, 0, 0);
   }
+  __device__ __forceinline__ static pf_f32x16 mma(pf_s16x8 a, uint4 b, pf_f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(pf_bf16x8, a),
+                                                   __builtin_bit_cast(pf_bf16x8, b), c, 0, 0, 0);
+  }
   __device__ __forceinline__ static uint32_t pack(float lo, float hi) {  // v_cvt_pk_bf16_f32 (RNE)
     return __builtin_bit_cast(uint32_t, __builtin_convertvector((pf_f32x2){lo, hi}, pf_bf16x2));
   }
 };
 template <> struct PrefillMfma<f16_t> {
   __device__ __forceinline__ static pf_f32x16 mma(uint4 a, uint4 b, pf_f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(pf_f16x8, a),
+                                                  __builtin_bit_cast(pf_f16x8, b), c, 0, 0, 0);
+  }
+  __device__ __forceinline__ static pf_f32x16 mma(pf_s16x8 a, uint4 b, pf_f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(pf_f16x8, a),
                                                   __builtin_bit_cast(pf_f16x8, b), c, 0, 0, 0);
   }
@@ -89,6 +98,24 @@ __device__ __forceinline__ void swap_halves(float x, float& a, float& b) {
                                                   false);
   a = __uint_as_float(r[0]);
   b = __uint_as_float(r[1]);
+}
+
+// s_waitcnt vmcnt(0) expcnt(7) lgkmcnt(15): wait for every outstanding vector memory access of
+// this wave (gfx9 encoding: vmcnt in bits [3:0] and [15:14], expcnt [6:4], lgkmcnt [11:8]).
+constexpr int kWaitVmcnt0 = 0x0F70;
+
+// global_load_lds_dwordx4: every lane copies 16 bytes from `src` to LDS at lds_dst + 16 * lane
+// (lds_dst wave-uniform). Issued through inline asm so that the compiler does not guard the
+// LDS reads of the other buffer with waits on these loads; completion is awaited explicitly
+// (s_waitcnt vmcnt(0) + barrier) before the tile is read.
+__device__ __forceinline__ void lds_dma16(const char* src, char* lds_dst) {
+  const unsigned m0 = (unsigned)(uintptr_t)(lds_void*)lds_dst;
+  asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(m0) : "memory");
+}
+// Same with a wave-uniform base (SGPR pair) and a 32-bit per-lane byte offset.
+__device__ __forceinline__ void lds_dma16_s(const char* sbase, int voff, char* lds_dst) {
+  const unsigned m0 = (unsigned)(uintptr_t)(lds_void*)lds_dst;
+  asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "{m0}"(m0) : "memory");
 }
 
 template <typename T, int D, bool PAGED>
@@ -166,10 +193,62 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PrefillArgs a) {
       qreg[c] = my_q < qe ? *(const uint4*)(qp + (16 * c + 8 * hh) * 2) : make_uint4(0, 0, 0, 0);
   }
 
-  // ---- HBM -> LDS tile load: wave instruction g moves 1 KiB = 64 chunks; lane `lane` takes
-  // physical chunk p of row R and fetches the logical chunk that the swizzle puts there. Rows
-  // outside [kv_lo, kv_hi) read a valid row instead (their scores are masked).
-  auto issue_tile = [&](int t0, char* buf) {
+  // ---- HBM -> LDS tile load: wave instruction g moves 1 KiB = RPI rows; lane `lane` takes
+  // physical chunk p of row R and fetches the logical chunk that the swizzle puts there.
+  // Interior tiles (every row inside [kv_lo, kv_hi)) take the fast path: the row group of each
+  // instruction is wave-uniform, so its base address is scalar and the lane part is a constant
+  // offset computed once here. Edge tiles clamp rows outside [kv_lo, kv_hi) to a valid row
+  // (their scores are masked) and compute per-lane addresses.
+  constexpr int RPI = 64 / CPR;  // rows per 1 KiB load
+  const int64_t row_pitch = PAGED ? (int64_t)RB : (int64_t)a.kv_tok * 2;
+  int voff[NLD];                  // lane part of each load's source offset (bytes)
+#pragma unroll
+  for (int u = 0; u < NLD; ++u) {
+    const int g = wave * NLD + u;
+    const int R = ((g * 1024) % TILE) / RB + lane / CPR;
+    voff[u] = (int)((lane / CPR) * row_pitch) + 16 * ((lane % CPR) ^ C::swz(R));
+  }
+  // Paged fast path: one block-table entry per load, fetched one tile ahead.
+  const bool paged_fast = PAGED && (a.block_size % RPI == 0);
+  int nblk[NLD];
+#pragma unroll
+  for (int u = 0; u < NLD; ++u) nblk[u] = 0;
+  auto tile_interior = [&](int t0) __attribute__((always_inline)) {
+    return t0 >= kv_lo && t0 + BN <= kv_hi;
+  };
+  // block ids of tile t0's row groups (paged fast path)
+  auto fetch_blocks = [&](int t0) __attribute__((always_inline)) {
+    if constexpr (PAGED) {
+      if (paged_fast && t0 < kv_hi && tile_interior(t0)) {
+#pragma unroll
+        for (int u = 0; u < NLD; ++u) {
+          const int g = wave * NLD + u;
+          const int row0 = t0 + ((g * 1024) % TILE) / RB;
+          nblk[u] = table[row0 / a.block_size];
+        }
+      }
+    }
+  };
+  auto issue_tile = [&](int t0, char* buf) __attribute__((always_inline)) {
+    if (tile_interior(t0) && (!PAGED || paged_fast)) {
+#pragma unroll
+      for (int u = 0; u < NLD; ++u) {
+        const int g = wave * NLD + u;
+        const bool is_v = g * 1024 >= TILE;
+        const int row0 = t0 + ((g * 1024) % TILE) / RB;
+        const char* sb;
+        if constexpr (PAGED) {
+          int blk = __builtin_amdgcn_readfirstlane(nblk[u]);
+          blk = (blk >= 0 && blk < a.num_blocks) ? blk : 0;  // never outside the pool
+          sb = (is_v ? a.vpool : a.kpool) + (int64_t)blk * a.block_stride_b + head_off +
+               (int64_t)(row0 % a.block_size) * RB;
+        } else {
+          sb = (is_v ? vbase : kbase) + (int64_t)row0 * row_pitch;
+        }
+        lds_dma16_s(sb, voff[u], buf + g * 1024);
+      }
+      return;
+    }
 #pragma unroll
     for (int u = 0; u < NLD; ++u) {
       const int g = wave * NLD + u;             // 0 .. BUF/1024 - 1 (K tiles first)
@@ -188,10 +267,9 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PrefillArgs a) {
       } else {
         src = (is_v ? vbase : kbase) + (int64_t)j * a.kv_tok * 2 + c * 16;
       }
-      __builtin_amdgcn_global_load_lds((const void*)src, (lds_void*)(buf + g * 1024), 16, 0, 0);
+      lds_dma16(src, buf + g * 1024);
     }
   };
-
   float m_run = -INFINITY, l_run = 0.f;
   pf_f32x16 acc[DB];
 #pragma unroll
@@ -205,7 +283,7 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PrefillArgs a) {
   const float c2 = a.scale_log2;  // > 0 (checked on the host)
   const int sw = C::swz(l32);     // swizzle of the K rows this lane reads (row & 15 == l32 & 15)
 
-  auto compute_tile = [&](int t0, const char* kl) {
+  auto compute_tile = [&](int t0, const char* kl) __attribute__((always_inline)) {
     const char* vl = kl + TILE;
     // S^T = K Q^T: two 32-key blocks, interleaved so that consecutive MFMAs are independent;
     // the K operands of step c+1 are read while the MFMAs of step c run.
@@ -230,58 +308,74 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PrefillArgs a) {
       k0 = n0;
       k1 = n1;
     }
-    // masks: only tiles that cross the sequence end, the window edge or the diagonal
+    // masks: only tiles that cross the sequence end, the window edge or the diagonal. Score
+    // (mb, r) of this lane is key t0 + 4hh + off with off = 32mb + 8(r/4) + r%4; it is visible
+    // iff lo <= key <= hi, tested as a compile-time offset against two per-lane bounds.
     bool need_mask = (t0 + BN > Lk) || (t0 < kv_lo);
     if (a.causal != SP_CAUSAL_NONE) need_mask = need_mask || (t0 + BN - 1 > wq_lo + pos_off);
     if (a.window_left >= 0) need_mask = need_mask || (t0 < wq_hi + pos_off - a.window_left);
-    if (need_mask) {
+    if (__builtin_amdgcn_readfirstlane((int)need_mask)) {
+      int lo = kv_lo, hi = Lk - 1;
+      if (a.causal != SP_CAUSAL_NONE) hi = min(hi, qpos);
+      if (a.window_left >= 0) lo = max(lo, qpos - a.window_left);
+      const int jb = t0 + 4 * hh;
+      const int olo = lo - jb, ohi = hi - jb;
 #pragma unroll
       for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const int j = t0 + 32 * mb + (r >> 2) * 8 + hh * 4 + (r & 3);
-          bool ok = j < Lk && j >= kv_lo;
-          if (a.causal != SP_CAUSAL_NONE) ok = ok && j <= qpos;
-          if (a.window_left >= 0) ok = ok && j >= qpos - a.window_left;
-          s[mb][r] = ok ? s[mb][r] : -INFINITY;
+          const int off = 32 * mb + (r >> 2) * 8 + (r & 3);
+          s[mb][r] = (off >= olo && off <= ohi) ? s[mb][r] : -INFINITY;
         }
     }
-    // online softmax for query l32 (scores kept unscaled; the scale folds into the exponent)
-    float mx = -INFINITY;
+    // online softmax for query l32. Scores stay unscaled (the scale folds into the exponent).
+    // The running maximum is only raised when the tile's maximum exceeds it by more than
+    // 2^kLazy (lazy rescaling): until then p = 2^(s*c - m) <= 2^kLazy, exact in fp32 and within
+    // bf16 range, and the accumulator rescale is skipped.
+    float mx;
+    {
+      float mq[4];
 #pragma unroll
-    for (int mb = 0; mb < 2; ++mb)
+      for (int k = 0; k < 4; ++k) {  // four independent max3 chains over 8 scores each
+        const int mb = k >> 1, r0 = (k & 1) * 8;
+        float x = __builtin_fmaxf(s[mb][r0], s[mb][r0 + 1]);
 #pragma unroll
-      for (int r = 0; r < 16; r += 2) mx = max3f(mx, s[mb][r], s[mb][r + 1]);
+        for (int r = r0 + 2; r < r0 + 8; r += 2) x = max3f(x, s[mb][r], s[mb][r + 1]);
+        mq[k] = x;
+      }
+      mx = __builtin_fmaxf(max3f(mq[0], mq[1], mq[2]), mq[3]);
+    }
     {
       float x0, x1;
       swap_halves(mx, x0, x1);
-      mx = __builtin_fmaxf(x0, x1);
+      mx = __builtin_fmaxf(x0, x1) * c2;
     }
-    const float m_new = __builtin_fmaxf(m_run, mx * c2);
-    const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
-    const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
-    m_run = m_new;
+    constexpr float kLazy = 8.f;
+    if (__any(mx > m_run + kLazy)) {
+      const float m_new = __builtin_fmaxf(m_run, mx);
+      const float alpha = __builtin_amdgcn_exp2f(m_run - (m_new == -INFINITY ? 0.f : m_new));
+      m_run = m_new;
+      l_run *= alpha;
+#pragma unroll
+      for (int db = 0; db < DB; ++db) acc[db] *= alpha;
+    }
+    const float m_use = (m_run == -INFINITY) ? 0.f : m_run;
     uint4 pb[4];
-    float lsum = 0.f;
+    float ls[4];
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
       float p[8];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
+      for (int e = 0; e < 8; ++e)
         p[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[ks >> 1][(ks & 1) * 8 + e], c2, -m_use));
-        lsum += p[e];
-      }
+      ls[ks] = ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
       pb[ks] = make_uint4(M::pack(p[0], p[1]), M::pack(p[2], p[3]), M::pack(p[4], p[5]),
                           M::pack(p[6], p[7]));
     }
-    l_run = __builtin_fmaf(l_run, alpha, lsum);
-    if (__any(alpha != 1.f)) {  // wave-uniform: skipped once the running maxima settle
-#pragma unroll
-      for (int db = 0; db < DB; ++db) acc[db] *= alpha;
-    }
+    l_run += (ls[0] + ls[1]) + (ls[2] + ls[3]);
     // O^T += V^T P^T: K-step ks covers tile tokens 16ks .. 16ks+15 in the S^T order. Operand
     // (ks, db) is read one MFMA ahead.
-    auto read_v = [&](int ks, int db) {
+    auto read_v = [&](int ks, int db) __attribute__((always_inline)) {
       const int row0 = 16 * ks + (g4 >> 1) * 4 + (i16 >> 2);
       const int colb = (db * 32 + (g4 & 1) * 16 + 4 * (i16 & 3)) * 2;
       const int ch = colb >> 4, within = colb & 15;
@@ -289,16 +383,15 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PrefillArgs a) {
       const char* a1 = vl + (row0 + 8) * RB + 16 * (ch ^ C::swz(row0 + 8)) + within;
       const pf_s16x4 v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(a0));
       const pf_s16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(a1));
-      const uint2 w0 = __builtin_bit_cast(uint2, v0), w1 = __builtin_bit_cast(uint2, v1);
-      return make_uint4(w0.x, w0.y, w1.x, w1.y);
+      return __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7);
     };
-    uint4 vop = read_v(0, 0);
+    pf_s16x8 vop = read_v(0, 0);
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
 #pragma unroll
       for (int db = 0; db < DB; ++db) {
         const int nks = db + 1 < DB ? ks : ks + 1, ndb = db + 1 < DB ? db + 1 : 0;
-        uint4 nxt = vop;
+        pf_s16x8 nxt = vop;
         if (nks < 4) nxt = read_v(nks, ndb);
         acc[db] = M::mma(vop, pb[ks], acc[db]);
         vop = nxt;
@@ -307,7 +400,7 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PrefillArgs a) {
   };
 
   // wave-uniform: does this wave see any key of the tile
-  auto visits = [&](int t0) {
+  auto visits = [&](int t0) __attribute__((always_inline)) {
     bool v = wave_active;
     if (a.causal != SP_CAUSAL_NONE) v = v && t0 <= wq_hi + pos_off;
     if (a.window_left >= 0) v = v && t0 + BN - 1 >= wq_lo + pos_off - a.window_left;
@@ -317,15 +410,29 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PrefillArgs a) {
   // One pipeline step: wait for this tile's rows (own loads, then everyone's), start the next
   // tile's loads into the other buffer, compute on this one. The barrier also guarantees every
   // wave is done reading `nxt` (its previous tile) before the loads overwrite it.
-  auto step = [&](int t0, char* cur, char* nxt) {
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  auto step = [&](int t0, char* cur, char* nxt) __attribute__((always_inline)) {
+    __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
     __syncthreads();
-    if (t0 + BN < kv_hi) issue_tile(t0 + BN, nxt);
+    if (t0 + BN < kv_hi) {
+      issue_tile(t0 + BN, nxt);
+      fetch_blocks(t0 + 2 * BN);
+    }
     if (visits(t0)) compute_tile(t0, cur);
   };
 
+  // Prologue: the first tile's loads go out while the Q loads are still in flight. The wait
+  // below covers both, so no wait inside the key loop refers to Q (the tile loads issued there
+  // are awaited explicitly).
   int t0 = t_first;
-  if (t0 < kv_hi) issue_tile(t0, lds0);
+  if (t0 < kv_hi) {
+    if constexpr (PAGED) {
+      fetch_blocks(t0);
+      __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+    }
+    issue_tile(t0, lds0);
+    fetch_blocks(t0 + BN);
+  }
+  __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
   while (t0 < kv_hi) {
     step(t0, lds0, lds1);
     t0 += BN;
