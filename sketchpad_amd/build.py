@@ -91,7 +91,7 @@ def build_host(jobs: int = 8) -> Path | None:
         exe.parent.mkdir(parents=True, exist_ok=True)
         _run([HIPCC, *DEVICE_FLAGS, f"-I{HOST}", "-x", "hip", str(test_src), "-o", str(exe),
               f"-L{LIBDIR}", "-lsketchpad_host", "-lsketchpad_attn",
-              f"-Wl,-rpath,{LIBDIR}"])
+              "-Wl,-rpath,$ORIGIN/../../../sketchpad_amd/lib"])
     return out
 
 

@@ -287,3 +287,65 @@ def test_paged_decode_reference_equals_dense():
         kg, vg = N.gather_kv(k_pool, v_pool, 0, tables[s], L, bs)
         ref = N.attention(q[s:s + 1], kg.transpose(1, 0, 2), vg.transpose(1, 0, 2), 0.2)
         np.testing.assert_allclose(got[s], ref[0], atol=1e-12)
+
+
+# ---------------------------------------------------------------------------------------------
+# the timed CPU baselines (bench.py's cpu_baseline legs) compute the same thing as the oracle
+# ---------------------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("window", [-1, 20])
+def test_cpu_decode_baseline_matches_oracle(window):
+    """spo_cpu_decode_baseline = store the step's token (store_kv) + gather + repeat_kv +
+    softmax((q k^T) * scale) v, in f32: within f32 rounding of the f64 oracle, and the append
+    lands exactly where the slot mapping says."""
+    rng = np.random.default_rng(29)
+    nb, hkv, bs, d, hq = 48, 2, 16, 64, 8
+    lens = np.array([1, 16, 17, 129, 250], np.int32)
+    perm = rng.permutation(nb).astype(np.int32)
+    tables, off = np.full((5, 16), -1, np.int32), 0
+    for s, L in enumerate(lens):
+        n = -(-L // bs)
+        tables[s, :n] = perm[off:off + n]
+        off += n
+    k_pool = _rand(rng, nb, 1, hkv, bs, d).astype(np.float32)
+    v_pool = _rand(rng, nb, 1, hkv, bs, d).astype(np.float32)
+    q = _rand(rng, 5, hq, d).astype(np.float32)
+    kn = _rand(rng, 5, hkv, d).astype(np.float32)
+    vn = _rand(rng, 5, hkv, d).astype(np.float32)
+    lay = _layout(nb, 1, 0, hkv, bs, d)
+    out = np.zeros_like(q)
+    kp, vp = k_pool.copy(), v_pool.copy()
+    O.cpu_decode_baseline(out, q, kn, vn, kp, vp, lay, tables, lens, scale=d ** -0.5,
+                          window_left=window, threads=2)
+    # the appended row of every sequence is bit-exact, everything else untouched
+    kp_ref, vp_ref = k_pool.copy(), v_pool.copy()
+    for s, L in enumerate(lens):
+        blk, slot = tables[s, (L - 1) // bs], (L - 1) % bs
+        kp_ref[blk, 0, :, slot] = kn[s]
+        vp_ref[blk, 0, :, slot] = vn[s]
+    np.testing.assert_array_equal(kp, kp_ref)
+    np.testing.assert_array_equal(vp, vp_ref)
+    ref = O.paged_decode_f64(q, kp_ref, vp_ref, lay, tables, lens, scale=d ** -0.5,
+                             window_left=window)
+    err = np.abs(out - ref).max(axis=-1) / np.abs(ref).max(axis=-1)
+    assert err.max() < 1e-5
+
+
+def test_cpu_prefill_baseline_matches_oracle():
+    """spo_cpu_prefill_baseline = per sequence repeat_kv + [Hq, L, L] scores + causal mask +
+    softmax + matmul in f32: within f32 rounding of the f64 oracle."""
+    rng = np.random.default_rng(31)
+    hq, hkv, d = 8, 2, 32
+    lens = [1, 7, 40, 65]
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    T = int(cu[-1])
+    q = _rand(rng, T, hq, d).astype(np.float32)
+    k = _rand(rng, T, hkv, d).astype(np.float32)
+    v = _rand(rng, T, hkv, d).astype(np.float32)
+    out = np.zeros_like(q)
+    O.cpu_prefill_baseline(out, q, k, v, cu, hq=hq, hkv=hkv, d=d, scale=d ** -0.5, threads=2)
+    for s in range(len(lens)):
+        a, b = cu[s], cu[s + 1]
+        ref = O.attention_f64(q[a:b], k[a:b], v[a:b], scale=d ** -0.5, causal=True, q_pos0=0)
+        err = np.abs(out[a:b] - ref).max(axis=-1) / np.abs(ref).max(axis=-1)
+        assert err.max() < 1e-5, s
