@@ -69,6 +69,20 @@ __device__ __forceinline__ f32x4_v mfma_f32(float a, float b, f32x4_v c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
+// Value held by lane ^ 16 / lane ^ 32. v_permlane16_swap(x, x) returns (x[l & ~16], x[l | 16])
+// and v_permlane32_swap(x, x) returns (x[l & ~32], x[l | 32]); the partner is the one that is not
+// the lane's own value.
+__device__ __forceinline__ float xor16(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return __uint_as_float((__lane_id() & 16) ? r[0] : r[1]);
+}
+__device__ __forceinline__ float xor32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return __uint_as_float((__lane_id() & 32) ? r[0] : r[1]);
+}
+
 template <typename T, int D>
 struct DecodeCfg {
   static constexpr int ES = Elem<T>::bytes;
@@ -129,16 +143,28 @@ __global__ void __launch_bounds__(64 * kDecodeWaves, decode_min_waves<T>())
     const bool real = n < G;
     const char* qp = (const char*)a.q + ((int64_t)seq * a.hq + kvh * G + (real ? n : 0)) * RB;
 #pragma unroll
-    for (int c = 0; c < NL; ++c)
-      qv[c] = real ? *(const uint4*)(qp + c * 64 + g * 16) : make_uint4(0, 0, 0, 0);
+    for (int c = 0; c < NL; ++c) {
+      const uint4 x = *(const uint4*)(qp + c * 64 + g * 16);  // padding heads read head 0
+      qv[c] = real ? x : make_uint4(0, 0, 0, 0);
+    }
   }
 
   const int32_t* table = a.block_tables + (int64_t)seq * a.max_blocks_per_seq;
   const int64_t head_off = a.layer_off_b + (int64_t)kvh * a.block_size * RB;
   char* vst = smem + wave * C::WAVE_LDS;
 
+  // Block ids of this split's tiles, fetched once up front: lane j holds the block of tile
+  // t_begin + j (tps <= 64), so no tile load waits on a dependent block-table read.
+  int my_blk = 0;
+  {
+    const int tj = t_begin + lane;
+    if (lane < t_end - t_begin) my_blk = table[(tj * kTile) / a.block_size];
+  }
+
   // Tile loads. K in MFMA A-operand order (token n, 16 bytes at c*64 + g*16); V coalesced
-  // (lane-linear 16-byte chunks of the contiguous 16 x RB tile).
+  // (lane-linear 16-byte chunks of the contiguous 16 x RB tile). Rows outside [start_tok, L)
+  // read a valid row of the same tile instead (their scores are masked to -inf, so their
+  // values are weighted by 0); a block id outside the pool reads block 0 and masks the tile.
   // K/V are streamed once: nontemporal loads keep them from displacing reusable L2 lines.
   typedef unsigned u32x4_v __attribute__((ext_vector_type(4)));
   auto ldnt = [](const char* p) {
@@ -146,21 +172,20 @@ __global__ void __launch_bounds__(64 * kDecodeWaves, decode_min_waves<T>())
   };
   auto load_tile = [&](int t, uint4* kr, uint4* vr, bool& ok) {
     const int pos0 = t * kTile;
-    const int blk = table[pos0 / a.block_size];
+    const int blk = __builtin_amdgcn_readlane(my_blk, t - t_begin);
     ok = blk >= 0 && blk < a.num_blocks;
     const int64_t base = (int64_t)(ok ? blk : 0) * a.block_stride_b + head_off +
                          (int64_t)(pos0 % a.block_size) * RB;
-    const int kpos = pos0 + n;
-    const bool kval = ok && kpos >= start_tok && kpos < L;
+    const int rlo = max(start_tok - pos0, 0), rhi = min(L - pos0, kTile) - 1;  // valid rows
+    const int kr_row = min(max(n, rlo), rhi);
 #pragma unroll
-    for (int c = 0; c < NL; ++c)
-      kr[c] = kval ? ldnt(a.kpool + base + n * RB + c * 64 + g * 16) : make_uint4(0, 0, 0, 0);
+    for (int c = 0; c < NL; ++c) kr[c] = ldnt(a.kpool + base + kr_row * RB + c * 64 + g * 16);
 #pragma unroll
     for (int i = 0; i < NL; ++i) {
       const int off = (i * 64 + lane) * 16;
-      const int vpos = pos0 + off / RB;
-      vr[i] = (ok && vpos >= start_tok && vpos < L) ? ldnt(a.vpool + base + off)
-                                                    : make_uint4(0, 0, 0, 0);
+      const int row = off / RB;
+      const int vrow = min(max(row, rlo), rhi);
+      vr[i] = ldnt(a.vpool + base + vrow * RB + off % RB);
     }
   };
 
@@ -211,13 +236,14 @@ __global__ void __launch_bounds__(64 * kDecodeWaves, decode_min_waves<T>())
       sv[j] = valid ? s[j] * a.scale_log2 : -INFINITY;
     }
     float mt = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
-    mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
-    mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+    mt = fmaxf(mt, xor16(mt));
+    mt = fmaxf(mt, xor32(mt));
     const float m_new = fmaxf(m_run, mt);
-    const float alpha = (m_run == -INFINITY) ? 0.f : exp2f(m_run - m_new);
+    const float alpha = (m_run == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m_run - m_new);
     float p[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) p[j] = (sv[j] == -INFINITY) ? 0.f : exp2f(sv[j] - m_new);
+    for (int j = 0; j < 4; ++j)
+      p[j] = (sv[j] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(sv[j] - m_new);
     l_run = l_run * alpha + ((p[0] + p[1]) + (p[2] + p[3]));
     m_run = m_new;
 #pragma unroll
@@ -251,8 +277,8 @@ __global__ void __launch_bounds__(64 * kDecodeWaves, decode_min_waves<T>())
   }
 
   // Per-head sums over the four token groups of the wave, then merge the four waves in LDS.
-  l_run += __shfl_xor(l_run, 16, 64);
-  l_run += __shfl_xor(l_run, 32, 64);
+  l_run += xor16(l_run);
+  l_run += xor32(l_run);
   __syncthreads();
   float* cm = (float*)smem;             // [waves][16]
   float* cl = cm + kDecodeWaves * 16;   // [waves][16]
@@ -365,10 +391,10 @@ DecodePlan plan_decode(int num_seqs, int hq, int hkv, int head_dim, int max_cont
     if (wt < max_tiles) max_tiles = wt;
   }
   p.max_tiles = max_tiles < 1 ? 1 : max_tiles;
-  int tps = 24;  // 384 tokens per split, 6 tiles per wave
+  int tps = 32;  // 512 tokens per split, 8 tiles per wave
   const char* env = getenv("SP_DECODE_TPS");
   if (env && atoi(env) > 0) {
-    tps = atoi(env);
+    tps = atoi(env) < kDecodeWaves ? kDecodeWaves : (atoi(env) > 64 ? 64 : atoi(env));
   } else {
     const int64_t units = (int64_t)num_seqs * (hkv > 0 ? hkv : 1);
     while (tps > kDecodeWaves && units * ((p.max_tiles + tps - 1) / tps) < 2048)
