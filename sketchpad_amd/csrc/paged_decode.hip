@@ -89,12 +89,22 @@ struct DecodeCfg {
   static constexpr bool kF32 = (ES == 4);
   static constexpr int RB = D * ES;                    // bytes per K/V row
   static constexpr int NL = RB / 64;                   // 16-byte loads per lane per tile (K or V)
-  static constexpr int VP = RB + (kF32 ? 16 : 8);      // V staging pitch (4-row stride hits new banks)
-  static constexpr int WAVE_LDS = kTile * VP;
+  static constexpr int VP = RB + (kF32 ? 16 : 0);      // f32: V staging pitch (new banks per row)
+  // 16-bit: K and V stages of 16 rows each, 16-byte chunks XOR-swizzled per row (swz below);
+  // f32: a padded V stage only (K is read from HBM straight into the MFMA operand).
+  static constexpr int WAVE_LDS = kF32 ? kTile * VP : 2 * kTile * RB;
+  static constexpr int CPR = RB / 16;                  // 16-byte chunks per row
   static constexpr int ND = D / 16;                    // 16-dim output blocks
   static constexpr int MERGE_LDS = kDecodeWaves * (2 * 16 + 16 * D) * 4;
   static constexpr int LDS = (kDecodeWaves * WAVE_LDS > MERGE_LDS) ? kDecodeWaves * WAVE_LDS : MERGE_LDS;
+  // Chunk swizzle of the 16-bit stages: the K operand read (16 rows at one logical chunk) and
+  // the V transpose read (8 consecutive rows x 32 bytes per 32 lanes) hit distinct banks.
+  __device__ __forceinline__ static int swz(int row) {
+    if constexpr (CPR == 16) return ((row & 7) << 1) | ((row >> 3) & 1);
+    else return (((row >> 1) & 3) << 1) | ((row >> 3) & 1);
+  }
 };
+typedef __attribute__((address_space(3))) s16x4_v lds_s16x4_v;
 
 // 16-bit kernels fit four waves per SIMD (<= 128 VGPRs, no spills); f32 D=128 would spill.
 template <typename T>
@@ -177,15 +187,18 @@ __global__ void __launch_bounds__(64 * kDecodeWaves, decode_min_waves<T>())
     const int64_t base = (int64_t)(ok ? blk : 0) * a.block_stride_b + head_off +
                          (int64_t)(pos0 % a.block_size) * RB;
     const int rlo = max(start_tok - pos0, 0), rhi = min(L - pos0, kTile) - 1;  // valid rows
-    const int kr_row = min(max(n, rlo), rhi);
+    if constexpr (kF32) {
+      const int kr_row = min(max(n, rlo), rhi);
 #pragma unroll
-    for (int c = 0; c < NL; ++c) kr[c] = ldnt(a.kpool + base + kr_row * RB + c * 64 + g * 16);
+      for (int c = 0; c < NL; ++c) kr[c] = ldnt(a.kpool + base + kr_row * RB + c * 64 + g * 16);
+    }
 #pragma unroll
     for (int i = 0; i < NL; ++i) {
       const int off = (i * 64 + lane) * 16;
       const int row = off / RB;
-      const int vrow = min(max(row, rlo), rhi);
-      vr[i] = ldnt(a.vpool + base + vrow * RB + off % RB);
+      const int o = min(max(row, rlo), rhi) * RB + off % RB;
+      if constexpr (!kF32) kr[i] = ldnt(a.kpool + base + o);  // coalesced, staged through LDS
+      vr[i] = ldnt(a.vpool + base + o);
     }
   };
 
@@ -201,31 +214,48 @@ __global__ void __launch_bounds__(64 * kDecodeWaves, decode_min_waves<T>())
   for (; t < t_end; t += kDecodeWaves) {
     const bool tile_ok = ok_c;
 
-    // Stage V rows in LDS (two 8-byte stores per 16-byte chunk: the pitch is 8-byte aligned).
-#pragma unroll
-    for (int i = 0; i < NL; ++i) {
-      const int off = (i * 64 + lane) * 16;
-      char* dst = vst + (off / RB) * VP + off % RB;
-      *(uint2*)dst = make_uint2(vc[i].x, vc[i].y);
-      *(uint2*)(dst + 8) = make_uint2(vc[i].z, vc[i].w);
-    }
-
-    // S^T = K Q^T
     f32x4_v s = {0.f, 0.f, 0.f, 0.f};
+    if constexpr (kF32) {
+      // Stage V rows in LDS (two 8-byte stores per 16-byte chunk: the pitch is 8-byte aligned).
 #pragma unroll
-    for (int c = 0; c < NL; ++c) {
-      if constexpr (kF32) {
+      for (int i = 0; i < NL; ++i) {
+        const int off = (i * 64 + lane) * 16;
+        char* dst = vst + (off / RB) * VP + off % RB;
+        *(uint2*)dst = make_uint2(vc[i].x, vc[i].y);
+        *(uint2*)(dst + 8) = make_uint2(vc[i].z, vc[i].w);
+      }
+      // S^T = K Q^T
+#pragma unroll
+      for (int c = 0; c < NL; ++c) {
         s = mfma_f32(__uint_as_float(kc[c].x), __uint_as_float(qv[c].x), s);
         s = mfma_f32(__uint_as_float(kc[c].y), __uint_as_float(qv[c].y), s);
         s = mfma_f32(__uint_as_float(kc[c].z), __uint_as_float(qv[c].z), s);
         s = mfma_f32(__uint_as_float(kc[c].w), __uint_as_float(qv[c].w), s);
-      } else {
-        s = DecodeMfma<T>::qk(kc[c], qv[c], s);
       }
+      // K went into the MFMAs and V into LDS: the registers take the next tile's loads, which
+      // stay in flight through this tile's softmax and PV.
+      if (t + kDecodeWaves < t_end) load_tile(t + kDecodeWaves, kc, vc, ok_c);
+    } else {
+      // Stage K and V rows (lane-linear 16-byte chunks at swizzled chunk positions).
+      char* kst = vst + kTile * RB;
+#pragma unroll
+      for (int i = 0; i < NL; ++i) {
+        const int off = (i * 64 + lane) * 16;
+        const int row = off / RB, lc = (off % RB) / 16;
+        const int dst = row * RB + 16 * (lc ^ C::swz(row));
+        *(uint4*)(kst + dst) = kc[i];
+        *(uint4*)(vst + dst) = vc[i];
+      }
+      wave_lds_sync();
+      // both tiles are in LDS: the registers take the next tile's loads, which stay in flight
+      // through this tile's MFMAs and softmax
+      if (t + kDecodeWaves < t_end) load_tile(t + kDecodeWaves, kc, vc, ok_c);
+      // S^T = K Q^T: the K operand of chunk c is row n, logical chunk 4c + g
+      const int ksw = C::swz(n);
+#pragma unroll
+      for (int c = 0; c < NL; ++c)
+        s = DecodeMfma<T>::qk(*(const uint4*)(kst + n * RB + 16 * ((4 * c + g) ^ ksw)), qv[c], s);
     }
-    // K went into the MFMAs and V into LDS: the registers take the next tile's loads, which
-    // stay in flight through this tile's softmax and PV.
-    if (t + kDecodeWaves < t_end) load_tile(t + kDecodeWaves, kc, vc, ok_c);
 
     // Online softmax for head column n over tokens 4g..4g+3 of this tile.
     const int pos = t * kTile + 4 * g;
@@ -249,7 +279,7 @@ __global__ void __launch_bounds__(64 * kDecodeWaves, decode_min_waves<T>())
 #pragma unroll
     for (int i = 0; i < ND; ++i) acc[i] *= alpha;
 
-    wave_lds_sync();  // V staging visible to the whole wave
+    if constexpr (kF32) wave_lds_sync();  // V staging visible to the whole wave
 
     // O^T += V^T P^T
     if constexpr (kF32) {
@@ -262,15 +292,17 @@ __global__ void __launch_bounds__(64 * kDecodeWaves, decode_min_waves<T>())
         }
       }
     } else {
+      // A operand = V^T[16 dims][tokens 4g..4g+3] straight from the row-major stage by a
+      // transpose read: lane n addresses row 4g + n/4, dims 16db + 4(n%4) .. +3
       const uint2 pp = make_uint2(DecodeMfma<T>::pack(p[0], p[1]), DecodeMfma<T>::pack(p[2], p[3]));
+      const int vrow = 4 * g + (n >> 2);
+      const int vsw = C::swz(vrow);
 #pragma unroll
       for (int db = 0; db < ND; ++db) {
-        const char* col = vst + (4 * g) * VP + (db * 16 + n) * ES;
-        const uint32_t v0 = *(const uint16_t*)(col);
-        const uint32_t v1 = *(const uint16_t*)(col + VP);
-        const uint32_t v2 = *(const uint16_t*)(col + 2 * VP);
-        const uint32_t v3 = *(const uint16_t*)(col + 3 * VP);
-        acc[db] = DecodeMfma<T>::pv(make_uint2(v0 | (v1 << 16), v2 | (v3 << 16)), pp, acc[db]);
+        const int colb = (db * 16 + 4 * (n & 3)) * ES;
+        const char* ap = vst + vrow * RB + 16 * ((colb >> 4) ^ vsw) + (colb & 15);
+        const s16x4_v vop = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_v*)ap);
+        acc[db] = DecodeMfma<T>::pv(__builtin_bit_cast(uint2, vop), pp, acc[db]);
       }
     }
     wave_lds_sync();  // reads done before the next tile overwrites the staging area
@@ -323,12 +355,13 @@ __global__ void __launch_bounds__(64 * kDecodeWaves, decode_min_waves<T>())
 }
 
 // Merge the per-split partials (m, l, acc[D]) of sequences that needed more than one split.
-// One wave per (query head, sequence): lane s reads split s's (m, l); the weights
-// 2^(m_s - M) are shared through LDS and every lane accumulates D/64 output dims.
+// One wave per (query head, sequence). Every partial's (m, l) and the lane's D/64 accumulator
+// columns are loaded in one batch (up to 16 splits per pass), so the merge waits on two memory
+// round trips: the context length, then the partials.
 template <typename T, int D>
 __global__ void __launch_bounds__(64) decode_combine_kernel(DecodeArgs a) {
   constexpr int DPL = D / 64;
-  __shared__ float w_lds[64];
+  constexpr int B = 16;  // splits per batch
   const int hq = blockIdx.x, seq = blockIdx.y, lane = threadIdx.x;
   int L = a.context_lens[seq];
   L = min(L, min(a.max_context_len, a.max_blocks_per_seq * a.block_size));
@@ -337,43 +370,37 @@ __global__ void __launch_bounds__(64) decode_combine_kernel(DecodeArgs a) {
   const int nsplit = ((L - 1) / kTile - start_tok / kTile + a.tps) / a.tps;
   if (nsplit <= 1) return;
   const float* pp = a.partials + ((int64_t)seq * a.hq + hq) * a.max_splits * (D + 4);
-  float M = -INFINITY;
-  for (int s = lane; s < nsplit; s += 64) M = fmaxf(M, pp[s * (D + 4)]);
-  M = group_max<64>(M);
+  float M = -INFINITY, lsum = 0.f;
   float acc[DPL];
 #pragma unroll
   for (int e = 0; e < DPL; ++e) acc[e] = 0.f;
-  float lsum = 0.f;
-  for (int s0 = 0; s0 < nsplit; s0 += 64) {
-    const int s = s0 + lane;
-    float w = 0.f;
-    if (s < nsplit && M != -INFINITY) {
-      const float ms = pp[s * (D + 4)];
-      w = (ms == -INFINITY) ? 0.f : exp2f(ms - M);
-      lsum = fmaf(pp[s * (D + 4) + 1], w, lsum);
+  for (int s0 = 0; s0 < nsplit; s0 += B) {
+    float ms[B], ls[B], v[B][DPL];
+#pragma unroll
+    for (int u = 0; u < B; ++u) {
+      const float* src = pp + min(s0 + u, nsplit - 1) * (D + 4);
+      ms[u] = (s0 + u < nsplit) ? src[0] : -INFINITY;
+      ls[u] = src[1];
+#pragma unroll
+      for (int e = 0; e < DPL; ++e) v[u][e] = src[4 + lane * DPL + e];
     }
-    w_lds[lane] = w;
-    __syncthreads();
-    const int cnt = min(64, nsplit - s0);
-    // Batches of 8 partial rows: the loads of a batch are all in flight before the FMAs.
-    for (int j0 = 0; j0 < cnt; j0 += 8) {
-      float v[8][DPL];
+    float mb = M;
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const float* src = pp + (s0 + min(j0 + u, cnt - 1)) * (D + 4) + 4 + lane * DPL;
+    for (int u = 0; u < B; ++u) mb = fmaxf(mb, ms[u]);
+    if (mb == -INFINITY) continue;
+    const float alpha = (M == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(M - mb);
+    lsum *= alpha;
 #pragma unroll
-        for (int e = 0; e < DPL; ++e) v[u][e] = src[e];
-      }
+    for (int e = 0; e < DPL; ++e) acc[e] *= alpha;
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const float wj = (j0 + u < cnt) ? w_lds[j0 + u] : 0.f;
+    for (int u = 0; u < B; ++u) {
+      const float w = (ms[u] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(ms[u] - mb);
+      lsum = fmaf(ls[u], w, lsum);
 #pragma unroll
-        for (int e = 0; e < DPL; ++e) acc[e] = fmaf(v[u][e], wj, acc[e]);
-      }
+      for (int e = 0; e < DPL; ++e) acc[e] = fmaf(v[u][e], w, acc[e]);
     }
-    __syncthreads();
+    M = mb;
   }
-  lsum = group_sum<64>(lsum);
   const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
 #pragma unroll
   for (int e = 0; e < DPL; ++e)
