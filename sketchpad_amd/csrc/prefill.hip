@@ -55,6 +55,11 @@ template <> struct PrefillMfma<bf16_t> {
   __device__ __forceinline__ static uint32_t pack(float lo, float hi) {  // v_cvt_pk_bf16_f32 (RNE)
     return __builtin_bit_cast(uint32_t, __builtin_convertvector((pf_f32x2){lo, hi}, pf_bf16x2));
   }
+  // c + lo + hi of a packed pair (v_dot2_f32_bf16 against (1, 1))
+  __device__ __forceinline__ static float sum2(uint32_t w, float c) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(pf_bf16x2, w),
+                                           __builtin_bit_cast(pf_bf16x2, 0x3f803f80u), c, false);
+  }
 };
 template <> struct PrefillMfma<f16_t> {
   __device__ __forceinline__ static pf_f32x16 mma(uint4 a, uint4 b, pf_f32x16 c) {
@@ -67,6 +72,10 @@ template <> struct PrefillMfma<f16_t> {
   }
   __device__ __forceinline__ static uint32_t pack(float lo, float hi) {
     return __builtin_bit_cast(uint32_t, __builtin_convertvector((pf_f32x2){lo, hi}, pf_f16x2));
+  }
+  __device__ __forceinline__ static float sum2(uint32_t w, float c) {  // v_dot2_f32_f16
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(pf_f16x2, w),
+                                  __builtin_bit_cast(pf_f16x2, 0x3c003c00u), c, false);
   }
 };
 
@@ -283,30 +292,45 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PrefillArgs a) {
   const float c2 = a.scale_log2;  // > 0 (checked on the host)
   const int sw = C::swz(l32);     // swizzle of the K rows this lane reads (row & 15 == l32 & 15)
 
+  // Lane parts of the LDS operand addresses (byte offsets inside a tile). With the XOR swizzle
+  // an operand's logical chunk index only flips bits the lane part owns alone, so every operand
+  // of a tile sits at (lane part ^ constant) + immediate offset.
+  const int k_lane = (l32 * RB) | (16 * (hh ^ sw));
+  const int rl = (g4 >> 1) * 4 + (i16 >> 2);
+  const int chl = (g4 & 1) * 2 + ((i16 & 3) >> 1);
+  const int v_lane0 = rl * RB + 16 * (chl ^ C::swz(rl)) + 8 * (i16 & 1);
+  const int v_lane1 = (rl + 8) * RB + 16 * (chl ^ C::swz(rl + 8)) + 8 * (i16 & 1);
+
   auto compute_tile = [&](int t0, const char* kl) __attribute__((always_inline)) {
     const char* vl = kl + TILE;
-    // S^T = K Q^T: two 32-key blocks, interleaved so that consecutive MFMAs are independent;
-    // the K operands of step c+1 are read while the MFMAs of step c run.
+    // S^T = K Q^T: two 32-key blocks, interleaved so that consecutive MFMAs are independent.
+    // K operand i (k-step i/2, key block i%2) is row 32(i%2) + l32, chunk 2(i/2) + hh, i.e.
+    // (k_lane ^ 32(i/2)) + 32(i%2) RB; reads run AH operands ahead of the MFMAs, an order the
+    // sched_barriers pin. The lane base goes through an empty asm so the compiler derives the
+    // addresses inside the tile (one v_xor each) instead of keeping them all live.
     pf_f32x16 s[2];
 #pragma unroll
     for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
       for (int r = 0; r < 16; ++r) s[mb][r] = 0.f;
-    const char* krow0 = kl + l32 * RB;
-    const char* krow1 = kl + (32 + l32) * RB;
-    uint4 k0 = *(const uint4*)(krow0 + 16 * (hh ^ sw));
-    uint4 k1 = *(const uint4*)(krow1 + 16 * (hh ^ sw));
+    {
+      int kb = k_lane;
+      asm volatile("" : "+v"(kb));
+      constexpr int NK = 2 * KC, AH = 4;
+      auto read_k = [&](int i) __attribute__((always_inline)) {
+        return *(const uint4*)(kl + (i & 1) * 32 * RB + (kb ^ (32 * (i >> 1))));
+      };
+      uint4 kop[AH];
 #pragma unroll
-    for (int c = 0; c < KC; ++c) {
-      uint4 n0 = k0, n1 = k1;
-      if (c + 1 < KC) {
-        n0 = *(const uint4*)(krow0 + 16 * ((2 * c + 2 + hh) ^ sw));
-        n1 = *(const uint4*)(krow1 + 16 * ((2 * c + 2 + hh) ^ sw));
+      for (int i = 0; i < AH; ++i) kop[i] = read_k(i);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = 0; i < NK; ++i) {
+        const uint4 cur = kop[i % AH];
+        if (i + AH < NK) kop[i % AH] = read_k(i + AH);
+        s[i & 1] = M::mma(cur, qreg[i >> 1], s[i & 1]);
+        __builtin_amdgcn_sched_barrier(0);
       }
-      s[0] = M::mma(k0, qreg[c], s[0]);
-      s[1] = M::mma(k1, qreg[c], s[1]);
-      k0 = n0;
-      k1 = n1;
     }
     // masks: only tiles that cross the sequence end, the window edge or the diagonal. Score
     // (mb, r) of this lane is key t0 + 4hh + off with off = 32mb + 8(r/4) + r%4; it is visible
@@ -338,10 +362,10 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PrefillArgs a) {
 #pragma unroll
       for (int k = 0; k < 4; ++k) {  // four independent max3 chains over 8 scores each
         const int mb = k >> 1, r0 = (k & 1) * 8;
-        float x = __builtin_fmaxf(s[mb][r0], s[mb][r0 + 1]);
-#pragma unroll
-        for (int r = r0 + 2; r < r0 + 8; r += 2) x = max3f(x, s[mb][r], s[mb][r + 1]);
-        mq[k] = x;
+        float x = max3f(s[mb][r0], s[mb][r0 + 1], s[mb][r0 + 2]);
+        x = max3f(x, s[mb][r0 + 3], s[mb][r0 + 4]);
+        x = max3f(x, s[mb][r0 + 5], s[mb][r0 + 6]);
+        mq[k] = __builtin_fmaxf(x, s[mb][r0 + 7]);
       }
       mx = __builtin_fmaxf(max3f(mq[0], mq[1], mq[2]), mq[3]);
     }
@@ -368,33 +392,36 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PrefillArgs a) {
 #pragma unroll
       for (int e = 0; e < 8; ++e)
         p[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[ks >> 1][(ks & 1) * 8 + e], c2, -m_use));
-      ls[ks] = ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
       pb[ks] = make_uint4(M::pack(p[0], p[1]), M::pack(p[2], p[3]), M::pack(p[4], p[5]),
                           M::pack(p[6], p[7]));
+      // the row sum adds the 16-bit P values the PV product uses (v_dot2 against ones)
+      ls[ks] = M::sum2(pb[ks].w, M::sum2(pb[ks].z, M::sum2(pb[ks].y, M::sum2(pb[ks].x, 0.f))));
     }
     l_run += (ls[0] + ls[1]) + (ls[2] + ls[3]);
-    // O^T += V^T P^T: K-step ks covers tile tokens 16ks .. 16ks+15 in the S^T order. Operand
-    // (ks, db) is read one MFMA ahead.
-    auto read_v = [&](int ks, int db) __attribute__((always_inline)) {
-      const int row0 = 16 * ks + (g4 >> 1) * 4 + (i16 >> 2);
-      const int colb = (db * 32 + (g4 & 1) * 16 + 4 * (i16 & 3)) * 2;
-      const int ch = colb >> 4, within = colb & 15;
-      const char* a0 = vl + row0 * RB + 16 * (ch ^ C::swz(row0)) + within;
-      const char* a1 = vl + (row0 + 8) * RB + 16 * (ch ^ C::swz(row0 + 8)) + within;
-      const pf_s16x4 v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(a0));
-      const pf_s16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(a1));
-      return __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7);
-    };
-    pf_s16x8 vop = read_v(0, 0);
+    // O^T += V^T P^T: K-step ks covers tile tokens 16ks .. 16ks+15 in the S^T order. The V^T
+    // operand (ks, db) is rows 16ks + rl (+ 8), chunk 4db + chl: (v_lane0 ^ 64db) + 16ks RB
+    // (v_lane1 for the second row group), read AH operands ahead.
+    {
+      int vb0 = v_lane0, vb1 = v_lane1;
+      asm volatile("" : "+v"(vb0), "+v"(vb1));
+      auto read_v = [&](int ks, int db) __attribute__((always_inline)) {
+        const char* a0 = vl + 16 * ks * RB + (vb0 ^ (64 * db));
+        const char* a1 = vl + 16 * ks * RB + (vb1 ^ (64 * db));
+        const pf_s16x4 v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(a0));
+        const pf_s16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(a1));
+        return __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7);
+      };
+      constexpr int NV = 4 * DB, AH = 4;
+      pf_s16x8 vop[AH];
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
+      for (int i = 0; i < AH; ++i) vop[i] = read_v(i / DB, i % DB);
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int db = 0; db < DB; ++db) {
-        const int nks = db + 1 < DB ? ks : ks + 1, ndb = db + 1 < DB ? db + 1 : 0;
-        pf_s16x8 nxt = vop;
-        if (nks < 4) nxt = read_v(nks, ndb);
-        acc[db] = M::mma(vop, pb[ks], acc[db]);
-        vop = nxt;
+      for (int i = 0; i < NV; ++i) {
+        const pf_s16x8 cur = vop[i % AH];
+        if (i + AH < NV) vop[i % AH] = read_v((i + AH) / DB, (i + AH) % DB);
+        acc[i % DB] = M::mma(cur, pb[i / DB], acc[i % DB]);
+        __builtin_amdgcn_sched_barrier(0);
       }
     }
   };
