@@ -15,7 +15,9 @@ before the timed region starts. Prints one JSON line:
              on this host on the same workload
   prefill    the C3 ragged causal prefill (sp_varlen_prefill, bf16 MFMA): average launch time,
              TFLOP/s over the unmasked (query, key) pairs and the fraction of the 2.5 PFLOP/s
-             dense bf16 peak, the C3 append, and the oracle's prefill port on a bounded sample
+             dense bf16 peak, the C3 append, the C3 RoPE-fused append (sp_rope_kv_append: K
+             rotated into the pool, V copied, Q rotated in place) and the oracle's prefill port
+             on a bounded sample
 """
 from __future__ import annotations
 
@@ -192,12 +194,29 @@ def time_prefill_c3(steps: int, warmup: int):
         append()
         prefill()
     torch.cuda.synchronize()
+    # RoPE fused into the append: rotate K into the pool, copy V, rotate Q in place, one pass
+    cos, sin = sp.rope_tables(int(w.lens.max()), w.head_dim, 500000.0)
+    cos_d, sin_d = torch.from_numpy(cos).cuda(), torch.from_numpy(sin).cuda()
+    positions = torch.from_numpy(
+        np.concatenate([np.arange(L) for L in w.lens]).astype(np.int32)).cuda()
+    q_rope = t["q"].clone()
+
+    def rope_append():
+        sp.rope_kv_append(t["k_pool"], t["v_pool"], lay, t["k"], t["v"], positions,
+                          t["slot_mapping"], cos_d, sin_d, q=q_rope, stream=s)
+
+    rope_append()
+    torch.cuda.synchronize()
     pf_ms, pf_min = _event_times(stream, prefill, steps)
     ap_ms, _ = _event_times(stream, append, steps)
+    ra_ms, _ = _event_times(stream, rope_append, steps)
     flops = w.flops()
     tflops = flops / (pf_ms * 1e-3) / 1e12
     e = 2
     append_bytes = w.total_tokens * w.hkv * w.head_dim * e * 2 * 2 + w.total_tokens * 4
+    # K, V rows read and written, Q rows read and written, slot + position, one table row each
+    rope_bytes = (w.total_tokens * (w.hkv * 4 + w.hq * 2) * w.head_dim * e
+                  + w.total_tokens * (8 + w.head_dim * 4))
     return w, {
         "workload": f"{w.name}: B={w.num_seqs}, lens={[int(x) for x in w.lens]} "
                     f"(sum {w.total_tokens}), Hq={w.hq}, Hkv={w.hkv}, D={w.head_dim}, causal, "
@@ -216,6 +235,8 @@ def time_prefill_c3(steps: int, warmup: int):
         },
         "append": {"ms": round(ap_ms, 5), "bytes": append_bytes,
                    "GBs": round(append_bytes / (ap_ms * 1e-3) / 1e9, 2)},
+        "rope_append": {"ms": round(ra_ms, 5), "bytes": rope_bytes,
+                        "GBs": round(rope_bytes / (ra_ms * 1e-3) / 1e9, 2)},
     }
 
 

@@ -103,6 +103,48 @@ int sp_kv_append(void* k_pool, void* v_pool, const sp_cache_layout* layout,
                  sp_dtype dtype, void* stream);
 
 /*
+ * Rotary tables for sp_rope_kv_append, built on the host exactly as the reference builds its
+ * caches (RotaryEmbedding::with_base, crates/sketchpad-core/src/rope.rs:60-92), in fp32:
+ *   inv_freq[i] = 1 / powf(base, (2i) / head_dim),  angle = p * inv_freq[i],
+ *   cos_table[p * head_dim/2 + i] = cosf(angle),   sin_table[...] = sinf(angle)
+ * for p < rows, i < head_dim / 2 (the reference stores each value twice, once per element of the
+ * pair; these tables keep one per pair). Host memory; copy them to the device once.
+ * head_dim must be even and positive, rows >= 0.
+ */
+int sp_rope_tables(float* cos_table, float* sin_table, int32_t rows, int32_t head_dim,
+                   float base);
+
+/*
+ * RoPE fused into the cache append. Rotates the new K rows and writes them, with the V rows,
+ * into the pools (as sp_kv_append), and rotates Q in place, in one pass. Replaces
+ * RotaryEmbedding::forward (rope.rs:115-170) on q and k followed by PagedKvCache::store_kv
+ * (paged_attention.rs:230-310), as called from MultiHeadAttention::forward_cached
+ * (transformer.rs:221-227). Adjacent dimensions (2i, 2i+1) of token t rotate by the angle of
+ * row positions[t] of the tables (rope.rs:145-170, rotate_half maps (x0, x1) to (-x1, x0)):
+ *   y[2i] = x[2i] c - x[2i+1] s,   y[2i+1] = x[2i+1] c + x[2i] s
+ * in fp32 with each product and the sum rounded (no fused multiply-add), then stored in the
+ * element type: bit-identical to the reference's fp32 op sequence for f32; bf16 / f16 round
+ * once from the fp32 result.
+ *   k_new, v_new : element (t, h, d) at t*token_stride + h*head_stride + d (as sp_kv_append)
+ *   q            : [T, num_q_heads, D] with element (t, h, d) at t*q_token_stride +
+ *                  h*q_head_stride + d, rotated in place; NULL to skip Q
+ *   positions    : [num_tokens] int32 (device), each token's position in its sequence
+ *   cos_table, sin_table : device copies of sp_rope_tables(rows = table_rows)
+ * A token whose slot is negative or past the pool has its K/V write skipped (as sp_kv_append;
+ * its Q is still rotated); a token whose position is outside [0, table_rows) is skipped entirely
+ * (K/V not written, Q not rotated). The reference panics on both (paged_attention.rs:242, the
+ * cache slice in rope.rs:124-131).
+ */
+int sp_rope_kv_append(void* k_pool, void* v_pool, const sp_cache_layout* layout,
+                      const void* k_new, const void* v_new,
+                      int64_t token_stride, int64_t head_stride,
+                      void* q, int64_t q_token_stride, int64_t q_head_stride,
+                      int32_t num_q_heads,
+                      const int32_t* positions, const int32_t* slot_mapping, int32_t num_tokens,
+                      const float* cos_table, const float* sin_table, int32_t table_rows,
+                      sp_dtype dtype, void* stream);
+
+/*
  * Cache gather: copy one sequence's first seq_len positions out of the pools into contiguous
  * k_out / v_out of shape [Hkv, seq_len, D]. Replaces PagedKvCache::gather_kv
  * (paged_attention.rs:313-378); seq_len == 0 is a no-op (the reference returns [Hkv, 0, D]).

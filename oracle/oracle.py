@@ -33,6 +33,9 @@ _SIG = {
                              c_void_p, c_int64, c_int64, c_int]),
     "spo_gather_kv": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, POINTER(Layout), c_void_p,
                               c_int64, c_int64, c_int]),
+    "spo_rope_caches": (None, [c_void_p, c_void_p, c_int64, c_int64, c_float]),
+    "spo_rope_apply": (c_int, [c_void_p, c_int64, c_int64, c_int64, c_int64, c_int64, c_void_p,
+                               c_void_p, c_void_p, c_int64]),
     "spo_causal_mask": (None, [c_int64, c_void_p]),
     "spo_prefill_causal_mask": (None, [c_int64, c_int64, c_void_p]),
     "spo_sliding_window_mask": (None, [c_int64, c_int64, c_void_p]),
@@ -237,3 +240,25 @@ def cpu_prefill_baseline(out, q, k, v, cu_seqlens, *, hq: int, hkv: int, d: int,
     cu = _c(cu_seqlens, np.int32)
     lib().spo_cpu_prefill_baseline(_p(out), _p(q), _p(k), _p(v), _p(cu), len(cu) - 1, hq, hkv, d,
                                    scale, threads)
+
+
+def rope_caches(rows: int, head_dim: int, base: float = 10000.0):
+    """RotaryEmbedding::with_base (rope.rs:60-102): full f32 caches [rows, head_dim] with each
+    pair's cos / sin repeated (repeat_interleave)."""
+    cos = np.zeros((rows, head_dim), dtype=np.float32)
+    sin = np.zeros_like(cos)
+    lib().spo_rope_caches(_p(cos), _p(sin), rows, head_dim, base)
+    return cos, sin
+
+
+def rope_apply(x: np.ndarray, positions, cos_full: np.ndarray, sin_full: np.ndarray) -> np.ndarray:
+    """apply_rotary (rope.rs:136-170) on a float32 [T, H, D] copy of x: token t rotated by the
+    caches' row positions[t]. Returns the rotated copy."""
+    y = np.ascontiguousarray(x, dtype=np.float32).copy()
+    t, h, d = y.shape
+    pos = _c(positions, np.int32)
+    rc = lib().spo_rope_apply(_p(y), t, h, d, h * d, d, _p(pos), _p(np.ascontiguousarray(cos_full)),
+                              _p(np.ascontiguousarray(sin_full)), cos_full.shape[0])
+    if rc != 0:
+        raise ValueError("position outside the rotary caches")
+    return y

@@ -419,3 +419,60 @@ void spo_cpu_prefill_baseline(float* out, const float* q, const float* k, const 
     }
   }
 }
+
+
+/* ---------------------------------------------------------------------------------------------
+ * Rotary position embedding (crates/sketchpad-core/src/rope.rs). Compiled without floating-point
+ * contraction: the reference evaluates x * cos + rotate_half(x) * sin as separate tensor ops,
+ * each product and the sum rounded to f32.
+ * ------------------------------------------------------------------------------------------- */
+#pragma GCC push_options
+#pragma GCC optimize("fp-contract=off")
+
+/* RotaryEmbedding::with_base (rope.rs:60-92) + repeat_interleave (:95-102): the full caches
+ * [rows][head_dim], each pair's cos / sin stored twice. inv_freq = 1 / base^(2i/d) in f32
+ * (:66-68), angles = positions x inv_freq (a [rows,1] x [1,d/2] matmul: one f32 product,
+ * :75-78), cos / sin in f32 (:81-82). */
+void spo_rope_caches(float* cos_full, float* sin_full, int64_t rows, int64_t head_dim, float base) {
+  const int64_t half = head_dim / 2;
+  for (int64_t i = 0; i < half; ++i) {
+    const float inv_freq = 1.0f / powf(base, (float)(2 * i) / (float)head_dim);
+    for (int64_t p = 0; p < rows; ++p) {
+      const float angle = (float)p * inv_freq;
+      const float c = cosf(angle), sn = sinf(angle);
+      cos_full[p * head_dim + 2 * i] = c;
+      cos_full[p * head_dim + 2 * i + 1] = c;
+      sin_full[p * head_dim + 2 * i] = sn;
+      sin_full[p * head_dim + 2 * i + 1] = sn;
+    }
+  }
+}
+
+/* apply_rotary + rotate_half (rope.rs:136-170) on f32 rows, in place: token t of x (element
+ * (t, h, d) at t*tok_stride + h*head_stride + d) at position positions[t] becomes
+ * x * cos[pos] + rotate_half(x) * sin[pos], rotate_half([x0, x1, ...]) = [-x1, x0, ...].
+ * Returns -1 if a position is outside the caches (the reference's slice would panic). */
+int spo_rope_apply(float* x, int64_t tokens, int64_t heads, int64_t head_dim, int64_t tok_stride,
+                   int64_t head_stride, const int32_t* positions, const float* cos_full,
+                   const float* sin_full, int64_t rows) {
+  for (int64_t t = 0; t < tokens; ++t) {
+    const int64_t pos = positions[t];
+    if (pos < 0 || pos >= rows) return -1;
+    const float* c = cos_full + pos * head_dim;
+    const float* sn = sin_full + pos * head_dim;
+    for (int64_t h = 0; h < heads; ++h) {
+      float* r = x + t * tok_stride + h * head_stride;
+      for (int64_t i = 0; i < head_dim; i += 2) {
+        const float x0 = r[i], x1 = r[i + 1];
+        const float rot0 = -x1, rot1 = x0; /* rotate_half */
+        const float a0 = x0 * c[i], b0 = rot0 * sn[i];
+        const float a1 = x1 * c[i + 1], b1 = rot1 * sn[i + 1];
+        r[i] = a0 + b0;
+        r[i + 1] = a1 + b1;
+      }
+    }
+  }
+  return 0;
+}
+
+#pragma GCC pop_options

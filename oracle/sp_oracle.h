@@ -30,6 +30,15 @@
  *               GQA == repeated-head MHA, mask-rule == explicit additive mask
  *   spo_attention_f32_refops                              transformer.rs:234-243 op order in f32
  *       pinned: within f32 rounding of spo_attention_f64 on every test case
+ *   spo_rope_caches                                       rope.rs:60-102 (with_base + repeat_interleave)
+ *       pinned: position 0 -> (1, 0) exactly, pair 0 -> (cos p, sin p) within 1 ulp of the
+ *               float64 values, every entry within a few ulp of float64 cos / sin of p / base^(2i/d),
+ *               duplicated entries equal
+ *   spo_rope_apply                                        rope.rs:136-170 (apply_rotary, rotate_half)
+ *       pinned: the reference's rope tests (zeros stay zeros, ones change, position 0 is the
+ *               identity; rope.rs:180-230), complex multiplication (x0 + i x1) e^{i angle} in
+ *               float64, pair norms preserved, rotating back by -angle restores x, and
+ *               <R(m) q, R(n) k> depends only on m - n (float64)
  *   spo_cpu_decode_baseline / spo_cpu_prefill_baseline    the reference's whole decode / prefill
  *       op sequence (store, gather+concat, repeat_kv, matmul, scale, mask, softmax, matmul), f32,
  *       OpenMP over sequences; pinned against spo_attention_f64.
@@ -112,6 +121,11 @@ void spo_cpu_decode_baseline(float* out, const float* q, const float* k_new, con
 void spo_cpu_prefill_baseline(float* out, const float* q, const float* k, const float* v,
                               const int32_t* cu_seqlens, int64_t num_seqs, int hq, int hkv,
                               int d, float scale, int threads);
+
+void spo_rope_caches(float* cos_full, float* sin_full, int64_t rows, int64_t head_dim, float base);
+int spo_rope_apply(float* x, int64_t tokens, int64_t heads, int64_t head_dim, int64_t tok_stride,
+                   int64_t head_stride, const int32_t* positions, const float* cos_full,
+                   const float* sin_full, int64_t rows);
 
 #ifdef __cplusplus
 }

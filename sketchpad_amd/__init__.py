@@ -22,5 +22,7 @@ from ._lib import (  # noqa: F401
     paged_decode,
     paged_decode_workspace_size,
     paged_prefill,
+    rope_kv_append,
+    rope_tables,
     varlen_prefill,
 )

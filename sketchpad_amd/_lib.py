@@ -62,6 +62,11 @@ _SIGNATURES = {
                                c_int64, c_int64, c_void_p, c_int32, c_int32, c_void_p]),
     "sp_kv_gather": (c_int32, [c_void_p, c_void_p, c_void_p, c_void_p, POINTER(CacheLayout),
                                c_void_p, c_int32, c_int32, c_int32, c_void_p]),
+    "sp_rope_tables": (c_int32, [c_void_p, c_void_p, c_int32, c_int32, c_float]),
+    "sp_rope_kv_append": (c_int32, [c_void_p, c_void_p, POINTER(CacheLayout), c_void_p, c_void_p,
+                                    c_int64, c_int64, c_void_p, c_int64, c_int64, c_int32,
+                                    c_void_p, c_void_p, c_int32, c_void_p, c_void_p, c_int32,
+                                    c_int32, c_void_p]),
     "sp_paged_decode_workspace_size": (c_size_t, [c_int32, c_int32, c_int32, c_int32,
                                                   POINTER(CacheLayout)]),
     "sp_paged_decode": (c_int32, [c_void_p, c_void_p, c_void_p, c_void_p, POINTER(CacheLayout),
@@ -149,6 +154,38 @@ def kv_append(k_pool, v_pool, lay: CacheLayout, k_new, v_new, slot_mapping, *,
     check(load().sp_kv_append(_ptr(k_pool), _ptr(v_pool), ctypes.byref(lay), _ptr(k_new),
                               _ptr(v_new), token_stride, head_stride, _ptr(slot_mapping),
                               slot_mapping.numel(), sp_dtype(k_pool), _stream(stream)))
+
+
+def rope_tables(rows: int, head_dim: int, base: float = 10000.0):
+    """sp_rope_tables: host fp32 (cos, sin) numpy arrays of shape [rows, head_dim // 2]."""
+    import numpy as np
+    cos = np.zeros((max(rows, 0), head_dim // 2), dtype=np.float32)
+    sin = np.zeros_like(cos)
+    check(load().sp_rope_tables(cos.ctypes.data, sin.ctypes.data, rows, head_dim, base))
+    return cos, sin
+
+
+def rope_kv_append(k_pool, v_pool, lay: CacheLayout, k_new, v_new, positions, slot_mapping,
+                   cos_table, sin_table, *, q=None, token_stride: int | None = None,
+                   head_stride: int | None = None, stream=None) -> None:
+    """sp_rope_kv_append: rotate K (and Q in place, when given) by the tables' angles at each
+    token's position and append K/V through the slot mapping. k_new/v_new default to
+    token-major [T, Hkv, D]; q is [T, Hq, D]; cos/sin tables are device fp32 [rows, D/2]."""
+    torch = _torch()
+    if token_stride is None:
+        token_stride = k_new.stride(0)
+    if head_stride is None:
+        head_stride = k_new.stride(1)
+    assert slot_mapping.dtype == torch.int32 and positions.dtype == torch.int32
+    assert cos_table.dtype == torch.float32 and sin_table.dtype == torch.float32
+    qp, qts, qhs, hq = None, 0, 0, 0
+    if q is not None:
+        qp, qts, qhs, hq = _ptr(q), q.stride(0), q.stride(1), q.shape[1]
+    check(load().sp_rope_kv_append(_ptr(k_pool), _ptr(v_pool), ctypes.byref(lay), _ptr(k_new),
+                                   _ptr(v_new), token_stride, head_stride, qp, qts, qhs, hq,
+                                   _ptr(positions), _ptr(slot_mapping), slot_mapping.numel(),
+                                   _ptr(cos_table), _ptr(sin_table), cos_table.shape[0],
+                                   sp_dtype(k_pool), _stream(stream)))
 
 
 def kv_gather(k_out, v_out, k_pool, v_pool, lay: CacheLayout, block_table, seq_len: int, *,

@@ -40,7 +40,7 @@ DEVICE_FLAGS = [
     f"-I{CSRC}",
 ]
 
-LIB_SOURCES = ["kv_cache.hip", "paged_decode.hip", "prefill.hip", "capi.cpp"]
+LIB_SOURCES = ["kv_cache.hip", "paged_decode.hip", "prefill.hip", "rope_append.hip", "capi.cpp"]
 HOST_SOURCES = ["paged_attention.cpp"]
 
 

@@ -11,6 +11,7 @@
 #include "kv_cache.hpp"
 #include "paged_decode.hpp"
 #include "prefill.hpp"
+#include "rope_append.hpp"
 #include "sp_common.hpp"
 
 namespace sp {
@@ -100,6 +101,72 @@ int sp_kv_append(void* k_pool, void* v_pool, const sp_cache_layout* layout, cons
   pool_strides(layout, es, &a.block_stride_b, &a.layer_off_b);
   a.num_slots = (int64_t)layout->num_blocks * layout->block_size;
   return launch_kv_append(a, (hipStream_t)stream);
+}
+
+int sp_rope_tables(float* cos_table, float* sin_table, int32_t rows, int32_t head_dim,
+                   float base) {
+  const char* fn = "sp_rope_tables";
+  if (rows < 0 || head_dim <= 0 || (head_dim & 1))
+    return fail(SP_EINVAL, "%s: rows %d, head_dim %d (must be even and > 0)", fn, rows, head_dim);
+  if (rows == 0) return SP_OK;
+  if (!cos_table || !sin_table) return fail(SP_EINVAL, "%s: NULL pointer argument", fn);
+  if (!(base > 0.f) || !isfinite(base)) return fail(SP_EINVAL, "%s: base must be > 0", fn);
+  const int half = head_dim / 2;
+  for (int i = 0; i < half; ++i) {
+    // fp32 throughout, as the reference: 1.0 / base.powf((2 * i) as f32 / head_dim as f32)
+    const float inv_freq = 1.0f / powf(base, (float)(2 * i) / (float)head_dim);
+    for (int p = 0; p < rows; ++p) {
+      const float angle = (float)p * inv_freq;
+      cos_table[(int64_t)p * half + i] = cosf(angle);
+      sin_table[(int64_t)p * half + i] = sinf(angle);
+    }
+  }
+  return SP_OK;
+}
+
+int sp_rope_kv_append(void* k_pool, void* v_pool, const sp_cache_layout* layout,
+                      const void* k_new, const void* v_new, int64_t token_stride,
+                      int64_t head_stride, void* q, int64_t q_token_stride, int64_t q_head_stride,
+                      int32_t num_q_heads, const int32_t* positions, const int32_t* slot_mapping,
+                      int32_t num_tokens, const float* cos_table, const float* sin_table,
+                      int32_t table_rows, sp_dtype dtype, void* stream) {
+  const char* fn = "sp_rope_kv_append";
+  if (int rc = check_layout(layout, fn)) return rc;
+  if (int rc = check_dtype(dtype, fn)) return rc;
+  if (num_tokens < 0 || table_rows < 0)
+    return fail(SP_EINVAL, "%s: num_tokens %d, table_rows %d", fn, num_tokens, table_rows);
+  if (layout->head_dim & 1) return fail(SP_EINVAL, "%s: head_dim %d is odd", fn, layout->head_dim);
+  if (num_tokens == 0) return SP_OK;
+  if (!k_pool || !v_pool || !k_new || !v_new || !positions || !slot_mapping || !cos_table ||
+      !sin_table)
+    return fail(SP_EINVAL, "%s: NULL pointer argument", fn);
+  if (token_stride < 0 || head_stride < 0 || q_token_stride < 0 || q_head_stride < 0)
+    return fail(SP_EINVAL, "%s: negative stride", fn);
+  if (q && num_q_heads <= 0) return fail(SP_EINVAL, "%s: num_q_heads %d", fn, num_q_heads);
+  const int es = dtype_size(dtype);
+  RopeAppendArgs a{};
+  a.kpool = (char*)k_pool;
+  a.vpool = (char*)v_pool;
+  a.knew = (const char*)k_new;
+  a.vnew = (const char*)v_new;
+  a.kv_tok_b = token_stride * es;
+  a.kv_head_b = head_stride * es;
+  a.q = (char*)q;
+  a.q_tok_b = q_token_stride * es;
+  a.q_head_b = q_head_stride * es;
+  a.positions = positions;
+  a.slots = slot_mapping;
+  a.cos_t = cos_table;
+  a.sin_t = sin_table;
+  a.table_rows = table_rows;
+  a.num_tokens = num_tokens;
+  a.hkv = layout->num_kv_heads;
+  a.hq = q ? num_q_heads : 0;
+  a.head_dim = layout->head_dim;
+  a.block_size = layout->block_size;
+  pool_strides(layout, es, &a.block_stride_b, &a.layer_off_b);
+  a.num_slots = (int64_t)layout->num_blocks * layout->block_size;
+  return launch_rope_kv_append(a, dtype, (hipStream_t)stream);
 }
 
 int sp_kv_gather(void* k_out, void* v_out, const void* k_pool, const void* v_pool,

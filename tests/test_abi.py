@@ -101,6 +101,26 @@ def test_decode_validation(sp_lib):
             "workspace")
 
 
+def test_rope_validation(sp_lib):
+    f = sp_lib.sp_rope_kv_append
+    fake = ctypes.c_void_p(0x1000)
+
+    def call(lay, q=None, hq=0, tokens=1, rows=8, dtype=1, cos=fake):
+        return f(fake, fake, ctypes.byref(lay), fake, fake, 128, 64, q, 256, 64, hq, fake, fake,
+                 tokens, cos, fake, rows, dtype, None)
+
+    _expect(_lib.SP_EINVAL, call(_lay(head_dim=63)), "odd")
+    _expect(_lib.SP_EINVAL, call(_lay(), tokens=-1), "num_tokens")
+    _expect(_lib.SP_EINVAL, call(_lay(), cos=None), "NULL")
+    _expect(_lib.SP_EINVAL, call(_lay(), q=fake, hq=0), "num_q_heads")
+    _expect(_lib.SP_EINVAL, call(_lay(), dtype=7), "dtype")
+    assert call(_lay(), tokens=0) == 0
+    t = sp_lib.sp_rope_tables
+    _expect(_lib.SP_EINVAL, t(fake, fake, 4, 7, ctypes.c_float(10000.0)), "even")
+    _expect(_lib.SP_EINVAL, t(fake, fake, 4, 8, ctypes.c_float(-1.0)), "base")
+    assert t(None, None, 0, 8, ctypes.c_float(10000.0)) == 0
+
+
 def test_workspace_size_monotone(sp_lib):
     lay = _lay(num_blocks=100000, num_kv_heads=8, head_dim=128)
     sizes = [sp_lib.sp_paged_decode_workspace_size(64, 32, L, -1, ctypes.byref(lay))
