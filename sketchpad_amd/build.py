@@ -41,7 +41,7 @@ DEVICE_FLAGS = [
 ]
 
 LIB_SOURCES = ["kv_cache.hip", "paged_decode.hip", "prefill.hip", "rope_append.hip", "capi.cpp"]
-HOST_SOURCES = ["paged_attention.cpp"]
+HOST_SOURCES = ["paged_attention.cpp", "continuous_batching.cpp", "ragged_batch.cpp"]
 
 
 def _run(cmd: list[str]) -> None:
@@ -85,11 +85,12 @@ def build_host(jobs: int = 8) -> Path | None:
     _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs),
           f"-L{LIBDIR}", "-lsketchpad_attn", "-Wl,-rpath,$ORIGIN", "-o", str(tmp)])
     tmp.replace(out)
-    test_src = ROOT / "tests" / "cpp" / "test_paged_attention.cpp"
-    if test_src.exists():
+    test_srcs = [ROOT / "tests" / "cpp" / s for s in ("test_paged_attention.cpp",
+                                                       "test_batching.cpp")]
+    if all(p.exists() for p in test_srcs):
         exe = ROOT / "tests" / "cpp" / "build" / "test_paged_attention"
         exe.parent.mkdir(parents=True, exist_ok=True)
-        _run([HIPCC, *DEVICE_FLAGS, f"-I{HOST}", "-x", "hip", str(test_src), "-o", str(exe),
+        _run([HIPCC, *DEVICE_FLAGS, f"-I{HOST}", "-x", "hip", *map(str, test_srcs), "-o", str(exe),
               f"-L{LIBDIR}", "-lsketchpad_host", "-lsketchpad_attn",
               "-Wl,-rpath,$ORIGIN/../../../sketchpad_amd/lib"])
     return out

@@ -1,6 +1,8 @@
-"""The C++ mirror of the reference's paged/flash attention API (sketchpad_amd/host/), through its
-test binary tests/cpp/test_paged_attention: the restated reference unit tests on the CPU, and the
-device paths (store/gather round trips, paged cache == concat cache, flash attention) on the GPU."""
+"""The C++ mirror of the reference's paged/flash attention API and its iteration-level scheduler
+(sketchpad_amd/host/), through the test binary tests/cpp/test_paged_attention: the restated
+reference unit tests (paged_attention.rs, continuous_batching.rs) on the CPU, and the device paths
+(store/gather round trips, paged cache == concat cache, flash attention, ragged-batch metadata and
+a continuous-batching loop checked against float64 attention) on the GPU."""
 import subprocess
 from pathlib import Path
 
@@ -19,7 +21,8 @@ def _run(args):
 
 
 def test_mirror_reference_unit_tests_cpu():
-    """test_block_table, test_config_from_memory_budget, causal mask entries, Result errors."""
+    """test_block_table, test_config_from_memory_budget, causal mask entries, Result errors, and
+    the scheduler tests of continuous_batching.rs with its tie-breaking."""
     _run(["--cpu-only"])
 
 
