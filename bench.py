@@ -18,6 +18,9 @@ before the timed region starts. Prints one JSON line:
              dense bf16 peak, the C3 append, the C3 RoPE-fused append (sp_rope_kv_append: K
              rotated into the pool, V copied, Q rotated in place) and the oracle's prefill port
              on a bounded sample
+  polar_decode  the same decode step on PolarQuant-compressed pools (sp_polar_kv_append +
+             sp_polar_paged_decode): launch time, algorithmic bytes (2 + D/2 per cached
+             vector), GB/s, fraction of HBM peak, and the speed-up over the dense decode
 """
 from __future__ import annotations
 
@@ -54,6 +57,10 @@ def parse_args():
                     help="only the C3 prefill leg (profiling); prints its JSON object")
     ap.add_argument("--no-prefill", action="store_true",
                     help="skip the C3 ragged-prefill leg")
+    ap.add_argument("--no-polar", action="store_true",
+                    help="skip the PolarQuant compressed-cache decode leg")
+    ap.add_argument("--polar-only", action="store_true",
+                    help="only the decode config's PolarQuant leg (profiling)")
     ap.add_argument("--secondary", action="store_true",
                     help="also time the other decode configs (C4, C5) and report them")
     return ap.parse_args()
@@ -120,6 +127,64 @@ def time_decode_config(w, steps: int, warmup: int):
         "decode_bytes": w.decode_bytes(),
         "append_bytes": w.append_bytes(),
         "tensors": t,
+    }
+
+
+def time_polar_decode(w, t, steps: int, warmup: int):
+    """The same decode step on PolarQuant pools: sp_polar_kv_append of the step's rows, then
+    sp_polar_paged_decode. Every slot of the pool holds an encoded random row first."""
+    import torch
+    import sketchpad_amd as sp
+    from sketchpad_amd import workloads as W
+
+    lay = w.layout()
+    kp, vp = sp.alloc_polar_pools(lay)
+    dt = W.torch_dtype(w.dtype)
+    g = torch.Generator(device="cuda").manual_seed(w.seed)
+    total = w.num_blocks * w.block_size
+    for s0 in range(0, total, 16384):
+        n = min(16384, total - s0)
+        k = torch.randn(n, w.hkv, w.head_dim, generator=g, device="cuda").to(dt)
+        v = torch.randn(n, w.hkv, w.head_dim, generator=g, device="cuda").to(dt)
+        sp.polar_kv_append(kp, vp, lay, k, v,
+                           torch.arange(s0, s0 + n, dtype=torch.int32, device="cuda"))
+    max_ctx = w.max_context_len
+    ws = sp.alloc_decode_workspace(w.num_seqs, w.hq, max_ctx, w.window_left, lay)
+    scale = w.head_dim ** -0.5
+    stream = torch.cuda.current_stream()
+
+    def append():
+        sp.polar_kv_append(kp, vp, lay, t["k_new"], t["v_new"], t["slot_mapping"],
+                           stream=stream.cuda_stream)
+
+    def decode():
+        sp.polar_paged_decode(t["out"], t["q"], kp, vp, lay, t["block_tables"], t["context_lens"],
+                              max_ctx, scale, window_left=w.window_left, workspace=ws,
+                              stream=stream.cuda_stream)
+
+    for _ in range(warmup):
+        append()
+        decode()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        append()
+        decode()
+    torch.cuda.synchronize()
+    step_s = (time.perf_counter() - t0) / steps
+    dec_ms, dec_min = _event_times(stream, decode, steps)
+    app_ms, _ = _event_times(stream, append, steps)
+    db = w.polar_decode_bytes()
+    return {
+        "ms_per_step": round(step_s * 1e3, 4),
+        "decode_ms": round(dec_ms, 5),
+        "decode_ms_min": round(dec_min, 5),
+        "decode_bytes": db,
+        "decode_GBs": round(db / (dec_ms * 1e-3) / 1e9, 2),
+        "frac_hbm": round(db / (dec_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "append_ms": round(app_ms, 5),
+        "append_bytes": w.polar_append_bytes(),
+        "kernel": "polar_decode_kernel + decode_combine_kernel (one sp_polar_paged_decode call)",
     }
 
 
@@ -301,7 +366,7 @@ def main():
     args = parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only; --gpus {args.gpus} is not supported "
-              "(the path's sharding is described in DESIGN.md)", file=sys.stderr)
+              "(multi-GPU sharding of the attention path is not built)", file=sys.stderr)
         sys.exit(2)
     import torch
     from sketchpad_amd import workloads as W
@@ -322,6 +387,10 @@ def main():
         print(json.dumps({"prefill": pf}), flush=True)
         return
     w = W.DECODE_CONFIGS[args.config]()
+    if args.polar_only:
+        pq = time_polar_decode(w, W.make_decode_tensors(w), args.steps, args.warmup)
+        print(json.dumps({"polar_decode": pq}), flush=True)
+        return
     r = time_decode_config(w, args.steps, args.warmup)
     step_bytes = r["decode_bytes"] + r["append_bytes"]
     value = step_bytes / r["step_s"] / 1e9
@@ -361,6 +430,10 @@ def main():
     }
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(w, r["tensors"], args.cpu_seconds)
+    if not args.no_polar and w.dtype in ("bf16", "f16"):
+        pq = time_polar_decode(w, r["tensors"], args.steps, args.warmup)
+        pq["decode_speedup_vs_dense"] = round(r["decode_ms_avg"] / pq["decode_ms"], 3)
+        line["polar_decode"] = pq
     del r
     if not args.no_prefill:
         wp, pf = time_prefill_c3(max(10, args.steps // 2), 3)

@@ -233,6 +233,88 @@ int sp_flash_attention(void* out, const void* q, const void* k, const void* v,
                        int32_t head_dim, float scale, int32_t causal, sp_dtype dtype,
                        void* stream);
 
+/*
+ * ---- PolarQuant compressed paged cache ----------------------------------------------------
+ * KvQuantMethod::PolarQuant of CompressedKvCache (crates/sketchpad-core/src/kv_cache.rs:300-324,
+ * :437-532, used at :640-727). A head_dim vector x is stored as a record of
+ *   2 bytes   |x| (f32 norm, summed left to right without fused multiply-add) as IEEE binary16,
+ *             little endian (f16::from_f32: round to nearest even)
+ *   ceil(head_dim/2) bytes of 4-bit two's-complement direction codes
+ *             n_j = (x_j * (1/|x|) * 7).round().clamp(-7, 7)  (half away from zero; NaN -> 0),
+ *             dimension 2p in the high nibble of byte p, 2p+1 in the low nibble
+ * (all codes zero when |x| == 0) and read back as n_j * (|x| / 7), a zero row when the stored
+ * norm is 0. Encoding is bit-exact with the reference's polar_quant_compress.
+ *
+ * Paged pools (one for K, one for V): pool[num_blocks][num_layers][num_kv_heads] regions of
+ * block_size * (head_dim/2 + 2) bytes; sp_polar_pool_bytes() gives the size of one pool. Within
+ * a region the codes come first (K: [block_size][head_dim/2], token-major; V:
+ * [block_size/4][head_dim/2][4], four consecutive tokens interleaved per byte pair), then the
+ * block_size binary16 norms. Paged pools need an even head_dim, block_size a multiple of 4 and
+ * 16-byte aligned pools; the decode kernel also needs block_size a multiple of 16.
+ */
+
+/* Bytes of one record: 2 + ceil(head_dim / 2); -1 when head_dim <= 0. The ratio to an f16 row
+ * (2 * head_dim bytes) is KvQuantMethod::PolarQuant.compression_ratio for even head_dim. */
+int64_t sp_polar_record_bytes(int32_t head_dim);
+
+/* Bytes of one paged PolarQuant pool for this layout (0 if the layout is not valid for one). */
+size_t sp_polar_pool_bytes(const sp_cache_layout* layout);
+
+/*
+ * polar_quant_compress / polar_quant_decompress (kv_cache.rs:437-532) on contiguous rows:
+ * x [num_vecs, head_dim] (dtype, converted exactly to f32 first) <-> records
+ * [num_vecs, sp_polar_record_bytes(head_dim)] bytes. Any head_dim > 0 (odd ones pad the last
+ * byte's low nibble with 0). Decompression computes the f32 value and rounds once to dtype.
+ */
+int sp_polar_compress(void* records, const void* x, int64_t num_vecs, int32_t head_dim,
+                      sp_dtype dtype, void* stream);
+int sp_polar_decompress(void* out, const void* records, int64_t num_vecs, int32_t head_dim,
+                        sp_dtype dtype, void* stream);
+
+/*
+ * Encode on append: the PolarQuant form of sp_kv_append (same slot mapping, strides and skip
+ * rules). Replaces the compress-and-extend step of CompressedKvCache::update_layer
+ * (kv_cache.rs:665-676) for a paged pool and a ragged batch.
+ */
+int sp_polar_kv_append(void* k_pool, void* v_pool, const sp_cache_layout* layout,
+                       const void* k_new, const void* v_new,
+                       int64_t token_stride, int64_t head_stride,
+                       const int32_t* slot_mapping, int32_t num_tokens,
+                       sp_dtype dtype, void* stream);
+
+/*
+ * One sequence's first seq_len positions out of PolarQuant pools (rules of sp_kv_gather):
+ *   sp_polar_kv_gather : decompressed into k_out / v_out [Hkv, seq_len, D] of dtype — the full
+ *                        K / V that CompressedKvCache::update_layer returns (kv_cache.rs:682-724)
+ *   sp_polar_kv_export : the records themselves, [Hkv, seq_len, sp_polar_record_bytes(D)] bytes
+ *                        (the reference's k_bytes / v_bytes of a batch-1 cache filled in one
+ *                        update, kv_cache.rs:670-671)
+ * Positions whose block id lies outside the pool give a zero record / zeros.
+ */
+int sp_polar_kv_gather(void* k_out, void* v_out, const void* k_pool, const void* v_pool,
+                       const sp_cache_layout* layout, const int32_t* block_table,
+                       int32_t num_table_blocks, int32_t seq_len, sp_dtype dtype, void* stream);
+int sp_polar_kv_export(void* k_records, void* v_records, const void* k_pool, const void* v_pool,
+                       const sp_cache_layout* layout, const int32_t* block_table,
+                       int32_t num_table_blocks, int32_t seq_len, void* stream);
+
+/*
+ * Paged decode attention on PolarQuant pools: sp_paged_decode with every cached key / value read
+ * as n_j * (|x| / 7) straight from the codes (same arguments, same workspace size:
+ * sp_paged_decode_workspace_size). Replaces the decompress-then-attend step of
+ * CompressedKvCache::update_layer + MultiHeadAttention::forward_cached (transformer.rs:227-243).
+ * q / out dtype bf16 or f16 (f32 -> SP_EUNSUPPORTED). Scores take q . n exactly in fp32 MFMA
+ * accumulation, times |k|/7 and scale; softmax and accumulation are fp32; the probabilities
+ * times |v|/7 enter the PV product as bf16.
+ */
+int sp_polar_paged_decode(void* out, const void* q,
+                          const void* k_pool, const void* v_pool, const sp_cache_layout* layout,
+                          const int32_t* block_tables, int32_t max_blocks_per_seq,
+                          const int32_t* context_lens, int32_t max_context_len,
+                          int32_t num_seqs, int32_t num_q_heads,
+                          float scale, int32_t window_left, sp_dtype dtype,
+                          void* workspace, size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

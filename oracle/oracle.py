@@ -36,6 +36,12 @@ _SIG = {
     "spo_rope_caches": (None, [c_void_p, c_void_p, c_int64, c_int64, c_float]),
     "spo_rope_apply": (c_int, [c_void_p, c_int64, c_int64, c_int64, c_int64, c_int64, c_void_p,
                                c_void_p, c_void_p, c_int64]),
+    "spo_f32_to_f16_bits": (ctypes.c_uint16, [c_float]),
+    "spo_f16_bits_to_f32": (c_float, [ctypes.c_uint16]),
+    "spo_polar_record_bytes": (c_int64, [c_int64]),
+    "spo_polar_compress": (None, [c_void_p, c_void_p, c_int64, c_int64]),
+    "spo_polar_decompress": (None, [c_void_p, c_void_p, c_int64, c_int64]),
+    "spo_polar_compression_ratio": (c_double, [c_int64]),
     "spo_causal_mask": (None, [c_int64, c_void_p]),
     "spo_prefill_causal_mask": (None, [c_int64, c_int64, c_void_p]),
     "spo_sliding_window_mask": (None, [c_int64, c_int64, c_void_p]),
@@ -262,3 +268,46 @@ def rope_apply(x: np.ndarray, positions, cos_full: np.ndarray, sin_full: np.ndar
     if rc != 0:
         raise ValueError("position outside the rotary caches")
     return y
+
+
+# --- PolarQuant codec (kv_cache.rs:437-532) ---------------------------------------------------
+
+def f32_to_f16_bits(x: float) -> int:
+    """f16::from_f32(x).to_bits() (IEEE round to nearest even)."""
+    return int(lib().spo_f32_to_f16_bits(float(x)))
+
+
+def f16_bits_to_f32(h: int) -> float:
+    return float(lib().spo_f16_bits_to_f32(int(h) & 0xFFFF))
+
+
+def polar_record_bytes(head_dim: int) -> int:
+    """Bytes of one PolarQuant record: 2 (f16 magnitude) + ceil(head_dim / 2) (kv_cache.rs:441-443)."""
+    return int(lib().spo_polar_record_bytes(head_dim))
+
+
+def polar_compress(x: np.ndarray) -> np.ndarray:
+    """polar_quant_compress (kv_cache.rs:437-483) of the float32 rows of x [..., head_dim]:
+    uint8 records [..., record_bytes]."""
+    a = np.ascontiguousarray(x, dtype=np.float32)
+    d = a.shape[-1]
+    n = a.size // d if d else 0
+    out = np.zeros(a.shape[:-1] + (polar_record_bytes(d),), dtype=np.uint8)
+    lib().spo_polar_compress(_p(out), _p(a), n, d)
+    return out
+
+
+def polar_decompress(records: np.ndarray, head_dim: int) -> np.ndarray:
+    """polar_quant_decompress (kv_cache.rs:486-532): uint8 records [..., record_bytes] -> float32
+    rows [..., head_dim]."""
+    r = np.ascontiguousarray(records, dtype=np.uint8)
+    assert r.shape[-1] == polar_record_bytes(head_dim)
+    n = r.size // r.shape[-1]
+    out = np.zeros(r.shape[:-1] + (head_dim,), dtype=np.float32)
+    lib().spo_polar_decompress(_p(out), _p(r), n, head_dim)
+    return out
+
+
+def polar_compression_ratio(head_dim: int) -> float:
+    """KvQuantMethod::PolarQuant.compression_ratio (kv_cache.rs:315-318)."""
+    return float(lib().spo_polar_compression_ratio(head_dim))

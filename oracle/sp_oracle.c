@@ -476,3 +476,126 @@ int spo_rope_apply(float* x, int64_t tokens, int64_t heads, int64_t head_dim, in
 }
 
 #pragma GCC pop_options
+
+
+/* ---------------------------------------------------------------------------------------------
+ * PolarQuant codec of CompressedKvCache (crates/sketchpad-core/src/kv_cache.rs:437-532). Each
+ * head_dim vector becomes one record: its Euclidean norm as an IEEE binary16 (2 bytes, little
+ * endian) followed by ceil(head_dim / 2) bytes of 4-bit two's-complement direction codes, the
+ * even dimension of a pair in the high nibble. Compiled without contraction: the reference sums
+ * the squares as separate f32 products and additions.
+ * ------------------------------------------------------------------------------------------- */
+#pragma GCC push_options
+#pragma GCC optimize("fp-contract=off")
+
+/* binary32 -> binary16 bits, IEEE 754 round to nearest even: overflow to infinity, results below
+ * the smallest normal rounded to a subnormal (or zero), NaN kept quiet with its sign and top
+ * payload bits. This is the conversion the reference's f16::from_f32 performs (kv_cache.rs:449).
+ * Written from the format definition; the tests compare it with numpy's float16 conversion. */
+uint16_t spo_f32_to_f16_bits(float f) {
+  uint32_t x;
+  memcpy(&x, &f, 4);
+  const uint32_t sign = (x >> 16) & 0x8000u;
+  const int32_t exp = (int32_t)((x >> 23) & 0xffu);
+  uint32_t man = x & 0x7fffffu;
+  if (exp == 0xff) return (uint16_t)(sign | 0x7c00u | (man ? 0x0200u | (man >> 13) : 0u));
+  const int32_t e = exp - 127 + 15; /* binary16 biased exponent */
+  if (e >= 31) return (uint16_t)(sign | 0x7c00u);
+  if (e <= 0) {
+    /* subnormal result: value = M * 2^(exp-150) with M the 24-bit significand, in units of
+     * 2^-24 that is M >> (14 - e) */
+    if (e < -10) return (uint16_t)sign; /* below 2^-25: rounds to zero */
+    const uint32_t m = man | 0x800000u;
+    const int shift = 14 - e;
+    uint32_t r = m >> shift;
+    const uint32_t rem = m & ((1u << shift) - 1u), half = 1u << (shift - 1);
+    if (rem > half || (rem == half && (r & 1u))) ++r; /* may carry into the smallest normal */
+    return (uint16_t)(sign | r);
+  }
+  uint32_t r = ((uint32_t)e << 10) | (man >> 13);
+  const uint32_t rem = man & 0x1fffu;
+  if (rem > 0x1000u || (rem == 0x1000u && (r & 1u))) ++r; /* may carry into infinity */
+  return (uint16_t)(sign | r);
+}
+
+/* binary16 bits -> binary32 (exact). */
+float spo_f16_bits_to_f32(uint16_t h) {
+  const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+  const uint32_t exp = (h >> 10) & 0x1fu, man = h & 0x3ffu;
+  uint32_t x;
+  if (exp == 0x1f) {
+    x = sign | 0x7f800000u | (man << 13);
+  } else if (exp != 0) {
+    x = sign | ((exp + 112u) << 23) | (man << 13);
+  } else {
+    const float v = ldexpf((float)man, -24); /* subnormal (or zero): man * 2^-24, exact */
+    memcpy(&x, &v, 4);
+    x |= sign;
+  }
+  float f;
+  memcpy(&f, &x, 4);
+  return f;
+}
+
+/* One direction code: (d * 7.0).round().clamp(-7.0, 7.0) as i8 (kv_cache.rs:462-469). f32::round
+ * rounds half away from zero (C roundf); clamp keeps a NaN and `as i8` maps it to 0. */
+static int polar_code(float d) {
+  const float t = roundf(d * 7.0f);
+  if (t != t) return 0;
+  return t < -7.0f ? -7 : (t > 7.0f ? 7 : (int)t);
+}
+
+int64_t spo_polar_record_bytes(int64_t head_dim) { return 2 + (head_dim + 1) / 2; }
+
+/* polar_quant_compress (kv_cache.rs:437-483): num_vecs rows of head_dim f32 -> num_vecs records
+ * of spo_polar_record_bytes(head_dim) bytes. */
+void spo_polar_compress(uint8_t* out, const float* x, int64_t num_vecs, int64_t head_dim) {
+  const int64_t nb = (head_dim + 1) / 2, rec = 2 + nb;
+  for (int64_t i = 0; i < num_vecs; ++i) {
+    const float* r = x + i * head_dim;
+    uint8_t* o = out + i * rec;
+    float ss = 0.0f; /* Sum::<f32> over the squares: a left fold */
+    for (int64_t j = 0; j < head_dim; ++j) ss = ss + r[j] * r[j];
+    const float mag = sqrtf(ss);
+    const uint16_t mb = spo_f32_to_f16_bits(mag);
+    o[0] = (uint8_t)(mb & 0xffu);
+    o[1] = (uint8_t)(mb >> 8);
+    memset(o + 2, 0, (size_t)nb);
+    if (mag == 0.0f) continue;
+    const float inv = 1.0f / mag;
+    for (int64_t j = 0; j < head_dim; j += 2) {
+      const int q0 = polar_code(r[j] * inv);
+      const int q1 = j + 1 < head_dim ? polar_code(r[j + 1] * inv) : 0;
+      o[2 + j / 2] = (uint8_t)(((q0 & 0xf) << 4) | (q1 & 0xf));
+    }
+  }
+}
+
+/* 4-bit two's complement nibble -> integer (kv_cache.rs:510-528). */
+static int polar_nibble(unsigned raw) { return raw > 7 ? (int)raw - 16 : (int)raw; }
+
+/* polar_quant_decompress (kv_cache.rs:486-532): records -> num_vecs rows of head_dim f32,
+ * element = code * (magnitude / 7); a zero magnitude gives a zero row. */
+void spo_polar_decompress(float* out, const uint8_t* bytes, int64_t num_vecs, int64_t head_dim) {
+  const int64_t rec = spo_polar_record_bytes(head_dim);
+  for (int64_t i = 0; i < num_vecs; ++i) {
+    const uint8_t* b = bytes + i * rec;
+    float* o = out + i * head_dim;
+    const float mag = spo_f16_bits_to_f32((uint16_t)(b[0] | (b[1] << 8)));
+    for (int64_t j = 0; j < head_dim; ++j) o[j] = 0.0f;
+    if (mag == 0.0f) continue;
+    const float scale = mag / 7.0f;
+    for (int64_t j = 0; j < head_dim; j += 2) {
+      const uint8_t byte = b[2 + j / 2];
+      o[j] = (float)polar_nibble((byte >> 4) & 0xfu) * scale;
+      if (j + 1 < head_dim) o[j + 1] = (float)polar_nibble(byte & 0xfu) * scale;
+    }
+  }
+}
+
+/* KvQuantMethod::PolarQuant.compression_ratio (kv_cache.rs:315-318): (2 + D/2) / (2 D). */
+double spo_polar_compression_ratio(int64_t head_dim) {
+  return (2.0 + (double)head_dim / 2.0) / ((double)head_dim * 2.0);
+}
+
+#pragma GCC pop_options

@@ -39,6 +39,17 @@
  *               identity; rope.rs:180-230), complex multiplication (x0 + i x1) e^{i angle} in
  *               float64, pair norms preserved, rotating back by -angle restores x, and
  *               <R(m) q, R(n) k> depends only on m - n (float64)
+ *   spo_f32_to_f16_bits / spo_f16_bits_to_f32             f16::from_f32 / to_f32 (kv_cache.rs:449, :496)
+ *       pinned: numpy's float16 conversion (a library routine) on every binary16 value and on
+ *               ties, overflow, subnormal and NaN inputs
+ *   spo_polar_compress / spo_polar_decompress             kv_cache.rs:437-532 (PolarQuant)
+ *   spo_polar_record_bytes / spo_polar_compression_ratio  kv_cache.rs:441-443, :315-318
+ *       pinned: hand-derived records (one-hot, negative, zero, odd head_dim, a half-way code that
+ *               f32::round takes away from zero), decompress(compress(x)) within the closed-form
+ *               bound |x_j - x'_j| <= |x|/14 + (f16 rounding of |x|), codes = sign-correct
+ *               rounded 7 x_j/|x| (float64 brute force away from ties), record size against
+ *               compression_ratio for even head_dim (the reference test's QJL ratio at :871-876
+ *               pins the same formula's shape), NaN / infinity / zero rows
  *   spo_cpu_decode_baseline / spo_cpu_prefill_baseline    the reference's whole decode / prefill
  *       op sequence (store, gather+concat, repeat_kv, matmul, scale, mask, softmax, matmul), f32,
  *       OpenMP over sequences; pinned against spo_attention_f64.
@@ -126,6 +137,13 @@ void spo_rope_caches(float* cos_full, float* sin_full, int64_t rows, int64_t hea
 int spo_rope_apply(float* x, int64_t tokens, int64_t heads, int64_t head_dim, int64_t tok_stride,
                    int64_t head_stride, const int32_t* positions, const float* cos_full,
                    const float* sin_full, int64_t rows);
+
+uint16_t spo_f32_to_f16_bits(float f);
+float spo_f16_bits_to_f32(uint16_t h);
+int64_t spo_polar_record_bytes(int64_t head_dim);
+void spo_polar_compress(uint8_t* out, const float* x, int64_t num_vecs, int64_t head_dim);
+void spo_polar_decompress(float* out, const uint8_t* bytes, int64_t num_vecs, int64_t head_dim);
+double spo_polar_compression_ratio(int64_t head_dim);
 
 #ifdef __cplusplus
 }

@@ -22,6 +22,15 @@ from ._lib import (  # noqa: F401
     paged_decode,
     paged_decode_workspace_size,
     paged_prefill,
+    alloc_polar_pools,
+    polar_compress,
+    polar_decompress,
+    polar_kv_append,
+    polar_kv_export,
+    polar_kv_gather,
+    polar_paged_decode,
+    polar_pool_bytes,
+    polar_record_bytes,
     rope_kv_append,
     rope_tables,
     varlen_prefill,

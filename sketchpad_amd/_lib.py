@@ -81,6 +81,22 @@ _SIGNATURES = {
     "sp_flash_attention": (c_int32, [c_void_p, c_void_p, c_void_p, c_void_p, c_int32, c_int32,
                                      c_int32, c_int32, c_int32, c_float, c_int32, c_int32,
                                      c_void_p]),
+    "sp_polar_record_bytes": (c_int64, [c_int32]),
+    "sp_polar_pool_bytes": (c_size_t, [POINTER(CacheLayout)]),
+    "sp_polar_compress": (c_int32, [c_void_p, c_void_p, c_int64, c_int32, c_int32, c_void_p]),
+    "sp_polar_decompress": (c_int32, [c_void_p, c_void_p, c_int64, c_int32, c_int32, c_void_p]),
+    "sp_polar_kv_append": (c_int32, [c_void_p, c_void_p, POINTER(CacheLayout), c_void_p,
+                                     c_void_p, c_int64, c_int64, c_void_p, c_int32, c_int32,
+                                     c_void_p]),
+    "sp_polar_kv_gather": (c_int32, [c_void_p, c_void_p, c_void_p, c_void_p,
+                                     POINTER(CacheLayout), c_void_p, c_int32, c_int32, c_int32,
+                                     c_void_p]),
+    "sp_polar_kv_export": (c_int32, [c_void_p, c_void_p, c_void_p, c_void_p,
+                                     POINTER(CacheLayout), c_void_p, c_int32, c_int32, c_void_p]),
+    "sp_polar_paged_decode": (c_int32, [c_void_p, c_void_p, c_void_p, c_void_p,
+                                        POINTER(CacheLayout), c_void_p, c_int32, c_void_p,
+                                        c_int32, c_int32, c_int32, c_float, c_int32, c_int32,
+                                        c_void_p, c_size_t, c_void_p]),
 }
 
 _lib = None
@@ -249,3 +265,82 @@ def flash_attention(out, q, k, v, scale: float, *, causal: bool = False, stream=
     b, h, sq, d = q.shape
     check(load().sp_flash_attention(_ptr(out), _ptr(q), _ptr(k), _ptr(v), b, h, sq, k.shape[2],
                                     d, scale, int(bool(causal)), sp_dtype(q), _stream(stream)))
+
+
+# ---------------------------------------------------------------------------------------------
+# PolarQuant compressed paged cache (KvQuantMethod::PolarQuant, kv_cache.rs:437-532)
+# ---------------------------------------------------------------------------------------------
+
+def polar_record_bytes(head_dim: int) -> int:
+    """sp_polar_record_bytes: 2 + ceil(head_dim / 2)."""
+    return int(load().sp_polar_record_bytes(head_dim))
+
+
+def polar_pool_bytes(lay: CacheLayout) -> int:
+    """sp_polar_pool_bytes: bytes of one paged PolarQuant pool (K or V) for this layout."""
+    n = int(load().sp_polar_pool_bytes(ctypes.byref(lay)))
+    if n == 0:
+        raise SketchpadError(SP_EUNSUPPORTED, load().sp_last_error().decode())
+    return n
+
+
+def alloc_polar_pools(lay: CacheLayout, device="cuda"):
+    """Zeroed uint8 K and V PolarQuant pools for this layout."""
+    torch = _torch()
+    n = polar_pool_bytes(lay)
+    return (torch.zeros(n, dtype=torch.uint8, device=device),
+            torch.zeros(n, dtype=torch.uint8, device=device))
+
+
+def polar_compress(records, x, *, stream=None) -> None:
+    """sp_polar_compress: x [..., D] contiguous -> records [..., record_bytes] uint8."""
+    d = x.shape[-1]
+    check(load().sp_polar_compress(_ptr(records), _ptr(x), x.numel() // d, d, sp_dtype(x),
+                                   _stream(stream)))
+
+
+def polar_decompress(out, records, *, stream=None) -> None:
+    """sp_polar_decompress: records [..., record_bytes] -> out [..., D] (its dtype)."""
+    d = out.shape[-1]
+    check(load().sp_polar_decompress(_ptr(out), _ptr(records), out.numel() // d, d,
+                                     sp_dtype(out), _stream(stream)))
+
+
+def polar_kv_append(k_pool, v_pool, lay: CacheLayout, k_new, v_new, slot_mapping, *,
+                    token_stride: int | None = None, head_stride: int | None = None,
+                    stream=None) -> None:
+    """sp_polar_kv_append. k_new/v_new default to token-major [T, Hkv, D] contiguous tensors."""
+    ts = token_stride if token_stride is not None else lay.num_kv_heads * lay.head_dim
+    hs = head_stride if head_stride is not None else lay.head_dim
+    check(load().sp_polar_kv_append(_ptr(k_pool), _ptr(v_pool), ctypes.byref(lay),
+                                    _ptr(k_new), _ptr(v_new), ts, hs, _ptr(slot_mapping),
+                                    slot_mapping.numel(), sp_dtype(k_new), _stream(stream)))
+
+
+def polar_kv_gather(k_out, v_out, k_pool, v_pool, lay: CacheLayout, block_table, seq_len: int, *,
+                    stream=None) -> None:
+    """sp_polar_kv_gather: decompressed [Hkv, seq_len, D] in k_out's dtype."""
+    check(load().sp_polar_kv_gather(_ptr(k_out), _ptr(v_out), _ptr(k_pool), _ptr(v_pool),
+                                    ctypes.byref(lay), _ptr(block_table), block_table.numel(),
+                                    seq_len, sp_dtype(k_out), _stream(stream)))
+
+
+def polar_kv_export(k_rec, v_rec, k_pool, v_pool, lay: CacheLayout, block_table, seq_len: int, *,
+                    stream=None) -> None:
+    """sp_polar_kv_export: records [Hkv, seq_len, record_bytes] uint8."""
+    check(load().sp_polar_kv_export(_ptr(k_rec), _ptr(v_rec), _ptr(k_pool), _ptr(v_pool),
+                                    ctypes.byref(lay), _ptr(block_table), block_table.numel(),
+                                    seq_len, _stream(stream)))
+
+
+def polar_paged_decode(out, q, k_pool, v_pool, lay: CacheLayout, block_tables, context_lens,
+                       max_context_len: int, scale: float, *, window_left: int = -1,
+                       workspace=None, stream=None) -> None:
+    """sp_polar_paged_decode (workspace as for paged_decode)."""
+    num_seqs, hq = q.shape[0], q.shape[1]
+    ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    check(load().sp_polar_paged_decode(_ptr(out), _ptr(q), _ptr(k_pool), _ptr(v_pool),
+                                       ctypes.byref(lay), _ptr(block_tables),
+                                       block_tables.shape[1], _ptr(context_lens),
+                                       max_context_len, num_seqs, hq, scale, window_left,
+                                       sp_dtype(q), _ptr(workspace), ws_bytes, _stream(stream)))

@@ -10,6 +10,7 @@
 
 #include "kv_cache.hpp"
 #include "paged_decode.hpp"
+#include "polar_cache.hpp"
 #include "prefill.hpp"
 #include "rope_append.hpp"
 #include "sp_common.hpp"
@@ -210,13 +211,14 @@ size_t sp_paged_decode_workspace_size(int32_t num_seqs, int32_t num_q_heads,
   return p.ws_bytes;
 }
 
-int sp_paged_decode(void* out, const void* q, const void* k_pool, const void* v_pool,
-                    const sp_cache_layout* layout, const int32_t* block_tables,
-                    int32_t max_blocks_per_seq, const int32_t* context_lens,
-                    int32_t max_context_len, int32_t num_seqs, int32_t num_q_heads, float scale,
-                    int32_t window_left, sp_dtype dtype, void* workspace, size_t workspace_bytes,
-                    void* stream) {
-  const char* fn = "sp_paged_decode";
+// Validation and arguments shared by the dense and the PolarQuant decode entry points. The pool
+// strides are left to the caller.
+static int decode_setup(const char* fn, void* out, const void* q, const void* k_pool,
+                        const void* v_pool, const sp_cache_layout* layout,
+                        const int32_t* block_tables, int32_t max_blocks_per_seq,
+                        const int32_t* context_lens, int32_t max_context_len, int32_t num_seqs,
+                        int32_t num_q_heads, float scale, int32_t window_left, sp_dtype dtype,
+                        void* workspace, size_t workspace_bytes, DecodeArgs* a) {
   if (int rc = check_layout(layout, fn)) return rc;
   if (int rc = check_dtype(dtype, fn)) return rc;
   if (num_seqs < 0 || num_q_heads <= 0 || max_context_len < 0 || max_blocks_per_seq < 0)
@@ -254,29 +256,43 @@ int sp_paged_decode(void* out, const void* q, const void* k_pool, const void* v_
                 p.ws_bytes);
   if (((uintptr_t)q | (uintptr_t)k_pool | (uintptr_t)v_pool | (uintptr_t)workspace) & 15)
     return fail(SP_EINVAL, "%s: q, pools and workspace must be 16-byte aligned", fn);
-  const int es = dtype_size(dtype);
+  a->out = out;
+  a->q = q;
+  a->kpool = (const char*)k_pool;
+  a->vpool = (const char*)v_pool;
+  a->block_tables = block_tables;
+  a->context_lens = context_lens;
+  a->partials = (float*)workspace;
+  a->max_blocks_per_seq = max_blocks_per_seq;
+  a->max_context_len = max_context_len;
+  a->num_blocks = layout->num_blocks;
+  a->block_size = layout->block_size;
+  a->num_seqs = num_seqs;
+  a->hq = num_q_heads;
+  a->hkv = hkv;
+  a->group = group;
+  a->window_left = window_left;
+  a->tps = p.tps;
+  a->max_splits = p.max_splits;
+  a->scale_log2 = scale * 1.4426950408889634f;
+  return SP_OK;
+}
+
+int sp_paged_decode(void* out, const void* q, const void* k_pool, const void* v_pool,
+                    const sp_cache_layout* layout, const int32_t* block_tables,
+                    int32_t max_blocks_per_seq, const int32_t* context_lens,
+                    int32_t max_context_len, int32_t num_seqs, int32_t num_q_heads, float scale,
+                    int32_t window_left, sp_dtype dtype, void* workspace, size_t workspace_bytes,
+                    void* stream) {
   DecodeArgs a{};
-  a.out = out;
-  a.q = q;
-  a.kpool = (const char*)k_pool;
-  a.vpool = (const char*)v_pool;
-  a.block_tables = block_tables;
-  a.context_lens = context_lens;
-  a.partials = (float*)workspace;
-  pool_strides(layout, es, &a.block_stride_b, &a.layer_off_b);
-  a.max_blocks_per_seq = max_blocks_per_seq;
-  a.max_context_len = max_context_len;
-  a.num_blocks = layout->num_blocks;
-  a.block_size = layout->block_size;
-  a.num_seqs = num_seqs;
-  a.hq = num_q_heads;
-  a.hkv = hkv;
-  a.group = group;
-  a.window_left = window_left;
-  a.tps = p.tps;
-  a.max_splits = p.max_splits;
-  a.scale_log2 = scale * 1.4426950408889634f;
-  return launch_paged_decode(a, dtype, D, (hipStream_t)stream);
+  if (int rc = decode_setup("sp_paged_decode", out, q, k_pool, v_pool, layout, block_tables,
+                            max_blocks_per_seq, context_lens, max_context_len, num_seqs,
+                            num_q_heads, scale, window_left, dtype, workspace, workspace_bytes,
+                            &a))
+    return rc;
+  if (num_seqs == 0) return SP_OK;
+  pool_strides(layout, dtype_size(dtype), &a.block_stride_b, &a.layer_off_b);
+  return launch_paged_decode(a, dtype, layout->head_dim, (hipStream_t)stream);
 }
 
 static int check_prefill_common(const char* fn, int32_t num_seqs, int32_t max_seqlen_q,
@@ -417,6 +433,167 @@ int sp_flash_attention(void* out, const void* q, const void* k, const void* v, i
   a.window_left = -1;
   a.scale_log2 = scale * 1.4426950408889634f;
   return launch_prefill(a, dtype, head_dim, false, (hipStream_t)stream);
+}
+
+// ---------------------------------------------------------------------------------------------
+// PolarQuant compressed paged cache
+// ---------------------------------------------------------------------------------------------
+int64_t sp_polar_record_bytes(int32_t head_dim) {
+  if (head_dim <= 0) return -1;
+  return 2 + ((int64_t)head_dim + 1) / 2;
+}
+
+static int check_polar_layout(const sp_cache_layout* l, const char* fn) {
+  if (int rc = check_layout(l, fn)) return rc;
+  if (l->head_dim & 1)
+    return fail(SP_EUNSUPPORTED, "%s: a paged PolarQuant pool needs an even head_dim (got %d)",
+                fn, l->head_dim);
+  if (l->block_size % 4)
+    return fail(SP_EUNSUPPORTED,
+                "%s: a paged PolarQuant pool needs block_size a multiple of 4 (got %d)", fn,
+                l->block_size);
+  return SP_OK;
+}
+
+static void polar_strides(const sp_cache_layout* l, int64_t* block_stride_b,
+                          int64_t* layer_off_b) {
+  const int64_t layer_b = (int64_t)l->num_kv_heads * polar_region_bytes(l->block_size, l->head_dim);
+  *block_stride_b = layer_b * l->num_layers;
+  *layer_off_b = layer_b * l->layer;
+}
+
+size_t sp_polar_pool_bytes(const sp_cache_layout* layout) {
+  if (check_polar_layout(layout, "sp_polar_pool_bytes")) return 0;
+  int64_t stride, off;
+  polar_strides(layout, &stride, &off);
+  return (size_t)stride * (size_t)layout->num_blocks;
+}
+
+int sp_polar_compress(void* records, const void* x, int64_t num_vecs, int32_t head_dim,
+                      sp_dtype dtype, void* stream) {
+  const char* fn = "sp_polar_compress";
+  if (int rc = check_dtype(dtype, fn)) return rc;
+  if (num_vecs < 0 || head_dim <= 0)
+    return fail(SP_EINVAL, "%s: num_vecs %lld, head_dim %d", fn, (long long)num_vecs, head_dim);
+  if (num_vecs == 0) return SP_OK;
+  if (!records || !x) return fail(SP_EINVAL, "%s: NULL pointer argument", fn);
+  if ((uintptr_t)x % dtype_size(dtype))
+    return fail(SP_EINVAL, "%s: x is not aligned to its element type", fn);
+  return launch_polar_compress(records, x, num_vecs, head_dim, dtype, (hipStream_t)stream);
+}
+
+int sp_polar_decompress(void* out, const void* records, int64_t num_vecs, int32_t head_dim,
+                        sp_dtype dtype, void* stream) {
+  const char* fn = "sp_polar_decompress";
+  if (int rc = check_dtype(dtype, fn)) return rc;
+  if (num_vecs < 0 || head_dim <= 0)
+    return fail(SP_EINVAL, "%s: num_vecs %lld, head_dim %d", fn, (long long)num_vecs, head_dim);
+  if (num_vecs == 0) return SP_OK;
+  if (!records || !out) return fail(SP_EINVAL, "%s: NULL pointer argument", fn);
+  if ((uintptr_t)out % dtype_size(dtype))
+    return fail(SP_EINVAL, "%s: out is not aligned to its element type", fn);
+  return launch_polar_decompress(out, records, num_vecs, head_dim, dtype, (hipStream_t)stream);
+}
+
+int sp_polar_kv_append(void* k_pool, void* v_pool, const sp_cache_layout* layout,
+                       const void* k_new, const void* v_new, int64_t token_stride,
+                       int64_t head_stride, const int32_t* slot_mapping, int32_t num_tokens,
+                       sp_dtype dtype, void* stream) {
+  const char* fn = "sp_polar_kv_append";
+  if (int rc = check_polar_layout(layout, fn)) return rc;
+  if (int rc = check_dtype(dtype, fn)) return rc;
+  if (num_tokens < 0) return fail(SP_EINVAL, "%s: num_tokens %d < 0", fn, num_tokens);
+  if (num_tokens == 0) return SP_OK;
+  if (!k_pool || !v_pool || !k_new || !v_new || !slot_mapping)
+    return fail(SP_EINVAL, "%s: NULL pointer argument", fn);
+  if (token_stride < 0 || head_stride < 0) return fail(SP_EINVAL, "%s: negative stride", fn);
+  if (((uintptr_t)k_pool | (uintptr_t)v_pool) & 15)
+    return fail(SP_EINVAL, "%s: pools must be 16-byte aligned", fn);
+  if (((uintptr_t)k_new | (uintptr_t)v_new) % dtype_size(dtype))
+    return fail(SP_EINVAL, "%s: k_new / v_new are not aligned to their element type", fn);
+  PolarAppendArgs a{};
+  a.kpool = (char*)k_pool;
+  a.vpool = (char*)v_pool;
+  a.knew = (const char*)k_new;
+  a.vnew = (const char*)v_new;
+  a.tok_stride_e = token_stride;
+  a.head_stride_e = head_stride;
+  a.slots = slot_mapping;
+  polar_strides(layout, &a.block_stride_b, &a.layer_off_b);
+  a.num_slots = (int64_t)layout->num_blocks * layout->block_size;
+  a.num_tokens = num_tokens;
+  a.hkv = layout->num_kv_heads;
+  a.head_dim = layout->head_dim;
+  a.block_size = layout->block_size;
+  return launch_polar_append(a, dtype, (hipStream_t)stream);
+}
+
+static int polar_gather_common(const char* fn, void* k_out, void* v_out, const void* k_pool,
+                               const void* v_pool, const sp_cache_layout* layout,
+                               const int32_t* block_table, int32_t num_table_blocks,
+                               int32_t seq_len, int dtype, void* stream) {
+  if (int rc = check_polar_layout(layout, fn)) return rc;
+  if (seq_len < 0) return fail(SP_EINVAL, "%s: seq_len %d < 0", fn, seq_len);
+  if (seq_len == 0) return SP_OK;
+  if (!k_out || !v_out || !k_pool || !v_pool || !block_table)
+    return fail(SP_EINVAL, "%s: NULL pointer argument", fn);
+  if (((uintptr_t)k_pool | (uintptr_t)v_pool) & 15)
+    return fail(SP_EINVAL, "%s: pools must be 16-byte aligned", fn);
+  if (dtype >= 0 && ((uintptr_t)k_out | (uintptr_t)v_out) % dtype_size((sp_dtype)dtype))
+    return fail(SP_EINVAL, "%s: outputs are not aligned to their element type", fn);
+  const int64_t needed = ((int64_t)seq_len + layout->block_size - 1) / layout->block_size;
+  if (num_table_blocks < needed)
+    return fail(SP_EOOB, "%s: seq_len %d needs %lld blocks, the table holds %d", fn, seq_len,
+                (long long)needed, num_table_blocks);
+  PolarGatherArgs a{};
+  a.kout = (char*)k_out;
+  a.vout = (char*)v_out;
+  a.kpool = (const char*)k_pool;
+  a.vpool = (const char*)v_pool;
+  a.table = block_table;
+  polar_strides(layout, &a.block_stride_b, &a.layer_off_b);
+  a.seq_len = seq_len;
+  a.hkv = layout->num_kv_heads;
+  a.head_dim = layout->head_dim;
+  a.block_size = layout->block_size;
+  a.num_blocks = layout->num_blocks;
+  return launch_polar_gather(a, dtype, (hipStream_t)stream);
+}
+
+int sp_polar_kv_gather(void* k_out, void* v_out, const void* k_pool, const void* v_pool,
+                       const sp_cache_layout* layout, const int32_t* block_table,
+                       int32_t num_table_blocks, int32_t seq_len, sp_dtype dtype, void* stream) {
+  const char* fn = "sp_polar_kv_gather";
+  if (int rc = check_dtype(dtype, fn)) return rc;
+  return polar_gather_common(fn, k_out, v_out, k_pool, v_pool, layout, block_table,
+                             num_table_blocks, seq_len, (int)dtype, stream);
+}
+
+int sp_polar_kv_export(void* k_records, void* v_records, const void* k_pool, const void* v_pool,
+                       const sp_cache_layout* layout, const int32_t* block_table,
+                       int32_t num_table_blocks, int32_t seq_len, void* stream) {
+  return polar_gather_common("sp_polar_kv_export", k_records, v_records, k_pool, v_pool, layout,
+                             block_table, num_table_blocks, seq_len, -1, stream);
+}
+
+int sp_polar_paged_decode(void* out, const void* q, const void* k_pool, const void* v_pool,
+                          const sp_cache_layout* layout, const int32_t* block_tables,
+                          int32_t max_blocks_per_seq, const int32_t* context_lens,
+                          int32_t max_context_len, int32_t num_seqs, int32_t num_q_heads,
+                          float scale, int32_t window_left, sp_dtype dtype, void* workspace,
+                          size_t workspace_bytes, void* stream) {
+  const char* fn = "sp_polar_paged_decode";
+  if (dtype != SP_BF16 && dtype != SP_F16)
+    return fail(dtype == SP_F32 ? SP_EUNSUPPORTED : SP_EINVAL,
+                "%s: dtype %d has no kernel (bf16, f16)", fn, (int)dtype);
+  DecodeArgs a{};
+  if (int rc = decode_setup(fn, out, q, k_pool, v_pool, layout, block_tables, max_blocks_per_seq,
+                            context_lens, max_context_len, num_seqs, num_q_heads, scale,
+                            window_left, dtype, workspace, workspace_bytes, &a))
+    return rc;
+  if (num_seqs == 0) return SP_OK;
+  polar_strides(layout, &a.block_stride_b, &a.layer_off_b);
+  return launch_polar_decode(a, dtype, layout->head_dim, (hipStream_t)stream);
 }
 
 }  // extern "C"

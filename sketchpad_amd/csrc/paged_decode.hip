@@ -453,6 +453,28 @@ static int launch_t(const DecodeArgs& a, int head_dim, hipStream_t stream) {
   }
 }
 
+template <typename T>
+static int combine_t(const DecodeArgs& a, int head_dim, hipStream_t stream) {
+  const dim3 grid(a.hq, a.num_seqs);
+  if (head_dim == 64)
+    hipLaunchKernelGGL((decode_combine_kernel<T, 64>), grid, dim3(64), 0, stream, a);
+  else if (head_dim == 128)
+    hipLaunchKernelGGL((decode_combine_kernel<T, 128>), grid, dim3(64), 0, stream, a);
+  else
+    return fail(SP_EUNSUPPORTED, "decode combine: head_dim %d has no kernel", head_dim);
+  return check_launch("decode_combine_kernel");
+}
+
+int launch_decode_combine(const DecodeArgs& a, sp_dtype dtype, int head_dim, hipStream_t stream) {
+  if (a.max_splits <= 1) return SP_OK;
+  switch (dtype) {
+    case SP_F32: return combine_t<float>(a, head_dim, stream);
+    case SP_BF16: return combine_t<bf16_t>(a, head_dim, stream);
+    case SP_F16: return combine_t<f16_t>(a, head_dim, stream);
+  }
+  return fail(SP_EUNSUPPORTED, "decode combine: dtype %d has no kernel", (int)dtype);
+}
+
 int launch_paged_decode(const DecodeArgs& a, sp_dtype dtype, int head_dim, hipStream_t stream) {
   switch (dtype) {
     case SP_F32: return launch_t<float>(a, head_dim, stream);

@@ -46,4 +46,8 @@ struct DecodeArgs {
 
 int launch_paged_decode(const DecodeArgs& a, sp_dtype dtype, int head_dim, hipStream_t stream);
 
+// The split merge alone (no-op when a.max_splits <= 1): for kernels that write the same
+// (m, l, acc[D]) partials in 16-token tiles.
+int launch_decode_combine(const DecodeArgs& a, sp_dtype dtype, int head_dim, hipStream_t stream);
+
 }  // namespace sp

@@ -83,6 +83,22 @@ class DecodeWorkload:
         e = self.elem_bytes
         return self.num_seqs * self.hkv * self.head_dim * e * 2 * 2 + self.num_seqs * 4
 
+    def polar_record_bytes(self) -> int:
+        """PolarQuant record of one vector: binary16 norm + head_dim/2 code bytes."""
+        return 2 + self.head_dim // 2
+
+    def polar_decode_bytes(self) -> int:
+        """decode_bytes with every attended K/V row read as a PolarQuant record."""
+        kv = int(self.attended_keys().sum()) * 2 * self.hkv * self.polar_record_bytes()
+        return self.decode_bytes() - int(self.attended_keys().sum()) * 2 * self.hkv * \
+            self.head_dim * self.elem_bytes + kv
+
+    def polar_append_bytes(self) -> int:
+        """Encode on append: read one K and one V row per sequence and KV head, write their
+        records, plus the slot mapping."""
+        return self.num_seqs * self.hkv * 2 * (self.head_dim * self.elem_bytes +
+                                               self.polar_record_bytes()) + self.num_seqs * 4
+
     def layout(self):
         from ._lib import layout
         return layout(self.num_blocks, self.num_layers, self.layer, self.hkv, self.block_size,

@@ -121,6 +121,45 @@ def test_rope_validation(sp_lib):
     assert t(None, None, 0, 8, ctypes.c_float(10000.0)) == 0
 
 
+def test_polar_pool_bytes_and_validation(sp_lib):
+    lay = _lay(num_blocks=10, num_layers=3, num_kv_heads=4, block_size=16, head_dim=128)
+    # regions of BS * (D/2 + 2) bytes per (block, layer, KV head)
+    assert sp_lib.sp_polar_pool_bytes(ctypes.byref(lay)) == 10 * 3 * 4 * 16 * 66
+    assert sp_lib.sp_polar_pool_bytes(ctypes.byref(_lay(head_dim=63))) == 0
+    assert sp_lib.sp_polar_pool_bytes(ctypes.byref(_lay(block_size=6))) == 0
+    fake = ctypes.c_void_p(0x1000)
+    app = sp_lib.sp_polar_kv_append
+    _expect(_lib.SP_EUNSUPPORTED, app(fake, fake, ctypes.byref(_lay(head_dim=63)), fake, fake,
+                                      128, 64, fake, 1, 1, None), "even head_dim")
+    _expect(_lib.SP_EUNSUPPORTED, app(fake, fake, ctypes.byref(_lay(block_size=6)), fake, fake,
+                                      128, 64, fake, 1, 1, None), "multiple of 4")
+    _expect(_lib.SP_EINVAL, app(ctypes.c_void_p(0x1008), fake, ctypes.byref(_lay()), fake, fake,
+                                128, 64, fake, 1, 1, None), "16-byte aligned")
+    _expect(_lib.SP_EINVAL, app(fake, fake, ctypes.byref(_lay()), fake, fake, 128, 64, None, 1,
+                                1, None), "NULL")
+    assert app(None, None, ctypes.byref(_lay()), None, None, 0, 0, None, 0, 1, None) == 0
+    gat = sp_lib.sp_polar_kv_gather
+    _expect(_lib.SP_EOOB, gat(fake, fake, fake, fake, ctypes.byref(_lay()), fake, 1, 17, 1, None),
+            "needs 2 blocks")
+    exp = sp_lib.sp_polar_kv_export
+    _expect(_lib.SP_EOOB, exp(fake, fake, fake, fake, ctypes.byref(_lay()), fake, 1, 17, None),
+            "needs 2 blocks")
+    comp = sp_lib.sp_polar_compress
+    _expect(_lib.SP_EINVAL, comp(fake, fake, 4, 0, 0, None), "head_dim 0")
+    _expect(_lib.SP_EINVAL, comp(fake, ctypes.c_void_p(0x1001), 4, 8, 0, None), "aligned")
+    assert comp(None, None, 0, 8, 0, None) == 0
+    dec = sp_lib.sp_polar_paged_decode
+
+    def call(lay, dtype=1, hq=4, max_ctx=32, mbs=2):
+        return dec(fake, fake, fake, fake, ctypes.byref(lay), fake, mbs, fake, max_ctx, 3, hq,
+                   0.125, -1, dtype, None, 0, None)
+
+    _expect(_lib.SP_EUNSUPPORTED, call(_lay(), dtype=0), "bf16, f16")
+    _expect(_lib.SP_EUNSUPPORTED, call(_lay(head_dim=96)), "head_dim 96")
+    _expect(_lib.SP_EUNSUPPORTED, call(_lay(block_size=8), mbs=4), "block_size 8")
+    _expect(_lib.SP_EINVAL, call(_lay(), hq=3), "multiple")
+
+
 def test_workspace_size_monotone(sp_lib):
     lay = _lay(num_blocks=100000, num_kv_heads=8, head_dim=128)
     sizes = [sp_lib.sp_paged_decode_workspace_size(64, 32, L, -1, ctypes.byref(lay))
