@@ -218,7 +218,8 @@ static int decode_setup(const char* fn, void* out, const void* q, const void* k_
                         const int32_t* block_tables, int32_t max_blocks_per_seq,
                         const int32_t* context_lens, int32_t max_context_len, int32_t num_seqs,
                         int32_t num_q_heads, float scale, int32_t window_left, sp_dtype dtype,
-                        void* workspace, size_t workspace_bytes, DecodeArgs* a) {
+                        void* workspace, size_t workspace_bytes, DecodeArgs* a,
+                        int max_tps = 32, int cap = 64) {
   if (int rc = check_layout(layout, fn)) return rc;
   if (int rc = check_dtype(dtype, fn)) return rc;
   if (num_seqs < 0 || num_q_heads <= 0 || max_context_len < 0 || max_blocks_per_seq < 0)
@@ -247,7 +248,7 @@ static int decode_setup(const char* fn, void* out, const void* q, const void* k_
   if (!isfinite(scale)) return fail(SP_EINVAL, "%s: scale is not finite", fn);
   const DecodePlan p =
       plan_decode(num_seqs, num_q_heads, hkv, D, max_context_len < 1 ? 1 : max_context_len,
-                  window_left);
+                  window_left, max_tps, cap);
   if (layout->block_size % p.tt != 0)
     return fail(SP_EUNSUPPORTED, "%s: block_size %d is not a multiple of the %d-token tile", fn,
                 layout->block_size, p.tt);
@@ -587,9 +588,11 @@ int sp_polar_paged_decode(void* out, const void* q, const void* k_pool, const vo
     return fail(dtype == SP_F32 ? SP_EUNSUPPORTED : SP_EINVAL,
                 "%s: dtype %d has no kernel (bf16, f16)", fn, (int)dtype);
   DecodeArgs a{};
+  // a compressed tile is a quarter of a dense one: splits of up to 64 tiles (never more splits
+  // than the dense plan, so sp_paged_decode_workspace_size covers this call too)
   if (int rc = decode_setup(fn, out, q, k_pool, v_pool, layout, block_tables, max_blocks_per_seq,
                             context_lens, max_context_len, num_seqs, num_q_heads, scale,
-                            window_left, dtype, workspace, workspace_bytes, &a))
+                            window_left, dtype, workspace, workspace_bytes, &a, 64, 128))
     return rc;
   if (num_seqs == 0) return SP_OK;
   polar_strides(layout, &a.block_stride_b, &a.layer_off_b);

@@ -408,7 +408,7 @@ __global__ void __launch_bounds__(64) decode_combine_kernel(DecodeArgs a) {
 }
 
 DecodePlan plan_decode(int num_seqs, int hq, int hkv, int head_dim, int max_context_len,
-                       int window_left) {
+                       int window_left, int max_tps, int cap) {
   DecodePlan p{};
   p.group = hkv > 0 ? hq / hkv : 0;
   p.tt = kTile;
@@ -418,10 +418,10 @@ DecodePlan plan_decode(int num_seqs, int hq, int hkv, int head_dim, int max_cont
     if (wt < max_tiles) max_tiles = wt;
   }
   p.max_tiles = max_tiles < 1 ? 1 : max_tiles;
-  int tps = 32;  // 512 tokens per split, 8 tiles per wave
+  int tps = max_tps < kDecodeWaves ? kDecodeWaves : (max_tps > cap ? cap : max_tps);
   const char* env = getenv("SP_DECODE_TPS");
   if (env && atoi(env) > 0) {
-    tps = atoi(env) < kDecodeWaves ? kDecodeWaves : (atoi(env) > 64 ? 64 : atoi(env));
+    tps = atoi(env) < kDecodeWaves ? kDecodeWaves : (atoi(env) > cap ? cap : atoi(env));
   } else {
     const int64_t units = (int64_t)num_seqs * (hkv > 0 ? hkv : 1);
     while (tps > kDecodeWaves && units * ((p.max_tiles + tps - 1) / tps) < 2048)

@@ -253,7 +253,8 @@ __global__ void __launch_bounds__(256) polar_gather_kernel(PolarGatherArgs a) {
 // ---------------------------------------------------------------------------------------------
 // Decode attention on the codes
 // ---------------------------------------------------------------------------------------------
-constexpr int kPTile = 16;  // tokens per tile (the plan of paged_decode.hip)
+constexpr int kPTile = 16;     // tokens per tile (the plan of paged_decode.hip)
+constexpr float kLazy = 8.0f;  // running-max slack of the lazy rescaling (log2 units)
 
 template <typename T> struct PolarQk;
 template <> struct PolarQk<bf16_t> {
@@ -350,6 +351,20 @@ __global__ void __launch_bounds__(64 * kDecodeWaves, 4) polar_decode_kernel(Deco
   const int seq = unit / a.hkv, kvh = unit - seq * a.hkv;
   const int G = a.group;
 
+  // Block ids of the split's tiles: lane j holds tile t_begin + j in blk0 and t_begin + 64 + j in
+  // blk1 (tps <= 128), so no tile load waits on a dependent block-table read. Without a window
+  // t_begin = split * tps does not depend on the context length, and the table read is issued
+  // together with it (one memory round trip before the first tile instead of two).
+  const int32_t* table = a.block_tables + (int64_t)seq * a.max_blocks_per_seq;
+  auto fetch_blocks = [&](int t0, int n_tiles, int& b0, int& b1) {
+    const int i0 = ((t0 + lane) * kPTile) / a.block_size;
+    const int i1 = ((t0 + 64 + lane) * kPTile) / a.block_size;
+    b0 = (lane < n_tiles && i0 < a.max_blocks_per_seq) ? table[i0] : 0;
+    b1 = (lane + 64 < n_tiles && i1 < a.max_blocks_per_seq) ? table[i1] : 0;
+  };
+  int blk0 = 0, blk1 = 0;
+  if (a.window_left < 0) fetch_blocks(split * a.tps, a.tps, blk0, blk1);
+
   int L = a.context_lens[seq];
   L = min(L, min(a.max_context_len, a.max_blocks_per_seq * a.block_size));
   if (L <= 0) {
@@ -365,6 +380,7 @@ __global__ void __launch_bounds__(64 * kDecodeWaves, 4) polar_decode_kernel(Deco
   if (split >= nsplit) return;
   const int t_begin = first_tile + split * a.tps;
   const int t_end = min(t_begin + a.tps, last_tile + 1);
+  if (a.window_left >= 0) fetch_blocks(t_begin, t_end - t_begin, blk0, blk1);
 
   // Q^T operand in the unpack order: for word c of lane (g, n), pairs P..P+3 with
   // P = g * HB/4 + 4c hold dimensions 2P..2P+7, and the unpacked elements are dimensions
@@ -383,6 +399,12 @@ __global__ void __launch_bounds__(64 * kDecodeWaves, 4) polar_decode_kernel(Deco
       r.y = (x.x & 0xffffu) | (x.z << 16);           // (d0, d4)
       r.z = (x.y >> 16) | (x.w & 0xffff0000u);       // (d3, d7)
       r.w = (x.y & 0xffffu) | (x.w << 16);           // (d2, d6)
+      // a negative scale is carried by q's sign (exact), so the scores scale by |scale| below
+      const uint32_t flip = a.scale_log2 < 0.f ? 0x80008000u : 0u;
+      r.x ^= flip;
+      r.y ^= flip;
+      r.z ^= flip;
+      r.w ^= flip;
       qv[c] = real ? r : make_uint4(0, 0, 0, 0);
       if (real) {
         qsum += (Dot2<T>::lo(x.x) + Dot2<T>::hi(x.x)) + (Dot2<T>::lo(x.y) + Dot2<T>::hi(x.y)) +
@@ -392,20 +414,17 @@ __global__ void __launch_bounds__(64 * kDecodeWaves, 4) polar_decode_kernel(Deco
   }
   qsum += pxor16(qsum);
   qsum += pxor32(qsum);
+  if (a.scale_log2 < 0.f) qsum = -qsum;
   const float s_init = -PolarQk<T>::kBias * qsum;
-  const float ck = a.scale_log2 * (1.0f / 7.0f);
+  const f32x4_v s0 = {s_init, s_init, s_init, s_init};
+  // score_j (log2 units) = (q . n_j) * |k_j| * ck; the 1/7 of the V side is applied at the end
+  // (at least FLT_MIN, so a masked -inf score stays -inf even for a zero scale)
+  const float ck = fmaxf(fabsf(a.scale_log2) * (1.0f / 7.0f), 1.17549435e-38f);
   // A operand of the sum(P') MFMA: row 0 of V^T all ones (bf16 1.0), other rows zero
   const uint2 ones_row0 = n == 0 ? make_uint2(0x3f803f80u, 0x3f803f80u) : make_uint2(0u, 0u);
 
-  const int32_t* table = a.block_tables + (int64_t)seq * a.max_blocks_per_seq;
   const int64_t head_off = a.layer_off_b + (int64_t)kvh * polar_region_bytes(a.block_size, D);
   const int mag_off = a.block_size * HB;
-
-  int my_blk = 0;
-  {
-    const int tj = t_begin + lane;
-    if (lane < t_end - t_begin) my_blk = table[(tj * kPTile) / a.block_size];
-  }
 
   // One tile's loads: lane (g, n) holds 16 (D=64: 8) bytes of token n's K code row, 16 (8)
   // bytes of the V token-quad g, and the binary16 norms of tokens 4g..4g+3.
@@ -414,15 +433,26 @@ __global__ void __launch_bounds__(64 * kDecodeWaves, 4) polar_decode_kernel(Deco
     uint2 km, vm;
     bool ok;
   };
+  // per-lane byte offsets inside a tile (the tile's base is wave-uniform: scalar address math)
+  const uint32_t k_lane = n * HB + g * (HB / 4);
+  const uint32_t v_lane = g * HB * 4 + n * (4 * NW);
+  const uint32_t m_lane = 8 * g;
   auto load_tile = [&](int t, Stage& s) {
-    const int blk = __builtin_amdgcn_readlane(my_blk, t - t_begin);
+    const int ti = t - t_begin;
+    const int b0 = __builtin_amdgcn_readlane(blk0, ti & 63);
+    const int b1 = __builtin_amdgcn_readlane(blk1, ti & 63);
+    const int blk = ti < 64 ? b0 : b1;
     s.ok = blk >= 0 && blk < a.num_blocks;
     const int sl0 = (t * kPTile) % a.block_size;
     const int64_t base = (int64_t)(s.ok ? blk : 0) * a.block_stride_b + head_off;
-    s.kw = *(const W*)(a.kpool + base + (int64_t)(sl0 + n) * HB + g * (HB / 4));
-    s.vw = *(const W*)(a.vpool + base + (int64_t)((sl0 >> 2) + g) * HB * 4 + n * (4 * NW));
-    s.km = *(const uint2*)(a.kpool + base + mag_off + 2 * (sl0 + 4 * g));
-    s.vm = *(const uint2*)(a.vpool + base + mag_off + 2 * (sl0 + 4 * g));
+    const char* kt = a.kpool + (base + (int64_t)sl0 * HB);
+    const char* vt = a.vpool + (base + (int64_t)(sl0 >> 2) * HB * 4);
+    const char* kmt = a.kpool + (base + mag_off + 2 * sl0);
+    const char* vmt = a.vpool + (base + mag_off + 2 * sl0);
+    s.kw = *(const W*)(kt + k_lane);
+    s.vw = *(const W*)(vt + v_lane);
+    s.km = *(const uint2*)(kmt + m_lane);
+    s.vm = *(const uint2*)(vmt + m_lane);
   };
 
   float m_run = -INFINITY, l_run = 0.f;
@@ -434,37 +464,52 @@ __global__ void __launch_bounds__(64 * kDecodeWaves, 4) polar_decode_kernel(Deco
 
   auto process = [&](int t, const Stage& cur) {
     // S^T = K Q^T - B sum(q): tokens 4g..4g+3 of the tile for head n
-    f32x4_v s = {s_init, s_init, s_init, s_init};
+    f32x4_v s = PolarQk<T>::qk(polar_unpack(CW::get(cur.kw, 0), PolarQk<T>::kKey), qv[0], s0);
 #pragma unroll
-    for (int c = 0; c < NW; ++c)
+    for (int c = 1; c < NW; ++c)
       s = PolarQk<T>::qk(polar_unpack(CW::get(cur.kw, c), PolarQk<T>::kKey), qv[c], s);
 
     const int rel0 = t * kPTile + 4 * g - start_tok;
-    float sv[4], mv[4];
+    float u[4], mv[4];  // u_j = (q . n_j) |k_j| (times ck: log2 units); mv_j = |v_j|
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const bool valid = cur.ok && (unsigned)(rel0 + j) < span;
-      const uint32_t kb = (j < 2 ? cur.km.x : cur.km.y) >> (16 * (j & 1));
-      const uint32_t vb = (j < 2 ? cur.vm.x : cur.vm.y) >> (16 * (j & 1));
-      sv[j] = valid ? s[j] * (f16_bits_to_f32((uint16_t)kb) * ck) : -INFINITY;
-      mv[j] = valid ? f16_bits_to_f32((uint16_t)vb) * (1.0f / 7.0f) : 0.f;
+      u[j] = s[j] * f16_bits_to_f32((uint16_t)((j < 2 ? cur.km.x : cur.km.y) >> (16 * (j & 1))));
+      mv[j] = f16_bits_to_f32((uint16_t)((j < 2 ? cur.vm.x : cur.vm.y) >> (16 * (j & 1))));
     }
-    float mt = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
+    const int rel_tile = t * kPTile - start_tok;  // wave-uniform
+    if (!(cur.ok && rel_tile >= 0 && rel_tile + kPTile <= (int)span)) {
+      // a tile that straddles start_tok or L, or an invalid block: mask its tokens (score -inf,
+      // |v| 0). The empty asm keeps this a branch: full tiles do no masking work.
+      asm volatile("");
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const bool valid = cur.ok && (unsigned)(rel0 + j) < span;
+        u[j] = valid ? u[j] : -INFINITY;
+        mv[j] = valid ? mv[j] : 0.f;
+      }
+    }
+    // Lazy rescaling: the running max m_run (log2 units) is raised (and acc, corr, l rescaled)
+    // only when a head's tile max exceeds it by more than kLazy; otherwise the weights
+    // exp2(score - m_run) stay below 2^kLazy, well inside fp32 and bf16 range. Any reference max
+    // gives the same acc / l; the merge and the split combine use each wave's own m_run.
+    float mt = fmaxf(fmaxf(u[0], u[1]), fmaxf(u[2], u[3]));
     mt = fmaxf(mt, pxor16(mt));
     mt = fmaxf(mt, pxor32(mt));
-    const float m_new = fmaxf(m_run, mt);
-    const float alpha = (m_run == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m_run - m_new);
-    float p[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-      p[j] = (sv[j] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(sv[j] - m_new);
-    l_run = l_run * alpha + ((p[0] + p[1]) + (p[2] + p[3]));
-    m_run = m_new;
-    if (__builtin_amdgcn_ballot_w64(alpha != 1.f)) {
+    mt *= ck;
+    if (__builtin_amdgcn_ballot_w64(mt > m_run + kLazy)) {
+      const float m_new = fmaxf(m_run, mt);
+      const float alpha = (m_run == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m_run - m_new);
 #pragma unroll
       for (int i = 0; i < ND; ++i) acc[i] *= alpha;
       corr[0] *= alpha;
+      l_run *= alpha;
+      m_run = m_new;
     }
+    const float m_use = (m_run == -INFINITY) ? 0.f : m_run;
+    float p[4];  // a masked token (u = -inf) gets exp2(-inf) = 0
+#pragma unroll
+    for (int j = 0; j < 4; ++j) p[j] = __builtin_amdgcn_exp2f(fmaf(u[j], ck, -m_use));
+    l_run += (p[0] + p[1]) + (p[2] + p[3]);
 
     // P'^T in the token order of the V unpack: (t0, t2), (t1, t3)
     const uint2 pp = make_uint2(pack_bf16(p[0] * mv[0], p[2] * mv[2]),
@@ -480,25 +525,30 @@ __global__ void __launch_bounds__(64 * kDecodeWaves, 4) polar_decode_kernel(Deco
 
   // The wave's tiles t_begin + wave + 4i through a ring of kRing register stages: a stage is
   // refilled with the tile kRing steps ahead as soon as its tile is consumed, so kRing - 1 tiles
-  // stay in flight while one is computed.
+  // stay in flight while one is computed. The refill is unconditional (past the wave's last tile
+  // it reloads the tile just consumed, which is cached and never processed): loads under a
+  // condition would make the compiler wait for every outstanding load before each tile.
   constexpr int kRing = 3, kStep = kDecodeWaves * kRing;
+  const int t_first = t_begin + wave;
   Stage st[kRing];
 #pragma unroll
-  for (int r = 0; r < kRing; ++r)
-    if (t_begin + wave + kDecodeWaves * r < t_end) load_tile(t_begin + wave + kDecodeWaves * r, st[r]);
-  for (int tb = t_begin + wave; tb < t_end; tb += kStep) {
+  for (int r = 0; r < kRing; ++r) {
+    const int tr = t_first + kDecodeWaves * r;
+    load_tile(tr < t_end ? tr : t_begin, st[r]);
+  }
+  for (int tb = t_first; tb < t_end; tb += kStep) {
 #pragma unroll
     for (int r = 0; r < kRing; ++r) {
       const int t = tb + kDecodeWaves * r;
-      if (t < t_end) {
-        process(t, st[r]);
-        if (t + kStep < t_end) load_tile(t + kStep, st[r]);
-      }
+      if (t < t_end) process(t, st[r]);
+      load_tile(t + kStep < t_end ? t + kStep : (t < t_end ? t : t_begin), st[r]);
     }
   }
 
-  // Remove the V bias: row 0 of corr (lane (0, n)) holds sum(P') of head n.
+  // Remove the V bias (row 0 of corr, lane (0, n), holds sum(P') of head n) and apply the 1/7
+  // of |v| / 7.
   const float cn = kVBias * __shfl(corr[0], n, 64);
+  constexpr float kSeventh = 1.0f / 7.0f;
   l_run += pxor16(l_run);
   l_run += pxor32(l_run);
   __syncthreads();
@@ -515,8 +565,8 @@ __global__ void __launch_bounds__(64 * kDecodeWaves, 4) polar_decode_kernel(Deco
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int pr = NW * (4 * g + r) + i;
-      ca[(wave * 16 + n) * D + 2 * pr + 1] = acc[2 * i][r] - cn;
-      ca[(wave * 16 + n) * D + 2 * pr] = acc[2 * i + 1][r] - cn;
+      ca[(wave * 16 + n) * D + 2 * pr + 1] = (acc[2 * i][r] - cn) * kSeventh;
+      ca[(wave * 16 + n) * D + 2 * pr] = (acc[2 * i + 1][r] - cn) * kSeventh;
     }
   __syncthreads();
 
