@@ -34,6 +34,7 @@ typedef _Float16 f16x8_v __attribute__((ext_vector_type(8)));
 typedef short s16x4_v __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x4_v __attribute__((ext_vector_type(4)));
 typedef float f32x4_v __attribute__((ext_vector_type(4)));
+typedef float f32x2_v __attribute__((ext_vector_type(2)));
 
 constexpr int kTile = 16;  // tokens per tile
 
@@ -47,8 +48,8 @@ template <> struct DecodeMfma<bf16_t> {
     return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4_v, v),
                                                      __builtin_bit_cast(s16x4_v, p), c, 0, 0, 0);
   }
-  __device__ __forceinline__ static uint32_t pack(float lo, float hi) {
-    return (uint32_t)f32_to_bf16_bits(lo) | ((uint32_t)f32_to_bf16_bits(hi) << 16);
+  __device__ __forceinline__ static uint32_t pack(float lo, float hi) {  // v_cvt_pk_bf16_f32 (RNE)
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_v){lo, hi}, bf16x2_v));
   }
 };
 template <> struct DecodeMfma<f16_t> {
@@ -60,8 +61,8 @@ template <> struct DecodeMfma<f16_t> {
     return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4_v, v),
                                                  __builtin_bit_cast(f16x4_v, p), c, 0, 0, 0);
   }
-  __device__ __forceinline__ static uint32_t pack(float lo, float hi) {
-    return (uint32_t)f32_to_f16_bits(lo) | ((uint32_t)f32_to_f16_bits(hi) << 16);
+  __device__ __forceinline__ static uint32_t pack(float lo, float hi) {  // RNE
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_v){lo, hi}, f16x2_v));
   }
 };
 
@@ -137,6 +138,9 @@ __global__ void __launch_bounds__(64 * kDecodeWaves, decode_min_waves<T>())
     if (split == 0) {
       for (int i = threadIdx.x; i < G * D; i += blockDim.x)
         Elem<T>::store(a.out, ((int64_t)seq * a.hq + kvh * G) * D + i, 0.f);
+      if (a.max_splits > 1 && threadIdx.x < G)  // split count 0: nothing for the combine
+        a.partials[((int64_t)seq * a.hq + kvh * G + threadIdx.x) * a.max_splits * (D + 4) + 2] =
+            0.f;
     }
     return;
   }
@@ -351,42 +355,48 @@ __global__ void __launch_bounds__(64 * kDecodeWaves, decode_min_waves<T>())
       }
       pp[4 + d] = asum;
     }
+    // word 2 of split 0's record: the split count, read by the combine in the same round trip as
+    // the partials (1: the output is final)
+    if (split == 0 && d == 0 && a.max_splits > 1)
+      a.partials[((int64_t)seq * a.hq + hq) * a.max_splits * (D + 4) + 2] = (float)nsplit;
   }
 }
 
 // Merge the per-split partials (m, l, acc[D]) of sequences that needed more than one split.
-// One wave per (query head, sequence). Every partial's (m, l) and the lane's D/64 accumulator
-// columns are loaded in one batch (up to 16 splits per pass), so the merge waits on two memory
-// round trips: the context length, then the partials.
+// One wave per (query head, sequence). The split count (word 2 of split 0's record, written by
+// the decode kernel) and the first 16 splits' (m, l) and the lane's D/64 accumulator columns are
+// loaded together, so the merge waits on a single memory round trip; slots past the split count
+// may hold stale data from earlier calls and are masked out.
 template <typename T, int D>
 __global__ void __launch_bounds__(64) decode_combine_kernel(DecodeArgs a) {
   constexpr int DPL = D / 64;
   constexpr int B = 16;  // splits per batch
   const int hq = blockIdx.x, seq = blockIdx.y, lane = threadIdx.x;
-  int L = a.context_lens[seq];
-  L = min(L, min(a.max_context_len, a.max_blocks_per_seq * a.block_size));
-  if (L <= 0) return;
-  const int start_tok = a.window_left >= 0 ? max(0, L - 1 - a.window_left) : 0;
-  const int nsplit = ((L - 1) / kTile - start_tok / kTile + a.tps) / a.tps;
-  if (nsplit <= 1) return;
   const float* pp = a.partials + ((int64_t)seq * a.hq + hq) * a.max_splits * (D + 4);
   float M = -INFINITY, lsum = 0.f;
   float acc[DPL];
 #pragma unroll
   for (int e = 0; e < DPL; ++e) acc[e] = 0.f;
+  int nsplit = B;  // refined by the header once the first batch is in
   for (int s0 = 0; s0 < nsplit; s0 += B) {
     float ms[B], ls[B], v[B][DPL];
+    const float hdr = pp[2];
 #pragma unroll
     for (int u = 0; u < B; ++u) {
-      const float* src = pp + min(s0 + u, nsplit - 1) * (D + 4);
-      ms[u] = (s0 + u < nsplit) ? src[0] : -INFINITY;
+      const float* src = pp + min(s0 + u, a.max_splits - 1) * (D + 4);
+      ms[u] = src[0];
       ls[u] = src[1];
 #pragma unroll
       for (int e = 0; e < DPL; ++e) v[u][e] = src[4 + lane * DPL + e];
     }
+    nsplit = (int)hdr;
+    if (nsplit <= 1) return;  // output written by the decode kernel (or an empty context)
     float mb = M;
 #pragma unroll
-    for (int u = 0; u < B; ++u) mb = fmaxf(mb, ms[u]);
+    for (int u = 0; u < B; ++u) {
+      if (s0 + u >= nsplit) ms[u] = -INFINITY;
+      mb = fmaxf(mb, ms[u]);
+    }
     if (mb == -INFINITY) continue;
     const float alpha = (M == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(M - mb);
     lsum *= alpha;
@@ -394,7 +404,8 @@ __global__ void __launch_bounds__(64) decode_combine_kernel(DecodeArgs a) {
     for (int e = 0; e < DPL; ++e) acc[e] *= alpha;
 #pragma unroll
     for (int u = 0; u < B; ++u) {
-      const float w = (ms[u] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(ms[u] - mb);
+      if (ms[u] == -INFINITY) continue;
+      const float w = __builtin_amdgcn_exp2f(ms[u] - mb);
       lsum = fmaf(ls[u], w, lsum);
 #pragma unroll
       for (int e = 0; e < DPL; ++e) acc[e] = fmaf(v[u][e], w, acc[e]);

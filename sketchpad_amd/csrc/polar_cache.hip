@@ -371,6 +371,9 @@ __global__ void __launch_bounds__(64 * kDecodeWaves, 4) polar_decode_kernel(Deco
     if (split == 0) {
       for (int i = threadIdx.x; i < G * D; i += blockDim.x)
         Elem<T>::store(a.out, ((int64_t)seq * a.hq + kvh * G) * D + i, 0.f);
+      if (a.max_splits > 1 && threadIdx.x < G)  // split count 0: nothing for the combine
+        a.partials[((int64_t)seq * a.hq + kvh * G + threadIdx.x) * a.max_splits * (D + 4) + 2] =
+            0.f;
     }
     return;
   }
@@ -596,6 +599,10 @@ __global__ void __launch_bounds__(64 * kDecodeWaves, 4) polar_decode_kernel(Deco
       }
       pp[4 + d] = asum;
     }
+    // word 2 of split 0's record: the split count, read by the combine in the same round trip as
+    // the partials (1: the output is final)
+    if (split == 0 && d == 0 && a.max_splits > 1)
+      a.partials[((int64_t)seq * a.hq + hq) * a.max_splits * (D + 4) + 2] = (float)nsplit;
   }
 }
 
