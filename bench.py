@@ -62,6 +62,9 @@ def parse_args():
                     help="skip the PolarQuant compressed-cache decode leg")
     ap.add_argument("--polar-only", action="store_true",
                     help="only the decode config's PolarQuant leg (profiling)")
+    ap.add_argument("--layer", action="store_true",
+                    help="also time a whole attention layer (projections + RoPE append + "
+                         "attention) on the C2 decode step and the C3 prefill")
     ap.add_argument("--secondary", action="store_true",
                     help="also time the other decode configs (C4, C5) and report them")
     return ap.parse_args()
@@ -312,6 +315,111 @@ def time_prefill_c3(steps: int, warmup: int):
     }
 
 
+def time_layer(steps: int, warmup: int, hidden: int = 4096):
+    """One whole attention layer of the Llama-3-8B shape (hidden 4096): q and k|v projections
+    (sp_linear), RoPE fused into the append (sp_rope_kv_append), attention, o projection — on the
+    C2 decode step (64 tokens, sp_paged_decode) and on the C3 prefill (9,476 tokens,
+    sp_paged_prefill through the pool). Returns per-part HIP-event times; random weights,
+    synthetic inputs."""
+    import torch
+    import sketchpad_amd as sp
+    from sketchpad_amd import workloads as W
+
+    stream = torch.cuda.current_stream()
+    s = stream.cuda_stream
+    res = {}
+    for name in ("decode_C2", "prefill_C3"):
+        if name == "decode_C2":
+            w = W.decode_c2()
+            t = W.make_decode_tensors(w)
+            T, hq, hkv, d = w.num_seqs, w.hq, w.hkv, w.head_dim
+            lay = w.layout()
+            positions = torch.from_numpy((w.context_lens - 1).astype(np.int32)).cuda()
+            slots, k_pool, v_pool = t["slot_mapping"], t["k_pool"], t["v_pool"]
+            ws = sp.alloc_decode_workspace(T, hq, w.max_context_len, -1, lay)
+            rows = w.max_context_len
+            attn_bytes = w.decode_bytes()
+        else:
+            w = W.prefill_c3()
+            t = W.make_prefill_tensors(w)
+            T, hq, hkv, d = w.total_tokens, w.hq, w.hkv, w.head_dim
+            lay = sp.layout(t["num_blocks"], 1, 0, hkv, w.block_size, d)
+            positions = torch.from_numpy(
+                np.concatenate([np.arange(L) for L in w.lens]).astype(np.int32)).cuda()
+            slots, k_pool, v_pool = t["slot_mapping"], t["k_pool"], t["v_pool"]
+            rows = int(w.lens.max())
+        dt = W.torch_dtype("bf16")
+        g = torch.Generator(device="cuda").manual_seed(7)
+        x = torch.randn(T, hidden, generator=g, device="cuda").to(dt)
+        # weights [out, in]
+        wq = (torch.randn(hq * d, hidden, generator=g, device="cuda") * hidden ** -0.5).to(dt)
+        wkv = (torch.randn(2 * hkv * d, hidden, generator=g, device="cuda") * hidden ** -0.5).to(dt)
+        wo = (torch.randn(hidden, hq * d, generator=g, device="cuda") * (hq * d) ** -0.5).to(dt)
+        q = torch.empty(T, hq, d, dtype=dt, device="cuda")
+        kv = torch.empty(T, 2 * hkv * d, dtype=dt, device="cuda")
+        attn = torch.empty(T, hq, d, dtype=dt, device="cuda")
+        out = torch.empty(T, hidden, dtype=dt, device="cuda")
+        lws = sp.alloc_linear_workspace([(T, hidden, hq * d), (T, hidden, 2 * hkv * d),
+                                         (T, hq * d, hidden)])
+        cos, sin = sp.rope_tables(rows, d, 500000.0)
+        cos_d, sin_d = torch.from_numpy(cos).cuda(), torch.from_numpy(sin).cuda()
+
+        def qkv():
+            sp.linear(q, x, wq, workspace=lws, stream=s)
+            sp.linear(kv, x, wkv, workspace=lws, stream=s)
+
+        def rope_append():
+            sp.rope_kv_append(k_pool, v_pool, lay, kv[:, :hkv * d], kv[:, hkv * d:], positions,
+                              slots, cos_d, sin_d, q=q, token_stride=2 * hkv * d, head_stride=d,
+                              stream=s)
+
+        if name == "decode_C2":
+            def attention():
+                sp.paged_decode(attn, q, k_pool, v_pool, lay, t["block_tables"],
+                                t["context_lens"], w.max_context_len, d ** -0.5, workspace=ws,
+                                stream=s)
+        else:
+            lens_d = torch.from_numpy(w.lens.astype(np.int32)).cuda()
+
+            def attention():  # the new tokens attend through the pool they were appended to
+                sp.paged_prefill(attn, q, k_pool, v_pool, lay, t["block_tables"], t["cu_seqlens"],
+                                 lens_d, w.max_seqlen, d ** -0.5, stream=s)
+
+        def o_proj():
+            sp.linear(out, attn.view(T, hq * d), wo, workspace=lws, stream=s)
+
+        def layer():
+            qkv()
+            rope_append()
+            attention()
+            o_proj()
+
+        for _ in range(warmup):
+            layer()
+        torch.cuda.synchronize()
+        n = max(10, steps // 2)
+        parts = {k: _event_times(stream, f, n)[0]
+                 for k, f in (("qkv_proj", qkv), ("rope_append", rope_append),
+                              ("attention", attention), ("o_proj", o_proj), ("layer", layer))}
+        wbytes = hidden * (hq + 2 * hkv) * d * 2
+        obytes = hq * d * hidden * 2
+        entry = {k + "_ms": round(v, 5) for k, v in parts.items()}
+        entry["tokens"] = T
+        entry["qkv_proj_TFLOPs"] = round(2 * T * hidden * (hq + 2 * hkv) * d /
+                                         (parts["qkv_proj"] * 1e-3) / 1e12, 2)
+        entry["o_proj_TFLOPs"] = round(2 * T * hq * d * hidden / (parts["o_proj"] * 1e-3) / 1e12, 2)
+        entry["qkv_proj_weight_GBs"] = round(wbytes / (parts["qkv_proj"] * 1e-3) / 1e9, 2)
+        entry["o_proj_weight_GBs"] = round(obytes / (parts["o_proj"] * 1e-3) / 1e9, 2)
+        if name == "decode_C2":
+            entry["attention_GBs"] = round(attn_bytes / (parts["attention"] * 1e-3) / 1e9, 2)
+        else:
+            entry["attention_TFLOPs"] = round(w.flops() / (parts["attention"] * 1e-3) / 1e12, 2)
+        entry["attention_share"] = round(parts["attention"] / parts["layer"], 3)
+        res[name] = entry
+        del t
+    return res
+
+
 def time_chunked_c4(steps: int, warmup: int):
     """C4 prefill half: 4 chunks of 512 new tokens against paged contexts (sp_paged_prefill)."""
     import torch
@@ -449,6 +557,8 @@ def main():
         line["prefill"] = pf
     if args.secondary:
         line.setdefault("secondary", {})["C4-chunked-prefill"] = time_chunked_c4(10, 2)
+    if args.layer or args.secondary:
+        line["layer"] = time_layer(args.steps, 3)
     if args.secondary:
         sec = {}
         for name in ("C4", "C5", "C1"):

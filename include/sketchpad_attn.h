@@ -315,6 +315,38 @@ int sp_polar_paged_decode(void* out, const void* q,
                           float scale, int32_t window_left, sp_dtype dtype,
                           void* workspace, size_t workspace_bytes, void* stream);
 
+/*
+ * ---- Projections on either side of the path ------------------------------------------------
+ * y[M, N] = x[M, K] . w[N, K]^T (+ bias[N]): burn's nn::Linear as MultiHeadAttention applies it
+ * for q_proj / k_proj / v_proj (transformer.rs:196-208) and o_proj (:249-253). The weight is
+ * taken [out, in] = [N, K] (K contiguous, the PyTorch / Hugging Face layout); burn stores it
+ * [in, out] = [K, N], which sp_linear_weight_nk turns into [N, K] once at load time.
+ * Row-major contiguous x, w, y; dtype f32 / bf16 / f16. The product accumulates in fp32 and is
+ * rounded once to dtype (the reference upcasts f16 activations to f32 for these projections and
+ * casts back); a bias is then added in fp32 and rounded again (matmul, then + bias, as two ops).
+ * bias may be NULL. bf16 / f16: K % 8 == 0 and x, w 16-byte aligned (else SP_EUNSUPPORTED /
+ * SP_EINVAL); M <= 65535 * 64. Hand-written MFMA kernels; no library GEMM is called.
+ *   workspace : optional device scratch (16-byte aligned) for split-K partials. Skinny shapes
+ *               (few output tiles, long K) split K over workgroups when the workspace holds
+ *               the fp32 partials, sp_linear_workspace_size(M, K, N) bytes for the full split;
+ *               a smaller (or NULL) workspace caps the split. Partials are summed in a fixed
+ *               order: the result is a deterministic function of the inputs, the shape and
+ *               workspace_bytes. Calls sharing one workspace must not overlap.
+ */
+size_t sp_linear_workspace_size(int64_t M, int64_t K, int64_t N);
+int sp_linear(void* y, const void* x, const void* w, const void* bias,
+              int64_t M, int64_t K, int64_t N, sp_dtype dtype,
+              void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * dst[N, K] = src[K, N]^T: burn's [in, out] Linear weight (transformer.rs:75-86 builds the
+ * projections with LinearConfig; burn keeps the weight as [d_input, d_output]) into sp_linear's
+ * [out, in].
+ * One pass, done once when weights are loaded; dst and src must not alias.
+ */
+int sp_linear_weight_nk(void* dst, const void* src, int64_t K, int64_t N, sp_dtype dtype,
+                        void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -22,7 +22,11 @@ from ._lib import (  # noqa: F401
     paged_decode,
     paged_decode_workspace_size,
     paged_prefill,
+    alloc_linear_workspace,
     alloc_polar_pools,
+    linear,
+    linear_weight_nk,
+    linear_workspace_size,
     polar_compress,
     polar_decompress,
     polar_kv_append,

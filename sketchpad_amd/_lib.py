@@ -97,6 +97,10 @@ _SIGNATURES = {
                                         POINTER(CacheLayout), c_void_p, c_int32, c_void_p,
                                         c_int32, c_int32, c_int32, c_float, c_int32, c_int32,
                                         c_void_p, c_size_t, c_void_p]),
+    "sp_linear_workspace_size": (c_size_t, [c_int64, c_int64, c_int64]),
+    "sp_linear": (c_int32, [c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int64,
+                            c_int32, c_void_p, c_size_t, c_void_p]),
+    "sp_linear_weight_nk": (c_int32, [c_void_p, c_void_p, c_int64, c_int64, c_int32, c_void_p]),
 }
 
 _lib = None
@@ -344,3 +348,42 @@ def polar_paged_decode(out, q, k_pool, v_pool, lay: CacheLayout, block_tables, c
                                        block_tables.shape[1], _ptr(context_lens),
                                        max_context_len, num_seqs, hq, scale, window_left,
                                        sp_dtype(q), _ptr(workspace), ws_bytes, _stream(stream)))
+
+
+# ---------------------------------------------------------------------------------------------
+# Projections (burn's nn::Linear in MultiHeadAttention, transformer.rs:196-208, :249-253)
+# ---------------------------------------------------------------------------------------------
+
+def linear_workspace_size(m: int, k: int, n: int) -> int:
+    """Bytes of split-K partials sp_linear uses for this shape (0: it does not split)."""
+    return int(load().sp_linear_workspace_size(m, k, n))
+
+
+def alloc_linear_workspace(shapes, device="cuda"):
+    """A device workspace large enough for every (M, K, N) in shapes (at least 16 bytes)."""
+    torch = _torch()
+    need = max([16] + [linear_workspace_size(*s) for s in shapes])
+    return torch.empty(need, dtype=torch.uint8, device=device)
+
+
+def linear(y, x, w, bias=None, *, workspace=None, stream=None) -> None:
+    """sp_linear: y[M, N] = x[M, K] @ w[N, K]^T (+ bias[N]); w is [out, in] (PyTorch layout);
+    contiguous row-major tensors."""
+    k = x.shape[-1]
+    m = x.numel() // k
+    n = w.shape[0]
+    if w.numel() != n * k or y.numel() != m * n:
+        raise ValueError(f"linear: x {tuple(x.shape)}, w {tuple(w.shape)}, y {tuple(y.shape)}")
+    ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    check(load().sp_linear(_ptr(y), _ptr(x), _ptr(w), _ptr(bias), m, k, n, sp_dtype(x),
+                           _ptr(workspace), ws_bytes, _stream(stream)))
+
+
+def linear_weight_nk(w_kn, *, stream=None):
+    """sp_linear_weight_nk: burn's [in, out] weight -> a new [out, in] tensor."""
+    torch = _torch()
+    k, n = w_kn.shape
+    dst = torch.empty(n, k, dtype=w_kn.dtype, device=w_kn.device)
+    check(load().sp_linear_weight_nk(_ptr(dst), _ptr(w_kn), k, n, sp_dtype(w_kn),
+                                     _stream(stream)))
+    return dst

@@ -9,6 +9,7 @@
 #include <string>
 
 #include "kv_cache.hpp"
+#include "linear.hpp"
 #include "paged_decode.hpp"
 #include "polar_cache.hpp"
 #include "prefill.hpp"
@@ -597,6 +598,60 @@ int sp_polar_paged_decode(void* out, const void* q, const void* k_pool, const vo
   if (num_seqs == 0) return SP_OK;
   polar_strides(layout, &a.block_stride_b, &a.layer_off_b);
   return launch_polar_decode(a, dtype, layout->head_dim, (hipStream_t)stream);
+}
+
+// ---------------------------------------------------------------------------------------------
+// Projections
+// ---------------------------------------------------------------------------------------------
+size_t sp_linear_workspace_size(int64_t M, int64_t K, int64_t N) {
+  if (M <= 0 || K <= 0 || N <= 0) return 0;
+  return plan_linear(M, K, N, SIZE_MAX).ws_bytes;
+}
+
+int sp_linear(void* y, const void* x, const void* w, const void* bias, int64_t M, int64_t K,
+              int64_t N, sp_dtype dtype, void* workspace, size_t workspace_bytes, void* stream) {
+  const char* fn = "sp_linear";
+  if (int rc = check_dtype(dtype, fn)) return rc;
+  if (M < 0 || K <= 0 || N <= 0)
+    return fail(SP_EINVAL, "%s: M=%lld K=%lld N=%lld", fn, (long long)M, (long long)K,
+                (long long)N);
+  if (M == 0) return SP_OK;
+  if (!y || !x || !w) return fail(SP_EINVAL, "%s: NULL pointer argument", fn);
+  if (M > kLinearMaxRows || K > INT32_MAX || N > INT32_MAX)
+    return fail(SP_EUNSUPPORTED, "%s: M past %lld or K / N past 2^31", fn,
+                (long long)kLinearMaxRows);
+  const int es = dtype_size(dtype);
+  if (((uintptr_t)y | (uintptr_t)bias) % es)
+    return fail(SP_EINVAL, "%s: y / bias are not aligned to the element type", fn);
+  if (dtype == SP_F32) {
+    if (((uintptr_t)x | (uintptr_t)w) % 4)
+      return fail(SP_EINVAL, "%s: x / w are not aligned to the element type", fn);
+  } else {
+    if (K % 8)
+      return fail(SP_EUNSUPPORTED, "%s: K = %lld is not a multiple of 8 (16-byte rows)", fn,
+                  (long long)K);
+    if (((uintptr_t)x | (uintptr_t)w) % 16)
+      return fail(SP_EINVAL, "%s: x / w are not 16-byte aligned", fn);
+  }
+  if (workspace && (uintptr_t)workspace % 16)
+    return fail(SP_EINVAL, "%s: workspace is not 16-byte aligned", fn);
+  return launch_linear(y, x, w, bias, M, K, N, dtype, workspace, workspace ? workspace_bytes : 0,
+                       (hipStream_t)stream);
+}
+
+int sp_linear_weight_nk(void* dst, const void* src, int64_t K, int64_t N, sp_dtype dtype,
+                        void* stream) {
+  const char* fn = "sp_linear_weight_nk";
+  if (int rc = check_dtype(dtype, fn)) return rc;
+  if (K <= 0 || N <= 0)
+    return fail(SP_EINVAL, "%s: K=%lld N=%lld", fn, (long long)K, (long long)N);
+  if (!dst || !src) return fail(SP_EINVAL, "%s: NULL pointer argument", fn);
+  if (dst == src) return fail(SP_EINVAL, "%s: dst and src must not alias", fn);
+  if (K > 65535LL * 32 || N > INT32_MAX)
+    return fail(SP_EUNSUPPORTED, "%s: K past 65535 * 32 or N past 2^31", fn);
+  if (((uintptr_t)dst | (uintptr_t)src) % dtype_size(dtype))
+    return fail(SP_EINVAL, "%s: pointers are not aligned to the element type", fn);
+  return launch_weight_transpose(dst, src, K, N, dtype, (hipStream_t)stream);
 }
 
 }  // extern "C"
