@@ -11,7 +11,8 @@ namespace sp {
 constexpr int64_t kLinearMaxRows = 65535LL * 64;
 
 struct LinearPlan {
-  int tile_m;      // 128 (large M) or 64 (M <= 64)
+  bool big;        // 256 x 256 tiles (M >= 512, K % 64 == 0)
+  int tile_m;      // 256, 128 or 64 (M <= 64)
   int splits;      // split-K factor (1: no partials)
   int64_t k_per_split;
   size_t ws_bytes; // fp32 partials [splits][M][N] when splits > 1

@@ -40,7 +40,6 @@ typedef float pf_f32x16 __attribute__((ext_vector_type(16)));
 typedef short pf_s16x4 __attribute__((ext_vector_type(4)));
 typedef short pf_s16x8 __attribute__((ext_vector_type(8)));
 typedef __attribute__((address_space(3))) pf_s16x4 lds_s16x4;
-typedef __attribute__((address_space(3))) void lds_void;
 
 template <typename T> struct PrefillMfma;
 template <> struct PrefillMfma<bf16_t> {
@@ -107,24 +106,6 @@ __device__ __forceinline__ void swap_halves(float x, float& a, float& b) {
                                                   false);
   a = __uint_as_float(r[0]);
   b = __uint_as_float(r[1]);
-}
-
-// s_waitcnt vmcnt(0) expcnt(7) lgkmcnt(15): wait for every outstanding vector memory access of
-// this wave (gfx9 encoding: vmcnt in bits [3:0] and [15:14], expcnt [6:4], lgkmcnt [11:8]).
-constexpr int kWaitVmcnt0 = 0x0F70;
-
-// global_load_lds_dwordx4: every lane copies 16 bytes from `src` to LDS at lds_dst + 16 * lane
-// (lds_dst wave-uniform). Issued through inline asm so that the compiler does not guard the
-// LDS reads of the other buffer with waits on these loads; completion is awaited explicitly
-// (s_waitcnt vmcnt(0) + barrier) before the tile is read.
-__device__ __forceinline__ void lds_dma16(const char* src, char* lds_dst) {
-  const unsigned m0 = (unsigned)(uintptr_t)(lds_void*)lds_dst;
-  asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(m0) : "memory");
-}
-// Same with a wave-uniform base (SGPR pair) and a 32-bit per-lane byte offset.
-__device__ __forceinline__ void lds_dma16_s(const char* sbase, int voff, char* lds_dst) {
-  const unsigned m0 = (unsigned)(uintptr_t)(lds_void*)lds_dst;
-  asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "{m0}"(m0) : "memory");
 }
 
 template <typename T, int D, bool PAGED>

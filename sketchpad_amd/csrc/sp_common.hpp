@@ -128,4 +128,33 @@ __device__ __forceinline__ float group_sum(float v) {
 
 __device__ __forceinline__ int wave_uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
 
+// s_waitcnt vmcnt(0) expcnt(7) lgkmcnt(15): wait for every outstanding vector memory access of
+// this wave (gfx9 encoding: vmcnt in bits [3:0] and [15:14], expcnt [6:4], lgkmcnt [11:8]).
+constexpr int kWaitVmcnt0 = 0x0F70;
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+// global_load_lds_dwordx4: every lane copies 16 bytes from `src` to LDS at lds_dst + 16 * lane
+// (lds_dst wave-uniform; the s_nop covers the M0 write -> LDS DMA wait state). Issued through inline asm so that the compiler does not guard the
+// LDS reads of the other buffer with waits on these loads; completion is awaited explicitly
+// (s_waitcnt vmcnt(0) + barrier) before the data is read.
+__device__ __forceinline__ void lds_dma16(const char* src, char* lds_dst) {
+  const unsigned m0 = (unsigned)(uintptr_t)(lds_void*)lds_dst;
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(m0) : "memory");
+}
+// Same with a wave-uniform base (SGPR pair) and a 32-bit per-lane byte offset.
+// sbase must be wave-uniform; it is moved to SGPRs explicitly (readfirstlane) for the cases where
+// the compiler keeps a uniform address in VGPRs. The compiler's hazard checks do not look inside
+// inline asm, so the asm starts with s_nop 4: a VALU write of an SGPR (the readfirstlane) needs
+// 5 wait states before a VMEM instruction reads that SGPR, and an M0 write 1 before LDS DMA.
+__device__ __forceinline__ void lds_dma16_s(const char* sbase, int voff, char* lds_dst) {
+  const unsigned m0 = (unsigned)(uintptr_t)(lds_void*)lds_dst;
+  const uint64_t b = (uint64_t)(uintptr_t)sbase;
+  const uint64_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)b);
+  const uint64_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(b >> 32));
+  const char* s = (const char*)(uintptr_t)((hi << 32) | lo);
+  asm volatile("s_nop 4\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(s), "{m0}"(m0)
+               : "memory");
+}
+
 }  // namespace sp

@@ -44,11 +44,13 @@ def _linear_tol(x, w, prod, ref, dtype):
 
 @pytest.mark.parametrize("dtype", ["f32", "bf16", "f16"])
 @pytest.mark.parametrize("m,k,n", [(1, 64, 32), (64, 4096, 6144), (7, 96, 40), (300, 512, 1024),
-                                   (129, 136, 130), (65, 1024, 4096), (2, 8192, 1027)])
+                                   (129, 136, 130), (65, 1024, 4096), (2, 8192, 1027),
+                                   (512, 128, 256), (1000, 512, 523), (777, 1024, 1000),
+                                   (1024, 4096, 1536)])
 @pytest.mark.parametrize("with_bias", [False, True])
 def test_linear(dtype, m, k, n, with_bias):
     """y = x . w^T (+ b) with w [out, in]; M/N tails, K not a multiple of the 32-deep stage,
-    the 64-row (decode) and 128-row tiles, split K with partials."""
+    the 64-row (decode), 128-row and 256 x 256 (M >= 512) tiles, split K with partials."""
     announce(f"linear {dtype} M={m} K={k} N={n} bias={with_bias}")
     g = torch.Generator(device="cuda").manual_seed(m * 7 + k + n)
     x = torch.randn(m, k, generator=g, device="cuda").to(DT[dtype])
