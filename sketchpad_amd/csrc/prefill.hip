@@ -172,9 +172,12 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PrefillArgs a) {
     vbase = (const char*)a.v + kv0 * 2;
   }
 
-  // ---- Q^T operand (B of the S^T MFMA): query wq0 + l32, dims 16c + 8hh .. +7
+  // ---- Q^T operand (B of the S^T MFMA): query wq0 + l32, dims 16c + 8hh .. +7. Q stays
+  // unscaled (its 16-bit values exactly): the scale is applied to the fp32 scores.
   const int wq0 = qs + 32 * wave;
   const int my_q = wq0 + l32;
+  const float c2 = a.scale_log2;  // > 0 (checked on the host)
+  const float inv_c2 = 1.f / c2;
   uint4 qreg[KC];
   {
     const char* qp = qbase + (int64_t)min(my_q, qe - 1) * a.q_tok * 2;
@@ -239,11 +242,15 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PrefillArgs a) {
       }
       return;
     }
+    // Edge tiles are rare: the lane id goes through an empty asm so that the per-lane source
+    // addresses are derived here, not hoisted out of the key loop as live registers.
+    int ln = lane;
+    asm volatile("" : "+v"(ln));
 #pragma unroll
     for (int u = 0; u < NLD; ++u) {
       const int g = wave * NLD + u;             // 0 .. BUF/1024 - 1 (K tiles first)
       const bool is_v = g * 1024 >= TILE;
-      const int q = ((g * 1024) % TILE) / 16 + lane;
+      const int q = ((g * 1024) % TILE) / 16 + ln;
       const int R = q / CPR, p = q % CPR;
       const int c = p ^ C::swz(R);
       const int j = min(max(t0 + R, kv_lo), kv_hi - 1);
@@ -260,7 +267,14 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PrefillArgs a) {
       lds_dma16(src, buf + g * 1024);
     }
   };
-  float m_run = -INFINITY, l_run = 0.f;
+  // Online softmax state of query l32 (both lanes of a query hold the same values).
+  // m_run: running maximum of the exponents x = q.k * scale * log2(e) seen (-inf before the
+  // first visible key); m_used: the offset subtracted from x (m_run once that is finite, else 0),
+  // applied through the QK accumulator input minit.
+  float m_run = -INFINITY, m_used = 0.f, l_run = 0.f;
+  pf_f32x16 minit;  // -m_used / (scale * log2 e): accumulator input of the QK MFMAs
+#pragma unroll
+  for (int r = 0; r < 16; ++r) minit[r] = 0.f;
   pf_f32x16 acc[DB];
 #pragma unroll
   for (int db = 0; db < DB; ++db)
@@ -270,8 +284,15 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PrefillArgs a) {
   const int wq_lo = wq0, wq_hi = min(wq0 + 32, qe) - 1;  // this wave's queries (inclusive)
   const bool wave_active = wq_lo < qe;
   const int qpos = my_q + pos_off;
-  const float c2 = a.scale_log2;  // > 0 (checked on the host)
   const int sw = C::swz(l32);     // swizzle of the K rows this lane reads (row & 15 == l32 & 15)
+  // A tile needs masking iff t0 < mask_below or t0 > mask_above (wave-uniform bounds): it starts
+  // before kv_lo or before the window edge of this wave's last query, or it runs past the
+  // sequence end or past the causal diagonal of this wave's first query.
+  int mask_below = kv_lo, mask_above = Lk - BN;
+  if (a.causal != SP_CAUSAL_NONE) mask_above = min(mask_above, wq_lo + pos_off - BN + 1);
+  if (a.window_left >= 0) mask_below = max(mask_below, wq_hi + pos_off - a.window_left);
+  mask_below = wave_uniform(mask_below);
+  mask_above = wave_uniform(mask_above);
 
   // Lane parts of the LDS operand addresses (byte offsets inside a tile). With the XOR swizzle
   // an operand's logical chunk index only flips bits the lane part owns alone, so every operand
@@ -282,6 +303,18 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PrefillArgs a) {
   const int v_lane0 = rl * RB + 16 * (chl ^ C::swz(rl)) + 8 * (i16 & 1);
   const int v_lane1 = (rl + 8) * RB + 16 * (chl ^ C::swz(rl + 8)) + 8 * (i16 & 1);
 
+  // Causal diagonal at 32-key granularity. When the diagonal key of this wave's first query,
+  // diag0 = wq_lo + pos_off, is 32-aligned with the key tiles (always so for self-attention:
+  // wq_lo is a multiple of 32 and pos_off = 0), the diagonal 32x32 block of a tile is a fixed
+  // triangle: query l32 sees block keys 0..l32, i.e. score r of the lane iff
+  // 8(r/4) + r%4 <= l32 - 4hh; such tiles take one compare per score of that block instead of
+  // the general two-sided test on all 32. Every valid query's diagonal key is inside the
+  // sequence (checked below), so these tiles need no sequence-end mask either.
+  const int diag0 = wave_uniform(wq_lo + pos_off);
+  const bool tri_ok = a.causal != SP_CAUSAL_NONE && pos_off >= 0 && (pos_off & 31) == 0 &&
+                      qe - 1 + pos_off < Lk;
+  const int tri_lim = l32 - 4 * hh;
+
   auto compute_tile = [&](int t0, const char* kl) __attribute__((always_inline)) {
     const char* vl = kl + TILE;
     // S^T = K Q^T: two 32-key blocks, interleaved so that consecutive MFMAs are independent.
@@ -289,11 +322,10 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PrefillArgs a) {
     // (k_lane ^ 32(i/2)) + 32(i%2) RB; reads run AH operands ahead of the MFMAs, an order the
     // sched_barriers pin. The lane base goes through an empty asm so the compiler derives the
     // addresses inside the tile (one v_xor each) instead of keeping them all live.
+    // The first k-step of each key block takes minit (= -m_used / (scale * log2 e)) as its
+    // accumulator input, so s = q.k - m_used / (scale * log2 e) and the softmax weight of a
+    // score is 2^(s * scale * log2 e): one multiply and one exp per score.
     pf_f32x16 s[2];
-#pragma unroll
-    for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) s[mb][r] = 0.f;
     {
       int kb = k_lane;
       asm volatile("" : "+v"(kb));
@@ -309,36 +341,79 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PrefillArgs a) {
       for (int i = 0; i < NK; ++i) {
         const uint4 cur = kop[i % AH];
         if (i + AH < NK) kop[i % AH] = read_k(i + AH);
-        s[i & 1] = M::mma(cur, qreg[i >> 1], s[i & 1]);
+        s[i & 1] = M::mma(cur, qreg[i >> 1], i < 2 ? minit : s[i & 1]);
         __builtin_amdgcn_sched_barrier(0);
       }
     }
-    // masks: only tiles that cross the sequence end, the window edge or the diagonal. Score
-    // (mb, r) of this lane is key t0 + 4hh + off with off = 32mb + 8(r/4) + r%4; it is visible
-    // iff lo <= key <= hi, tested as a compile-time offset against two per-lane bounds.
-    bool need_mask = (t0 + BN > Lk) || (t0 < kv_lo);
-    if (a.causal != SP_CAUSAL_NONE) need_mask = need_mask || (t0 + BN - 1 > wq_lo + pos_off);
-    if (a.window_left >= 0) need_mask = need_mask || (t0 < wq_hi + pos_off - a.window_left);
-    if (__builtin_amdgcn_readfirstlane((int)need_mask)) {
-      int lo = kv_lo, hi = Lk - 1;
-      if (a.causal != SP_CAUSAL_NONE) hi = min(hi, qpos);
-      if (a.window_left >= 0) lo = max(lo, qpos - a.window_left);
-      const int jb = t0 + 4 * hh;
-      const int olo = lo - jb, ohi = hi - jb;
+    // Masks, only on tiles that cross the sequence end, the window edge, kv_lo or the causal
+    // diagonal. Score (mb, r) of this lane is key t0 + 4hh + off, off = 32mb + 8(r/4) + r%4.
+    if (t0 < mask_below || t0 > mask_above) {
+      if (tri_ok && t0 >= mask_below && (t0 == diag0 || t0 + 32 == diag0)) {
+        // 32-aligned causal diagonal: the diagonal block is the triangle 8(r/4) + r%4 <=
+        // l32 - 4hh; with the diagonal at the tile start, block 1 lies wholly above it.
+        int tl = tri_lim;
+        asm volatile("" : "+v"(tl));  // compare inside the tile (hoisted, 16 masks pin SGPRs)
+        if (t0 == diag0) {
 #pragma unroll
-      for (int mb = 0; mb < 2; ++mb)
+          for (int r = 0; r < 16; ++r) {
+            s[0][r] = (8 * (r >> 2) + (r & 3) <= tl) ? s[0][r] : -INFINITY;
+            s[1][r] = -INFINITY;
+          }
+        } else {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int off = 32 * mb + (r >> 2) * 8 + (r & 3);
-          s[mb][r] = (off >= olo && off <= ohi) ? s[mb][r] : -INFINITY;
+          for (int r = 0; r < 16; ++r)
+            s[1][r] = (8 * (r >> 2) + (r & 3) <= tl) ? s[1][r] : -INFINITY;
         }
+      } else {
+        // general: visible iff lo <= key <= hi, a compile-time offset against two per-lane bounds
+        int lo = kv_lo, hi = Lk - 1;
+        if (a.causal != SP_CAUSAL_NONE) hi = min(hi, qpos);
+        if (a.window_left >= 0) lo = max(lo, qpos - a.window_left);
+        const int jb = t0 + 4 * hh;
+        const int olo = lo - jb, ohi = hi - jb;
+#pragma unroll
+        for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int off = 32 * mb + (r >> 2) * 8 + (r & 3);
+            s[mb][r] = (off >= olo && off <= ohi) ? s[mb][r] : -INFINITY;
+          }
+      }
     }
-    // online softmax for query l32. Scores stay unscaled (the scale folds into the exponent).
-    // The running maximum is only raised when the tile's maximum exceeds it by more than
-    // 2^kLazy (lazy rescaling): until then p = 2^(s*c - m) <= 2^kLazy, exact in fp32 and within
-    // bf16 range, and the accumulator rescale is skipped.
-    float mx;
-    {
+    // Online softmax for query l32 (FlashAttention-2, Dao 2023) with a lazily raised maximum.
+    // The weights are p = 2^(x - m_used), x = q.k * scale * log2(e), with the offset m_used
+    // already inside s (above). m_run only ever holds a maximum actually seen (m_used = m_run
+    // once it is finite), so the largest weight of the row never underflows; it is raised
+    // only when this lane's 32 weights of the tile sum past 2^kLazy (so every weight that enters
+    // the accumulators is <= 2^kLazy, far inside fp32 and bf16 range) or while the query has no
+    // maximum yet. Otherwise the tile costs one exp per score and no max reduction.
+    // The row sum adds the 16-bit P values the PV product uses (v_dot2 against ones).
+    uint4 pb[4];
+    float lsum;
+    auto weights = [&](float delta) __attribute__((always_inline)) {
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        float p[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          p[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[ks >> 1][(ks & 1) * 8 + e], c2, -delta));
+        pb[ks] = make_uint4(M::pack(p[0], p[1]), M::pack(p[2], p[3]), M::pack(p[4], p[5]),
+                            M::pack(p[6], p[7]));
+      }
+      float la = 0.f, lb = 0.f;  // two independent dot2 chains
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        la = M::sum2(pb[ks].w, M::sum2(pb[ks].z, M::sum2(pb[ks].y, M::sum2(pb[ks].x, la))));
+        lb = M::sum2(pb[ks + 2].w,
+                     M::sum2(pb[ks + 2].z, M::sum2(pb[ks + 2].y, M::sum2(pb[ks + 2].x, lb))));
+      }
+      lsum = la + lb;
+    };
+    weights(0.f);
+    constexpr float kLazyBound = 4096.f;  // 2^kLazy, kLazy = 12
+    if (__any(lsum > kLazyBound || m_run == -INFINITY)) {
+      // Exact maximum of the tile for this query (both halves of the wave), then the new
+      // offset; the weights are recomputed against it and the running state rescaled.
       float mq[4];
 #pragma unroll
       for (int k = 0; k < 4; ++k) {  // four independent max3 chains over 8 scores each
@@ -348,37 +423,22 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PrefillArgs a) {
         x = max3f(x, s[mb][r0 + 5], s[mb][r0 + 6]);
         mq[k] = __builtin_fmaxf(x, s[mb][r0 + 7]);
       }
-      mx = __builtin_fmaxf(max3f(mq[0], mq[1], mq[2]), mq[3]);
-    }
-    {
+      float mx = __builtin_fmaxf(max3f(mq[0], mq[1], mq[2]), mq[3]);
       float x0, x1;
       swap_halves(mx, x0, x1);
-      mx = __builtin_fmaxf(x0, x1) * c2;
-    }
-    constexpr float kLazy = 8.f;
-    if (__any(mx > m_run + kLazy)) {
-      const float m_new = __builtin_fmaxf(m_run, mx);
-      const float alpha = __builtin_amdgcn_exp2f(m_run - (m_new == -INFINITY ? 0.f : m_new));
+      const float m_new = __builtin_fmaxf(m_run, __builtin_fmaf(__builtin_fmaxf(x0, x1), c2, m_used));
+      const float used_new = (m_new == -INFINITY) ? 0.f : m_new;
+      const float alpha = __builtin_amdgcn_exp2f(m_run - used_new);  // 0 while m_run = -inf
+      weights(used_new - m_used);
       m_run = m_new;
+      m_used = used_new;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) minit[r] = -used_new * inv_c2;
       l_run *= alpha;
 #pragma unroll
       for (int db = 0; db < DB; ++db) acc[db] *= alpha;
     }
-    const float m_use = (m_run == -INFINITY) ? 0.f : m_run;
-    uint4 pb[4];
-    float ls[4];
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      float p[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e)
-        p[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[ks >> 1][(ks & 1) * 8 + e], c2, -m_use));
-      pb[ks] = make_uint4(M::pack(p[0], p[1]), M::pack(p[2], p[3]), M::pack(p[4], p[5]),
-                          M::pack(p[6], p[7]));
-      // the row sum adds the 16-bit P values the PV product uses (v_dot2 against ones)
-      ls[ks] = M::sum2(pb[ks].w, M::sum2(pb[ks].z, M::sum2(pb[ks].y, M::sum2(pb[ks].x, 0.f))));
-    }
-    l_run += (ls[0] + ls[1]) + (ls[2] + ls[3]);
+    l_run += lsum;
     // O^T += V^T P^T: K-step ks covers tile tokens 16ks .. 16ks+15 in the S^T order. The V^T
     // operand (ks, db) is rows 16ks + rl (+ 8), chunk 4db + chl: (v_lane0 ^ 64db) + 16ks RB
     // (v_lane1 for the second row group), read AH operands ahead.
@@ -425,7 +485,9 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PrefillArgs a) {
       issue_tile(t0 + BN, nxt);
       fetch_blocks(t0 + 2 * BN);
     }
-    if (visits(t0)) compute_tile(t0, cur);
+    if (visits(t0)) {
+      compute_tile(t0, cur);
+    }
   };
 
   // Prologue: the first tile's loads go out while the Q loads are still in flight. The wait

@@ -40,14 +40,17 @@ def _as_f64(t):
     return t.float().cpu().numpy().astype(np.float64)
 
 
-def run_varlen(lens_q, lens_k, hq, hkv, d, dtype, causal, window, seed):
+def run_varlen(lens_q, lens_k, hq, hkv, d, dtype, causal, window, seed, inputs=None):
     g = torch.Generator(device="cuda").manual_seed(seed)
     dt = DT[dtype]
     cu_q = np.concatenate([[0], np.cumsum(lens_q)]).astype(np.int32)
     cu_k = np.concatenate([[0], np.cumsum(lens_k)]).astype(np.int32)
-    q = _rand(g, int(cu_q[-1]), hq, d, dt=dt)
-    k = _rand(g, int(cu_k[-1]), hkv, d, dt=dt)
-    v = _rand(g, int(cu_k[-1]), hkv, d, dt=dt)
+    if inputs is None:
+        q = _rand(g, int(cu_q[-1]), hq, d, dt=dt)
+        k = _rand(g, int(cu_k[-1]), hkv, d, dt=dt)
+        v = _rand(g, int(cu_k[-1]), hkv, d, dt=dt)
+    else:
+        q, k, v = (x.to(device="cuda", dtype=dt) for x in inputs(cu_q, cu_k))
     out = torch.full_like(q, float("nan"))
     announce(f"varlen prefill lens_q={list(lens_q)} lens_k={list(lens_k)} hq={hq} hkv={hkv} "
              f"d={d} {dtype} causal={causal} window={window}")
@@ -87,6 +90,46 @@ def test_varlen_sliding_window(window):
     """Mistral's sliding_window_mask(W): keys [i - W, i] (window_left = W)."""
     lens = [7, 150, 300, 65]
     run_varlen(lens, lens, 8, 2, 128, "bf16", sp.SP_CAUSAL_BOTTOM_RIGHT, window, seed=21 + window)
+
+
+def _score_range_inputs(mode, hq, hkv, d, seed):
+    """q/k/v whose scores sit far from the N(0,1) range: 'up' rises along every sequence's keys
+    (x = score * scale * log2 e climbs to ~390, so the running maximum is raised tile after tile),
+    'down' falls (the maximum is in the first tile, later weights underflow to zero), 'neg' sits
+    near x = -390 for every key (weights would underflow without a maximum taken from the data),
+    'wide' draws q and k from N(0, 4^2) (|x| up to ~100: peaked softmax, large exponents)."""
+    def make(cu_q, cu_k):
+        g = torch.Generator().manual_seed(seed)
+        tq, tk = int(cu_q[-1]), int(cu_k[-1])
+        v = torch.randn(tk, hkv, d, generator=g)
+        if mode == "wide":
+            return (4 * torch.randn(tq, hq, d, generator=g), 4 * torch.randn(tk, hkv, d, generator=g),
+                    v)
+        q = 2.0 + 0.5 * torch.randn(tq, hq, d, generator=g)
+        level = torch.zeros(tk)
+        for s in range(len(cu_k) - 1):
+            a, b = int(cu_k[s]), int(cu_k[s + 1])
+            ramp = torch.arange(b - a, dtype=torch.float32) / max(b - a, 1)
+            level[a:b] = {"up": 12.0 * ramp, "down": 12.0 * (1 - ramp),
+                          "neg": torch.full_like(ramp, -12.0)}[mode]
+        k = level[:, None, None] + 0.5 * torch.randn(tk, hkv, d, generator=g)
+        return q, k, v
+    return make
+
+
+@pytest.mark.parametrize("mode", ["up", "down", "neg", "wide"])
+def test_varlen_score_range(mode):
+    """The online softmax's maximum handling over score ranges far from N(0,1) inputs."""
+    lens = [1, 70, 200, 333]
+    run_varlen(lens, lens, 8, 2, 128, "bf16", sp.SP_CAUSAL_BOTTOM_RIGHT, -1, seed=41,
+               inputs=_score_range_inputs(mode, 8, 2, 128, seed=41))
+
+
+def test_varlen_score_range_window():
+    """Rising scores under a sliding window: each query's maximum leaves the window."""
+    lens = [150, 300]
+    run_varlen(lens, lens, 4, 4, 64, "bf16", sp.SP_CAUSAL_BOTTOM_RIGHT, 40, seed=43,
+               inputs=_score_range_inputs("up", 4, 4, 64, seed=43))
 
 
 def test_varlen_empty_sequences():
