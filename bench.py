@@ -380,10 +380,12 @@ def time_layer(steps: int, warmup: int, hidden: int = 4096):
                                 stream=s)
         else:
             lens_d = torch.from_numpy(w.lens.astype(np.int32)).cuda()
+            pws = sp.alloc_paged_prefill_workspace(w.num_seqs, w.max_seqlen, hq, lay,
+                                                   t["block_tables"].shape[1])
 
             def attention():  # the new tokens attend through the pool they were appended to
                 sp.paged_prefill(attn, q, k_pool, v_pool, lay, t["block_tables"], t["cu_seqlens"],
-                                 lens_d, w.max_seqlen, d ** -0.5, stream=s)
+                                 lens_d, w.max_seqlen, d ** -0.5, workspace=pws, stream=s)
 
         def o_proj():
             sp.linear(out, attn.view(T, hq * d), wo, workspace=lws, stream=s)
@@ -434,18 +436,28 @@ def time_chunked_c4(steps: int, warmup: int):
     sp.kv_append(t["k_pool"], t["v_pool"], lay, t["k_new"], t["v_new"], t["slot_mapping"],
                  stream=s)
 
-    def prefill():
-        sp.paged_prefill(t["out"], t["q"], t["k_pool"], t["v_pool"], lay, t["block_tables"],
-                         t["cu_seqlens_q"], t["context_lens"], w.max_seqlen_q,
-                         w.head_dim ** -0.5, stream=s)
+    # the workspace lets sp_paged_prefill split the long contexts' keys over workgroups
+    ws = sp.alloc_paged_prefill_workspace(w.num_seqs, w.max_seqlen_q, w.hq, lay,
+                                          t["block_tables"].shape[1])
 
-    for _ in range(warmup):
-        prefill()
-    torch.cuda.synchronize()
-    ms, _ = _event_times(stream, prefill, steps)
+    def run(workspace):
+        def prefill():
+            sp.paged_prefill(t["out"], t["q"], t["k_pool"], t["v_pool"], lay, t["block_tables"],
+                             t["cu_seqlens_q"], t["context_lens"], w.max_seqlen_q,
+                             w.head_dim ** -0.5, workspace=workspace, stream=s)
+
+        for _ in range(warmup):
+            prefill()
+        torch.cuda.synchronize()
+        return _event_times(stream, prefill, steps)[0]
+
+    ms_unsplit = run(None)
+    ms = run(ws)
     tflops = w.flops() / (ms * 1e-3) / 1e12
     return {"ms": round(ms, 5), "tflops": round(tflops, 2),
-            "frac_mfma": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4)}
+            "frac_mfma": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
+            "workspace_bytes": 0 if ws is None else ws.numel(),
+            "ms_without_key_split": round(ms_unsplit, 5)}
 
 
 def cpu_prefill_baseline(w, budget_s: float):

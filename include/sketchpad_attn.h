@@ -213,14 +213,24 @@ int sp_varlen_prefill(void* out, const void* q, const void* k, const void* v,
  * Replaces forward_cached with seq_len > 1 and prefill_causal_mask (llama.rs:250-260, :374-388):
  * sequence s has context_lens[s] keys in the pools and cu_seqlens_q[s+1] - cu_seqlens_q[s] new
  * queries, which sit at the last positions of the context (bottom-right causal).
- *   q, out : [total_q, Hq, D] contiguous; block_tables [num_seqs, max_blocks_per_seq] (device).
+ *   q, out    : [total_q, Hq, D] contiguous; block_tables [num_seqs, max_blocks_per_seq] (device).
+ *   workspace : optional device scratch (16-byte aligned). Batches of few query blocks over long
+ *               contexts split each sequence's keys over several workgroups when the workspace
+ *               holds their fp32 partials, sp_paged_prefill_workspace_size() bytes for the full
+ *               split; a smaller (or NULL) workspace lowers the split (NULL: none). The result
+ *               does not depend on whether the keys were split beyond fp32 rounding of the
+ *               merge. Calls sharing one workspace must not overlap.
  */
+size_t sp_paged_prefill_workspace_size(int32_t num_seqs, int32_t max_seqlen_q,
+                                       int32_t num_q_heads, const sp_cache_layout* layout,
+                                       int32_t max_blocks_per_seq);
 int sp_paged_prefill(void* out, const void* q,
                      const void* k_pool, const void* v_pool, const sp_cache_layout* layout,
                      const int32_t* block_tables, int32_t max_blocks_per_seq,
                      const int32_t* cu_seqlens_q, const int32_t* context_lens,
                      int32_t num_seqs, int32_t max_seqlen_q, int32_t num_q_heads,
-                     float scale, int32_t window_left, sp_dtype dtype, void* stream);
+                     float scale, int32_t window_left, sp_dtype dtype,
+                     void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * Dense attention on [batch, heads, seq, head_dim] tensors: flash_attention(q, k, v,

@@ -22,6 +22,8 @@ from ._lib import (  # noqa: F401
     paged_decode,
     paged_decode_workspace_size,
     paged_prefill,
+    paged_prefill_workspace_size,
+    alloc_paged_prefill_workspace,
     alloc_linear_workspace,
     alloc_polar_pools,
     linear,

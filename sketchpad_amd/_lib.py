@@ -75,9 +75,12 @@ _SIGNATURES = {
     "sp_varlen_prefill": (c_int32, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                                     c_int32, c_int32, c_int32, c_int32, c_int32, c_float,
                                     c_int32, c_int32, c_int32, c_void_p]),
+    "sp_paged_prefill_workspace_size": (c_size_t, [c_int32, c_int32, c_int32,
+                                                   POINTER(CacheLayout), c_int32]),
     "sp_paged_prefill": (c_int32, [c_void_p, c_void_p, c_void_p, c_void_p, POINTER(CacheLayout),
                                    c_void_p, c_int32, c_void_p, c_void_p, c_int32, c_int32,
-                                   c_int32, c_float, c_int32, c_int32, c_void_p]),
+                                   c_int32, c_float, c_int32, c_int32, c_void_p, c_size_t,
+                                   c_void_p]),
     "sp_flash_attention": (c_int32, [c_void_p, c_void_p, c_void_p, c_void_p, c_int32, c_int32,
                                      c_int32, c_int32, c_int32, c_float, c_int32, c_int32,
                                      c_void_p]),
@@ -253,15 +256,31 @@ def varlen_prefill(out, q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q: int, 
                                    window_left, sp_dtype(q), _stream(stream)))
 
 
+def paged_prefill_workspace_size(num_seqs: int, max_seqlen_q: int, num_q_heads: int,
+                                 lay: CacheLayout, max_blocks_per_seq: int) -> int:
+    return int(load().sp_paged_prefill_workspace_size(num_seqs, max_seqlen_q, num_q_heads,
+                                                      ctypes.byref(lay), max_blocks_per_seq))
+
+
+def alloc_paged_prefill_workspace(num_seqs: int, max_seqlen_q: int, num_q_heads: int,
+                                  lay: CacheLayout, max_blocks_per_seq: int, device="cuda"):
+    """A workspace of sp_paged_prefill_workspace_size() bytes (None when no split is planned)."""
+    n = paged_prefill_workspace_size(num_seqs, max_seqlen_q, num_q_heads, lay, max_blocks_per_seq)
+    return _torch().empty(n, dtype=_torch().uint8, device=device) if n > 0 else None
+
+
 def paged_prefill(out, q, k_pool, v_pool, lay: CacheLayout, block_tables, cu_seqlens_q,
                   context_lens, max_seqlen_q: int, scale: float, *, window_left: int = -1,
-                  stream=None) -> None:
-    """sp_paged_prefill. q/out [total_q, Hq, D]; the new tokens are already in the pools."""
+                  workspace=None, stream=None) -> None:
+    """sp_paged_prefill. q/out [total_q, Hq, D]; the new tokens are already in the pools.
+    workspace: optional device tensor for the split-key partials (None: no split)."""
+    ws_ptr = _ptr(workspace) if workspace is not None else None
+    ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
     check(load().sp_paged_prefill(_ptr(out), _ptr(q), _ptr(k_pool), _ptr(v_pool),
                                   ctypes.byref(lay), _ptr(block_tables), block_tables.shape[1],
                                   _ptr(cu_seqlens_q), _ptr(context_lens),
                                   cu_seqlens_q.numel() - 1, max_seqlen_q, q.shape[1], scale,
-                                  window_left, sp_dtype(q), _stream(stream)))
+                                  window_left, sp_dtype(q), ws_ptr, ws_bytes, _stream(stream)))
 
 
 def flash_attention(out, q, k, v, scale: float, *, causal: bool = False, stream=None) -> None:

@@ -5,6 +5,7 @@
 #include <stdarg.h>
 #include <math.h>
 #include <stdio.h>
+#include <stdlib.h>
 
 #include <string>
 
@@ -357,12 +358,39 @@ int sp_varlen_prefill(void* out, const void* q, const void* k, const void* v,
   return launch_prefill(a, dtype, head_dim, false, (hipStream_t)stream);
 }
 
+// Key-range splits of a chunked prefill: the planner's count for the batch shape (the context
+// bound is the block tables' width), lowered until the partials fit the caller's workspace.
+static int prefill_splits(int32_t num_seqs, int32_t max_seqlen_q, int32_t num_q_heads,
+                          int32_t head_dim, int64_t max_context, size_t workspace_bytes) {
+  const int64_t base = (int64_t)((max_seqlen_q + kPrefillBM - 1) / kPrefillBM) * num_seqs *
+                       num_q_heads;
+  int s = plan_prefill_splits(base, (max_context + kPrefillBN - 1) / kPrefillBN);
+  const char* env = getenv("SP_PREFILL_SPLITS");  // tuning override, clamped to 1..8
+  if (env && atoi(env) > 0) s = atoi(env) > 8 ? 8 : atoi(env);
+  while (s > 1 &&
+         prefill_partials_bytes(num_seqs, max_seqlen_q, num_q_heads, head_dim, s) > workspace_bytes)
+    --s;
+  return s;
+}
+
+size_t sp_paged_prefill_workspace_size(int32_t num_seqs, int32_t max_seqlen_q,
+                                       int32_t num_q_heads, const sp_cache_layout* layout,
+                                       int32_t max_blocks_per_seq) {
+  if (!layout || num_seqs <= 0 || max_seqlen_q <= 0 || num_q_heads <= 0 ||
+      max_blocks_per_seq <= 0 || (layout->head_dim != 64 && layout->head_dim != 128))
+    return 0;
+  const int64_t max_context = (int64_t)max_blocks_per_seq * layout->block_size;
+  const int s = prefill_splits(num_seqs, max_seqlen_q, num_q_heads, layout->head_dim,
+                               max_context, SIZE_MAX);
+  return prefill_partials_bytes(num_seqs, max_seqlen_q, num_q_heads, layout->head_dim, s);
+}
+
 int sp_paged_prefill(void* out, const void* q, const void* k_pool, const void* v_pool,
                      const sp_cache_layout* layout, const int32_t* block_tables,
                      int32_t max_blocks_per_seq, const int32_t* cu_seqlens_q,
                      const int32_t* context_lens, int32_t num_seqs, int32_t max_seqlen_q,
                      int32_t num_q_heads, float scale, int32_t window_left, sp_dtype dtype,
-                     void* stream) {
+                     void* workspace, size_t workspace_bytes, void* stream) {
   const char* fn = "sp_paged_prefill";
   if (int rc = check_layout(layout, fn)) return rc;
   if (int rc = check_prefill_common(fn, num_seqs, max_seqlen_q, num_q_heads,
@@ -398,6 +426,14 @@ int sp_paged_prefill(void* out, const void* q, const void* k_pool, const void* v
   a.block_size = layout->block_size;
   a.num_blocks = layout->num_blocks;
   pool_strides(layout, dtype_size(dtype), &a.block_stride_b, &a.layer_off_b);
+  if (workspace && misaligned16(workspace))
+    return fail(SP_EINVAL, "%s: workspace must be 16-byte aligned", fn);
+  a.nsplit = workspace ? prefill_splits(num_seqs, max_seqlen_q, num_q_heads, D,
+                                        (int64_t)max_blocks_per_seq * layout->block_size,
+                                        workspace_bytes)
+                       : 1;
+  a.partials = a.nsplit > 1 ? (float*)workspace : nullptr;
+  a.max_q = max_seqlen_q;
   return launch_prefill(a, dtype, D, true, (hipStream_t)stream);
 }
 

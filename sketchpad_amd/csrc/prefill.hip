@@ -125,7 +125,9 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PrefillArgs a) {
   const int gm = id % a.group;
   id /= a.group;
   const int seq = id % a.num_seqs;
-  const int qblk = a.num_qblocks - 1 - id / a.num_seqs;
+  id /= a.num_seqs;
+  const int split = id % a.nsplit;
+  const int qblk = a.num_qblocks - 1 - id / a.nsplit;
   const int h = kvh * a.group + gm;
 
   const int q_begin = a.cu_q ? a.cu_q[seq] : 0;
@@ -145,7 +147,15 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PrefillArgs a) {
   int kv_lo = 0, kv_hi = Lk;
   if (a.causal != SP_CAUSAL_NONE) kv_hi = min(Lk, qe - 1 + pos_off + 1);
   if (a.window_left >= 0) kv_lo = max(0, qs + pos_off - a.window_left);
-  const int t_first = (kv_lo / BN) * BN;
+  // This workgroup's key tiles: all of [kv_lo, kv_hi), or its 1/nsplit share of them (masks and
+  // row clamps keep using the full range; only the walk stops at kv_end).
+  int t_first = (kv_lo / BN) * BN, kv_end = kv_hi;
+  if (a.nsplit > 1) {
+    const int ntiles = kv_hi > t_first ? (kv_hi - t_first + BN - 1) / BN : 0;
+    const int tps = (ntiles + a.nsplit - 1) / a.nsplit;
+    t_first += split * tps * BN;
+    kv_end = min(kv_hi, t_first + tps * BN);
+  }
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -481,7 +491,7 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PrefillArgs a) {
   auto step = [&](int t0, char* cur, char* nxt) __attribute__((always_inline)) {
     __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
     __syncthreads();
-    if (t0 + BN < kv_hi) {
+    if (t0 + BN < kv_end) {
       issue_tile(t0 + BN, nxt);
       fetch_blocks(t0 + 2 * BN);
     }
@@ -494,7 +504,7 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PrefillArgs a) {
   // below covers both, so no wait inside the key loop refers to Q (the tile loads issued there
   // are awaited explicitly).
   int t0 = t_first;
-  if (t0 < kv_hi) {
+  if (t0 < kv_end) {
     if constexpr (PAGED) {
       fetch_blocks(t0);
       __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
@@ -503,10 +513,10 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PrefillArgs a) {
     fetch_blocks(t0 + BN);
   }
   __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
-  while (t0 < kv_hi) {
+  while (t0 < kv_end) {
     step(t0, lds0, lds1);
     t0 += BN;
-    if (t0 >= kv_hi) break;
+    if (t0 >= kv_end) break;
     step(t0, lds1, lds0);
     t0 += BN;
   }
@@ -516,6 +526,21 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PrefillArgs a) {
   swap_halves(l_run, x0, x1);
   const float l = x0 + x1;
   if (my_q >= qe) return;
+  if (a.nsplit > 1) {
+    // partial record (m, l, -, -, acc[D]) of this split; m is the offset the weights are
+    // relative to (0 when the split saw no key, with l = 0 and acc = 0)
+    float* rec = a.partials +
+        ((((int64_t)seq * a.max_q + my_q) * a.hq + h) * a.nsplit + split) * (D + 4);
+    if (hh == 0) *(float2*)rec = make_float2(m_used, l);
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int rg = 0; rg < 4; ++rg)
+        *(float4*)(rec + 4 + db * 32 + rg * 8 + hh * 4) =
+            make_float4(acc[db][rg * 4 + 0], acc[db][rg * 4 + 1], acc[db][rg * 4 + 2],
+                        acc[db][rg * 4 + 3]);
+    return;
+  }
   const float inv = l > 0.f ? 1.f / l : 0.f;
   char* op = obase + (int64_t)my_q * a.o_tok * 2;
 #pragma unroll
@@ -530,16 +555,74 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PrefillArgs a) {
     }
 }
 
+// Merge the split partials of one (sequence, query block, head): out = sum_s 2^(m_s - M) acc_s /
+// sum_s 2^(m_s - M) l_s, M = max_s m_s (zeros when no split saw a key). D/4 lanes per row, four
+// output elements each.
+template <typename T, int D>
+__global__ void __launch_bounds__(256) prefill_combine_kernel(PrefillArgs a) {
+  using M = PrefillMfma<T>;
+  constexpr int TPR = D / 4, RPP = 256 / TPR;
+  const int h = blockIdx.x % a.hq;
+  const int id = blockIdx.x / a.hq;
+  const int seq = id % a.num_seqs, qblk = id / a.num_seqs;
+  const int q_begin = a.cu_q[seq];
+  const int Lq = a.cu_q[seq + 1] - q_begin;
+  const int qs = qblk * kPrefillBM;
+  if (qs >= Lq) return;
+  const int qe = min(qs + kPrefillBM, Lq);
+  const int c = threadIdx.x % TPR;
+  for (int q = qs + (int)threadIdx.x / TPR; q < qe; q += RPP) {
+    const float* rec =
+        a.partials + ((((int64_t)seq * a.max_q + q) * a.hq + h) * a.nsplit) * (D + 4);
+    float m = -INFINITY;
+    for (int sp = 0; sp < a.nsplit; ++sp) m = fmaxf(m, rec[sp * (D + 4)]);
+    float l = 0.f, o0 = 0.f, o1 = 0.f, o2 = 0.f, o3 = 0.f;
+    for (int sp = 0; sp < a.nsplit; ++sp) {
+      const float* r = rec + sp * (D + 4);
+      const float w = __builtin_amdgcn_exp2f(r[0] - m);
+      const float4 v = *(const float4*)(r + 4 + 4 * c);
+      l += w * r[1];
+      o0 += w * v.x;
+      o1 += w * v.y;
+      o2 += w * v.z;
+      o3 += w * v.w;
+    }
+    const float inv = l > 0.f ? 1.f / l : 0.f;
+    char* op = (char*)a.out + ((int64_t)(q_begin + q) * a.o_tok + (int64_t)h * a.o_head + 4 * c) * 2;
+    *(uint2*)op = make_uint2(M::pack(o0 * inv, o1 * inv), M::pack(o2 * inv, o3 * inv));
+  }
+}
+
+int plan_prefill_splits(int64_t base_wgs, int64_t max_ctx_tiles) {
+  if (base_wgs <= 0 || base_wgs >= 1024) return 1;
+  int64_t s = (1024 + base_wgs / 2) / base_wgs;
+  s = s > 8 ? 8 : s;
+  const int64_t by_len = max_ctx_tiles / 16;
+  s = s > by_len ? by_len : s;
+  return s < 1 ? 1 : (int)s;
+}
+
+size_t prefill_partials_bytes(int num_seqs, int max_seqlen_q, int hq, int head_dim, int nsplit) {
+  if (nsplit <= 1) return 0;
+  return (size_t)num_seqs * max_seqlen_q * hq * nsplit * (head_dim + 4) * sizeof(float);
+}
+
 template <typename T, int D>
 static int launch_td(const PrefillArgs& a, bool paged, hipStream_t stream) {
-  const int64_t blocks = (int64_t)a.num_qblocks * a.num_seqs * a.hq;
+  const int64_t base = (int64_t)a.num_qblocks * a.num_seqs * a.hq;
+  const int64_t blocks = base * (a.nsplit > 1 ? a.nsplit : 1);
   if (blocks <= 0) return SP_OK;
   if (blocks > 0x7fffffff) return fail(SP_EINVAL, "prefill: grid of %lld workgroups", (long long)blocks);
   if (paged)
     hipLaunchKernelGGL((prefill_kernel<T, D, true>), dim3((unsigned)blocks), dim3(256), 0, stream, a);
   else
     hipLaunchKernelGGL((prefill_kernel<T, D, false>), dim3((unsigned)blocks), dim3(256), 0, stream, a);
-  return check_launch("prefill_kernel");
+  if (int rc = check_launch("prefill_kernel")) return rc;
+  if (a.nsplit > 1) {
+    hipLaunchKernelGGL((prefill_combine_kernel<T, D>), dim3((unsigned)base), dim3(256), 0, stream, a);
+    return check_launch("prefill_combine_kernel");
+  }
+  return SP_OK;
 }
 
 template <typename T>
@@ -551,8 +634,10 @@ static int launch_t(const PrefillArgs& a, int head_dim, bool paged, hipStream_t 
   }
 }
 
-int launch_prefill(const PrefillArgs& a, sp_dtype dtype, int head_dim, bool paged,
+int launch_prefill(const PrefillArgs& args, sp_dtype dtype, int head_dim, bool paged,
                    hipStream_t stream) {
+  PrefillArgs a = args;
+  if (a.nsplit < 1 || !a.partials) a.nsplit = 1;
   switch (dtype) {
     case SP_BF16: return launch_t<bf16_t>(a, head_dim, paged, stream);
     case SP_F16: return launch_t<f16_t>(a, head_dim, paged, stream);

@@ -36,7 +36,19 @@ struct PrefillArgs {
   int num_blocks;
   int64_t block_stride_b;
   int64_t layer_off_b;
+  // split key range (paged prefill with a workspace): nsplit > 1 makes every workgroup take
+  // 1/nsplit of its sequence's key tiles and write fp32 partials [num_seqs][max_q][Hq][nsplit]
+  // records of (m, l, pad, pad, acc[D]) that prefill_combine_kernel merges into out.
+  float* partials;
+  int nsplit;
+  int max_q;  // max_seqlen_q: the partials' per-sequence row stride
 };
+
+// Split count for a chunked prefill of base_wgs workgroups whose sequences span up to
+// max_ctx_tiles 64-key tiles: about 1024 workgroups in all, at least 16 tiles per split, at
+// most 8 splits.
+int plan_prefill_splits(int64_t base_wgs, int64_t max_ctx_tiles);
+size_t prefill_partials_bytes(int num_seqs, int max_seqlen_q, int hq, int head_dim, int nsplit);
 
 int launch_prefill(const PrefillArgs& a, sp_dtype dtype, int head_dim, bool paged,
                    hipStream_t stream);

@@ -135,10 +135,14 @@ void BatchedPagedAttention::forward(size_t layer_idx, const DeviceRaggedBatch& b
                              workspace_.data(), workspace_.nbytes(), stream),
              "sp_paged_decode");
   } else {
+    const size_t need = sp_paged_prefill_workspace_size((int32_t)hb.num_seqs(), hb.max_seqlen_q,
+                                                        hq, &lay, hb.max_blocks);
+    if (need > workspace_.nbytes())
+      workspace_ = DeviceTensor({(int64_t)((need + 3) / 4)}, SP_F32);
     check_sp(sp_paged_prefill(out.data(), q.data(), kp, vp, &lay, batch.block_tables(),
                               hb.max_blocks, batch.cu_seqlens_q(), batch.context_lens(),
                               (int32_t)hb.num_seqs(), hb.max_seqlen_q, hq, scale, -1,
-                              cache_.dtype(), stream),
+                              cache_.dtype(), workspace_.data(), workspace_.nbytes(), stream),
              "sp_paged_prefill");
   }
 }

@@ -86,9 +86,10 @@ struct RopeTables {
 
 // One attention layer of a ragged batch over a paged cache (the batched form of
 // PagedAttentionCache::update_layer + forward_cached). q and out are [T, Hq, D], k_new / v_new
-// [T, Hkv, D], packed in batch order. Keeps the decode workspace between calls (zeroed when
-// allocated, as sp_paged_decode requires). Failures throw std::runtime_error with the library's
-// message.
+// [T, Hkv, D], packed in batch order. Keeps one workspace between calls for the decode partials
+// and the chunked prefill's split-key partials (grown to what sp_paged_decode_workspace_size /
+// sp_paged_prefill_workspace_size ask for). Failures throw std::runtime_error with the
+// library's message.
 class BatchedPagedAttention {
  public:
   explicit BatchedPagedAttention(PagedKvCache& cache) : cache_(cache) {}

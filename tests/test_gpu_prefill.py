@@ -160,14 +160,22 @@ def test_flash_attention_dense(causal, sq, sk):
     assert_attention_close(_as_f64(out), ref, "bf16", "flash_attention")
 
 
-def run_chunked(w: W.ChunkedPrefillWorkload, sample_rows=None):
+def run_chunked(w: W.ChunkedPrefillWorkload, sample_rows=None, split=False):
+    """split: hand sp_paged_prefill the workspace it asks for, so long contexts are split over
+    several workgroups per query block (the test asserts that a split is planned)."""
     t = W.make_chunked_tensors(w)
     lay = sp.layout(t["num_blocks"], 1, 0, w.hkv, w.block_size, w.head_dim)
-    announce(f"chunked prefill {w.name} chunks={list(w.chunk_lens)} ctx={list(w.ctx_before)}")
+    ws = None
+    if split:
+        ws = sp.alloc_paged_prefill_workspace(w.num_seqs, w.max_seqlen_q, w.hq, lay,
+                                              t["block_tables"].shape[1])
+        assert ws is not None, "no key split planned for this shape"
+    announce(f"chunked prefill {w.name} chunks={list(w.chunk_lens)} ctx={list(w.ctx_before)} "
+             f"workspace={0 if ws is None else ws.numel()}")
     sp.kv_append(t["k_pool"], t["v_pool"], lay, t["k_new"], t["v_new"], t["slot_mapping"])
     sp.paged_prefill(t["out"], t["q"], t["k_pool"], t["v_pool"], lay, t["block_tables"],
                      t["cu_seqlens_q"], t["context_lens"], w.max_seqlen_q, w.head_dim ** -0.5,
-                     window_left=w.window_left)
+                     window_left=w.window_left, workspace=ws)
     torch.cuda.synchronize()
     olay = O.make_layout(t["num_blocks"], 1, 0, w.hkv, w.block_size, w.head_dim)
     kp, vp, q = host_array(t["k_pool"]), host_array(t["v_pool"]), host_array(t["q"])
@@ -211,8 +219,19 @@ def test_paged_prefill_block_size_32():
     run_chunked(w)
 
 
-def test_chunked_prefill_c4_sampled_rows():
-    run_chunked(W.chunked_prefill_c4(), sample_rows=24)
+@pytest.mark.parametrize("window", [-1, 1000])
+def test_paged_prefill_split_keys(window):
+    """Few query blocks over long contexts: the keys are split over workgroups (4 splits here)
+    and the fp32 partials merged; every row checked against the f64 oracle."""
+    w = W.ChunkedPrefillWorkload("chunked-split", 47, np.array([64, 200, 1], np.int32),
+                                 np.array([3000, 2100, 5000], np.int32), 8, 2, 128, "bf16",
+                                 window_left=window)
+    run_chunked(w, split=True)
+
+
+@pytest.mark.parametrize("split", [False, True])
+def test_chunked_prefill_c4_sampled_rows(split):
+    run_chunked(W.chunked_prefill_c4(), sample_rows=24, split=split)
 
 
 def _torch_ref_causal(q, k, v, cu, scale):
