@@ -171,6 +171,21 @@ def test_workspace_size_monotone(sp_lib):
     assert w1 == w2 > 0
 
 
+def test_paged_prefill_workspace_size(sp_lib):
+    """Key splits are planned only for few query blocks over long contexts: C4's shape (4 x 512
+    queries, 28 heads, contexts up to 428 blocks of 16) gets 2 splits of fp32 (m, l, acc) records;
+    a C3-sized batch (2,496 query blocks) and short contexts get none."""
+    lay = _lib.layout(10_000, 1, 0, 4, 16, 128)
+    rec = 128 + 4
+    assert sp_lib.sp_paged_prefill_workspace_size(4, 512, 28, ctypes.byref(lay), 428) == \
+        4 * 512 * 28 * 2 * rec * 4
+    lay32 = _lib.layout(10_000, 1, 0, 8, 16, 128)
+    assert sp_lib.sp_paged_prefill_workspace_size(8, 1672, 32, ctypes.byref(lay32), 105) == 0
+    assert sp_lib.sp_paged_prefill_workspace_size(4, 512, 28, ctypes.byref(lay), 10) == 0
+    assert sp_lib.sp_paged_prefill_workspace_size(0, 512, 28, ctypes.byref(lay), 428) == 0
+    assert sp_lib.sp_paged_prefill_workspace_size(4, 512, 28, None, 428) == 0
+
+
 def test_missing_library_fails_loudly(monkeypatch, tmp_path):
     monkeypatch.setattr(_lib, "_lib", None)
     monkeypatch.setattr(_lib, "LIB_PATH", tmp_path / "nope.so")
