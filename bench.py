@@ -40,6 +40,7 @@ sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0
 MFMA_BF16_PEAK_TFLOPS = 2500.0
+MFMA_FP32_PEAK_TFLOPS = 157.3
 METRIC = "paged-decode HBM GB/s (% of peak) + ragged-prefill TFLOP/s, Llama-3-8B shape"
 
 
@@ -460,6 +461,30 @@ def time_chunked_c4(steps: int, warmup: int):
             "ms_without_key_split": round(ms_unsplit, 5)}
 
 
+def time_flash_f32(steps: int, warmup: int, b: int = 2, h: int = 8, s: int = 4096, d: int = 64):
+    """sp_flash_attention in f32 (the reference flash_attention's element type) on a dense
+    non-causal [2, 8, 4096, 64] batch (self-attention at a diffusion UNet's 64x64 latent):
+    TFLOP/s (4 B H S^2 D) against the 157.3 TFLOP/s dense fp32 MFMA peak."""
+    import torch
+    import sketchpad_amd as sp
+
+    g = torch.Generator(device="cuda").manual_seed(7)
+    q, k, v = (torch.randn(b, h, s, d, generator=g, device="cuda") for _ in range(3))
+    out = torch.empty_like(q)
+    stream = torch.cuda.current_stream()
+
+    def attn():
+        sp.flash_attention(out, q, k, v, d ** -0.5, causal=False, stream=stream.cuda_stream)
+
+    for _ in range(warmup):
+        attn()
+    torch.cuda.synchronize()
+    ms, _ = _event_times(stream, attn, steps)
+    tflops = 4 * b * h * s * s * d / (ms * 1e-3) / 1e12
+    return {"shape": [b, h, s, d], "ms": round(ms, 4), "tflops": round(tflops, 2),
+            "frac_fp32_mfma": round(tflops / MFMA_FP32_PEAK_TFLOPS, 4)}
+
+
 def cpu_prefill_baseline(w, budget_s: float):
     """The oracle's C port of the reference's prefill op sequence ([Hq, L, L] f32 scores per
     sequence) on a bounded sample: the two shortest C3 sequences."""
@@ -569,6 +594,7 @@ def main():
         line["prefill"] = pf
     if args.secondary:
         line.setdefault("secondary", {})["C4-chunked-prefill"] = time_chunked_c4(10, 2)
+        line["secondary"]["flash-attention-f32"] = time_flash_f32(5, 2)
     if args.layer or args.secondary:
         line["layer"] = time_layer(args.steps, 3)
     if args.secondary:

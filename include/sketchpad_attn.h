@@ -197,8 +197,9 @@ int sp_paged_decode(void* out, const void* q,
  *   cu_seqlens_k[s]..cu_seqlens_k[s+1] (device int32 arrays of num_seqs + 1 entries; pass the same
  *   array twice for self-attention). max_seqlen_q must bound every sequence's query count.
  *   causal : sp_causal; window_left >= 0 adds the sliding window (see above).
- * Softmax and accumulation are fp32; a query that sees no key gets zeros. bf16 and f16,
- * head_dim 64 or 128, GQA groups of any size.
+ * Softmax and accumulation are fp32; a query that sees no key gets zeros. f32 (fp32 MFMA, fp32
+ * weights: the reference flash_attention's element type), bf16 and f16 (16-bit weights on the
+ * bf16/f16 MFMA), head_dim 64 or 128, GQA groups of any size.
  */
 int sp_varlen_prefill(void* out, const void* q, const void* k, const void* v,
                       const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,

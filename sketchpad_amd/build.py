@@ -41,7 +41,7 @@ DEVICE_FLAGS = [
     f"-I{CSRC}",
 ]
 
-LIB_SOURCES = ["kv_cache.hip", "paged_decode.hip", "prefill.hip", "rope_append.hip",
+LIB_SOURCES = ["kv_cache.hip", "paged_decode.hip", "prefill.hip", "prefill_f32.hip", "rope_append.hip",
                "polar_cache.hip", "linear.hip", "capi.cpp"]
 HOST_SOURCES = ["paged_attention.cpp", "continuous_batching.cpp", "ragged_batch.cpp"]
 

@@ -302,7 +302,6 @@ static int check_prefill_common(const char* fn, int32_t num_seqs, int32_t max_se
                                 int32_t hq, int32_t hkv, int32_t D, float scale,
                                 int32_t causal, int32_t window_left, sp_dtype dtype) {
   if (int rc = check_dtype(dtype, fn)) return rc;
-  if (dtype == SP_F32) return fail(SP_EUNSUPPORTED, "%s: f32 prefill has no kernel yet", fn);
   if (num_seqs < 0 || max_seqlen_q < 0 || hq <= 0 || hkv <= 0)
     return fail(SP_EINVAL, "%s: invalid sizes (num_seqs=%d max_seqlen_q=%d hq=%d hkv=%d)", fn,
                 num_seqs, max_seqlen_q, hq, hkv);

@@ -638,6 +638,10 @@ int launch_prefill(const PrefillArgs& args, sp_dtype dtype, int head_dim, bool p
                    hipStream_t stream) {
   PrefillArgs a = args;
   if (a.nsplit < 1 || !a.partials) a.nsplit = 1;
+  if (dtype == SP_F32) {
+    a.nsplit = 1;  // the fp32 kernel walks every key tile itself (no split partials)
+    return launch_prefill_f32(a, head_dim, paged, stream);
+  }
   switch (dtype) {
     case SP_BF16: return launch_t<bf16_t>(a, head_dim, paged, stream);
     case SP_F16: return launch_t<f16_t>(a, head_dim, paged, stream);

@@ -52,5 +52,7 @@ size_t prefill_partials_bytes(int num_seqs, int max_seqlen_q, int hq, int head_d
 
 int launch_prefill(const PrefillArgs& a, sp_dtype dtype, int head_dim, bool paged,
                    hipStream_t stream);
+// fp32 tensors (prefill_f32.hip); called by launch_prefill for SP_F32.
+int launch_prefill_f32(const PrefillArgs& a, int head_dim, bool paged, hipStream_t stream);
 
 }  // namespace sp

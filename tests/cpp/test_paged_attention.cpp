@@ -275,6 +275,41 @@ TEST(test_flash_attention_causal_bf16, true) {
   }
 }
 
+TEST(test_flash_attention_f32, true) {
+  // f32 is the element type the reference's flash tests run (correctness_cpu.rs:1104-1234);
+  // checked per output row at 1e-5 relative against a double-precision host computation
+  for (auto shp : {std::vector<int>{1, 4, 16, 64}, std::vector<int>{2, 8, 64, 64},
+                   std::vector<int>{1, 2, 100, 128}}) {
+    for (bool causal : {false, true}) {
+      const int B = shp[0], H = shp[1], S = shp[2], D = shp[3];
+      const size_t n = (size_t)B * H * S * D;
+      auto qf = randn(n, 400 + S), kf = randn(n, 500 + S), vf = randn(n, 600 + S);
+      const std::vector<int64_t> shape = {B, H, S, D};
+      auto q = DeviceTensor::from_host(qf.data(), shape, SP_F32);
+      auto k = DeviceTensor::from_host(kf.data(), shape, SP_F32);
+      auto v = DeviceTensor::from_host(vf.data(), shape, SP_F32);
+      auto r = flash_attention(q, k, v, FlashAttentionOptions().with_causal(causal));
+      CHECK(r.is_ok());
+      if (!r.is_ok()) continue;
+      CHECK(hipDeviceSynchronize() == hipSuccess);
+      std::vector<float> oh(n);
+      r.out->to_host(oh.data());
+      std::vector<double> ref;
+      host_attention(qf, kf, vf, B, H, S, S, D, causal, ref);
+      double worst = 0;
+      for (size_t row = 0; row < n / D; ++row) {
+        double scale = 1e-30, err = 0;
+        for (int d = 0; d < D; ++d) {
+          scale = fmax(scale, fabs(ref[row * D + d]));
+          err = fmax(err, fabs((double)oh[row * D + d] - ref[row * D + d]));
+        }
+        worst = fmax(worst, err / scale);
+      }
+      CHECK(worst <= 1e-5);
+    }
+  }
+}
+
 TEST(test_flash_attention_setup_errors, true) {
   DeviceTensor q({1, 2, 8, 64}, SP_BF16), k({1, 2, 8, 32}, SP_BF16);
   auto r = flash_attention(q, k, k, FlashAttentionOptions());

@@ -13,7 +13,7 @@ from tests.helpers import announce, assert_attention_close, host_array, oracle_d
 
 pytestmark = pytest.mark.gpu
 
-DT = {"bf16": torch.bfloat16, "f16": torch.float16}
+DT = {"bf16": torch.bfloat16, "f16": torch.float16, "f32": torch.float32}
 
 
 def _rand(g, *shape, dt):
@@ -40,7 +40,11 @@ def _as_f64(t):
     return t.float().cpu().numpy().astype(np.float64)
 
 
-def run_varlen(lens_q, lens_k, hq, hkv, d, dtype, causal, window, seed, inputs=None):
+def run_varlen(lens_q, lens_k, hq, hkv, d, dtype, causal, window, seed, inputs=None,
+               f32_bar="abs"):
+    """f32_bar: "abs" checks f32 outputs at 1e-5 per row against the f64 oracle; "refops" (for
+    inputs whose scores are so large that fp32 rounding of the scores alone exceeds that) bounds
+    the worst and mean row error by twice those of the reference's own f32 op order."""
     g = torch.Generator(device="cuda").manual_seed(seed)
     dt = DT[dtype]
     cu_q = np.concatenate([[0], np.cumsum(lens_q)]).astype(np.int32)
@@ -60,6 +64,28 @@ def run_varlen(lens_q, lens_k, hq, hkv, d, dtype, causal, window, seed, inputs=N
     # the oracle reads 16-bit tensors as bf16 bits; f16 inputs are handed over as float32
     to_host = host_array if dtype == "bf16" else (lambda t: t.float().cpu().numpy())
     ref = _oracle_varlen(to_host(q), to_host(k), to_host(v), cu_q, cu_k, d ** -0.5, causal, window)
+    if dtype == "f32" and f32_bar == "refops":
+        got = _as_f64(out)
+        r32 = np.zeros_like(ref)
+        qh, kh, vh = to_host(q), to_host(k), to_host(v)
+        for s_ in range(len(cu_q) - 1):
+            qa, qb, ka, kb = cu_q[s_], cu_q[s_ + 1], cu_k[s_], cu_k[s_ + 1]
+            if qb == qa:
+                continue
+            pos0 = 0 if causal == sp.SP_CAUSAL_TOP_LEFT else (kb - ka) - (qb - qa)
+            r32[qa:qb] = O.attention_f32_refops(qh[qa:qb], kh[ka:kb], vh[ka:kb], scale=d ** -0.5,
+                                                causal=causal != sp.SP_CAUSAL_NONE, q_pos0=pos0,
+                                                window_left=window)
+        row = np.maximum(np.abs(ref).max(axis=-1, keepdims=True), 1e-30)
+        ours = (np.abs(got - ref) / row).max(axis=-1)
+        theirs = (np.abs(r32 - ref) / row).max(axis=-1)
+        # per-row errors of two fp32 computations scatter independently, so the distributions
+        # are compared: the worst and the mean row within twice the reference op order's
+        assert ours.max() <= max(1e-5, 2 * theirs.max()), (
+            f"f32 worst row {ours.max():.3e} vs reference op order {theirs.max():.3e}")
+        assert ours.mean() <= max(1e-5, 2 * theirs.mean()), (
+            f"f32 mean row {ours.mean():.3e} vs reference op order {theirs.mean():.3e}")
+        return
     assert_attention_close(_as_f64(out), ref, dtype, "varlen prefill")
 
 
@@ -137,6 +163,54 @@ def test_varlen_empty_sequences():
     run_varlen(lens, lens, 4, 2, 64, "bf16", sp.SP_CAUSAL_BOTTOM_RIGHT, -1, seed=31)
 
 
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("hq,hkv", [(4, 4), (8, 2)])
+def test_varlen_f32(d, hq, hkv):
+    """fp32 prefill (fp32 MFMA, fp32 P): within 1e-5 of the f64 oracle per output row."""
+    lens = [1, 17, 31, 32, 33, 64, 127, 129, 300]
+    run_varlen(lens, lens, hq, hkv, d, "f32", sp.SP_CAUSAL_BOTTOM_RIGHT, -1, seed=51 + d + hq)
+
+
+@pytest.mark.parametrize("causal", [sp.SP_CAUSAL_NONE, sp.SP_CAUSAL_TOP_LEFT])
+def test_varlen_f32_cross_lengths_and_window(causal):
+    lens_q = [3, 40, 130, 1]
+    lens_k = [10, 200, 130, 77]
+    run_varlen(lens_q, lens_k, 8, 4, 64, "f32", causal, -1, seed=61 + causal)
+    run_varlen([150, 300], [150, 300], 4, 2, 128, "f32", sp.SP_CAUSAL_BOTTOM_RIGHT, 40,
+               seed=63)
+
+
+@pytest.mark.parametrize("mode", ["neg", "wide"])
+def test_varlen_f32_score_range(mode):
+    lens = [1, 70, 200]
+    run_varlen(lens, lens, 4, 2, 128, "f32", sp.SP_CAUSAL_BOTTOM_RIGHT, -1, seed=65,
+               inputs=_score_range_inputs(mode, 4, 2, 128, seed=65), f32_bar="refops")
+
+
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("sq,sk,d", [(77, 77, 64), (256, 256, 128), (40, 300, 64)])
+def test_flash_attention_f32(causal, sq, sk, d):
+    """flash_attention in f32, the element type the reference's flash_attention runs
+    (sketchpad-cubecl attention.rs:21-25): [B, H, S, D], top-left causal, 1e-5 relative."""
+    B, H = 2, 3
+    g = torch.Generator(device="cuda").manual_seed(sq * 3 + sk + causal)
+    q = _rand(g, B, H, sq, d, dt=torch.float32)
+    k = _rand(g, B, H, sk, d, dt=torch.float32)
+    v = _rand(g, B, H, sk, d, dt=torch.float32)
+    out = torch.full_like(q, float("nan"))
+    announce(f"flash_attention f32 sq={sq} sk={sk} d={d} causal={causal}")
+    sp.flash_attention(out, q, k, v, d ** -0.5, causal=causal)
+    torch.cuda.synchronize()
+    qh, kh, vh = (x.cpu().numpy() for x in (q, k, v))
+    ref = np.zeros((B, H, sq, d))
+    for bi in range(B):
+        r = O.attention_f64(qh[bi].transpose(1, 0, 2), kh[bi].transpose(1, 0, 2),
+                            vh[bi].transpose(1, 0, 2), scale=d ** -0.5, causal=causal, q_pos0=0,
+                            dtype=O.F32)
+        ref[bi] = r.transpose(1, 0, 2)
+    assert_attention_close(_as_f64(out), ref, "f32", "flash_attention f32")
+
+
 @pytest.mark.parametrize("causal", [False, True])
 @pytest.mark.parametrize("sq,sk", [(16, 16), (64, 64), (130, 70), (33, 200)])
 def test_flash_attention_dense(causal, sq, sk):
@@ -195,7 +269,7 @@ def run_chunked(w: W.ChunkedPrefillWorkload, sample_rows=None, split=False):
             pos = L - lq + i
             ref = O.attention_f64(q[cu[s] + i:cu[s] + i + 1], kt[:pos + 1], vt[:pos + 1],
                                   scale=w.head_dim ** -0.5, causal=True, q_pos0=pos,
-                                  window_left=w.window_left, dtype=O.BF16)
+                                  window_left=w.window_left, dtype=oracle_dtype(t["q"]))
             assert_attention_close(got[cu[s] + i:cu[s] + i + 1], ref, w.dtype,
                                    f"{w.name} seq {s} row {i}")
     return t
@@ -210,6 +284,15 @@ def test_paged_prefill_small():
 def test_paged_prefill_window():
     w = W.ChunkedPrefillWorkload("chunked-window", 42, np.array([50, 129], np.int32),
                                  np.array([200, 90], np.int32), 8, 2, 64, "bf16", window_left=70)
+    run_chunked(w)
+
+
+@pytest.mark.parametrize("window", [-1, 50])
+def test_paged_prefill_f32(window):
+    """Chunked prefill on an f32 paged cache (the reference cache's default element type)."""
+    w = W.ChunkedPrefillWorkload("chunked-f32", 53, np.array([1, 40, 130], np.int32),
+                                 np.array([0, 300, 77], np.int32), 8, 2, 64, "f32",
+                                 window_left=window)
     run_chunked(w)
 
 
