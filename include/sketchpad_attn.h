@@ -245,6 +245,21 @@ int sp_flash_attention(void* out, const void* q, const void* k, const void* v,
                        void* stream);
 
 /*
+ * flash_attention_masked (sketchpad-cubecl attention.rs:119-128): sp_flash_attention plus an
+ * additive mask, out = softmax(q k^T scale + mask) v, f32 tensors (the element type the
+ * reference's flash_attention runs; 16-bit inputs return SP_EUNSUPPORTED). mask is f32
+ * [batch, heads, seq_q, seq_k] addressed as b*mask_stride_b + h*mask_stride_h + i*mask_stride_q
+ * + j elements: stride 0 broadcasts (the reference's tests expand one [seq_q, seq_k] mask).
+ * Masked entries are -inf or large negatives; causal != 0 also applies the j > i mask. A query
+ * whose every key is masked gets zeros.
+ */
+int sp_flash_attention_masked(void* out, const void* q, const void* k, const void* v,
+                              const float* mask, int64_t mask_stride_b, int64_t mask_stride_h,
+                              int64_t mask_stride_q, int32_t batch, int32_t num_heads,
+                              int32_t seq_q, int32_t seq_k, int32_t head_dim, float scale,
+                              int32_t causal, sp_dtype dtype, void* stream);
+
+/*
  * ---- PolarQuant compressed paged cache ----------------------------------------------------
  * KvQuantMethod::PolarQuant of CompressedKvCache (crates/sketchpad-core/src/kv_cache.rs:300-324,
  * :437-532, used at :640-727). A head_dim vector x is stored as a record of

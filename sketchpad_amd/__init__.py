@@ -15,6 +15,7 @@ from ._lib import (  # noqa: F401
     SP_F32,
     alloc_decode_workspace,
     flash_attention,
+    flash_attention_masked,
     kv_append,
     kv_gather,
     layout,

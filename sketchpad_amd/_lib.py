@@ -84,6 +84,10 @@ _SIGNATURES = {
     "sp_flash_attention": (c_int32, [c_void_p, c_void_p, c_void_p, c_void_p, c_int32, c_int32,
                                      c_int32, c_int32, c_int32, c_float, c_int32, c_int32,
                                      c_void_p]),
+    "sp_flash_attention_masked": (c_int32, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+                                            c_int64, c_int64, c_int64, c_int32, c_int32, c_int32,
+                                            c_int32, c_int32, c_float, c_int32, c_int32,
+                                            c_void_p]),
     "sp_polar_record_bytes": (c_int64, [c_int32]),
     "sp_polar_pool_bytes": (c_size_t, [POINTER(CacheLayout)]),
     "sp_polar_compress": (c_int32, [c_void_p, c_void_p, c_int64, c_int32, c_int32, c_void_p]),
@@ -281,6 +285,21 @@ def paged_prefill(out, q, k_pool, v_pool, lay: CacheLayout, block_tables, cu_seq
                                   _ptr(cu_seqlens_q), _ptr(context_lens),
                                   cu_seqlens_q.numel() - 1, max_seqlen_q, q.shape[1], scale,
                                   window_left, sp_dtype(q), ws_ptr, ws_bytes, _stream(stream)))
+
+
+def flash_attention_masked(out, q, k, v, mask, scale: float, *, causal: bool = False,
+                           stream=None) -> None:
+    """sp_flash_attention_masked on f32 [B, H, S, D] tensors; mask: an f32 tensor that expands
+    to [B, H, Sq, Sk] (its strides are passed, so broadcast views work; last stride 1)."""
+    b, h, sq, d = q.shape
+    sk = k.shape[2]
+    m = mask.expand(b, h, sq, sk)
+    if sk > 1 and m.stride(3) != 1:
+        raise ValueError("mask: the key dimension must be contiguous")
+    check(load().sp_flash_attention_masked(_ptr(out), _ptr(q), _ptr(k), _ptr(v), _ptr(m),
+                                           m.stride(0), m.stride(1), m.stride(2), b, h, sq, sk,
+                                           d, scale, int(bool(causal)), sp_dtype(q),
+                                           _stream(stream)))
 
 
 def flash_attention(out, q, k, v, scale: float, *, causal: bool = False, stream=None) -> None:

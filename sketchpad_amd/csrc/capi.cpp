@@ -436,10 +436,11 @@ int sp_paged_prefill(void* out, const void* q, const void* k_pool, const void* v
   return launch_prefill(a, dtype, D, true, (hipStream_t)stream);
 }
 
-int sp_flash_attention(void* out, const void* q, const void* k, const void* v, int32_t batch,
-                       int32_t num_heads, int32_t seq_q, int32_t seq_k, int32_t head_dim,
-                       float scale, int32_t causal, sp_dtype dtype, void* stream) {
-  const char* fn = "sp_flash_attention";
+static int flash_attention_impl(const char* fn, void* out, const void* q, const void* k,
+                                const void* v, const float* mask, int64_t mask_stride_b,
+                                int64_t mask_stride_h, int64_t mask_stride_q, int32_t batch,
+                                int32_t num_heads, int32_t seq_q, int32_t seq_k, int32_t head_dim,
+                                float scale, int32_t causal, sp_dtype dtype, void* stream) {
   if (int rc = check_prefill_common(fn, batch, seq_q, num_heads, num_heads, head_dim, scale,
                                     causal ? SP_CAUSAL_TOP_LEFT : SP_CAUSAL_NONE, -1, dtype))
     return rc;
@@ -469,7 +470,39 @@ int sp_flash_attention(void* out, const void* q, const void* k, const void* v, i
   a.causal = causal ? SP_CAUSAL_TOP_LEFT : SP_CAUSAL_NONE;
   a.window_left = -1;
   a.scale_log2 = scale * 1.4426950408889634f;
+  a.mask = mask;
+  a.mask_b = mask_stride_b;
+  a.mask_h = mask_stride_h;
+  a.mask_q = mask_stride_q;
+  a.inv_scale = 1.f / scale;
   return launch_prefill(a, dtype, head_dim, false, (hipStream_t)stream);
+}
+
+int sp_flash_attention(void* out, const void* q, const void* k, const void* v, int32_t batch,
+                       int32_t num_heads, int32_t seq_q, int32_t seq_k, int32_t head_dim,
+                       float scale, int32_t causal, sp_dtype dtype, void* stream) {
+  return flash_attention_impl("sp_flash_attention", out, q, k, v, nullptr, 0, 0, 0, batch,
+                              num_heads, seq_q, seq_k, head_dim, scale, causal, dtype, stream);
+}
+
+int sp_flash_attention_masked(void* out, const void* q, const void* k, const void* v,
+                              const float* mask, int64_t mask_stride_b, int64_t mask_stride_h,
+                              int64_t mask_stride_q, int32_t batch, int32_t num_heads,
+                              int32_t seq_q, int32_t seq_k, int32_t head_dim, float scale,
+                              int32_t causal, sp_dtype dtype, void* stream) {
+  const char* fn = "sp_flash_attention_masked";
+  if (dtype != SP_F32)
+    return fail(dtype == SP_BF16 || dtype == SP_F16 ? SP_EUNSUPPORTED : SP_EINVAL,
+                "%s: the additive mask is supported for f32 tensors only (the reference's "
+                "flash_attention element type), got %s",
+                fn, dtype_name(dtype));
+  if (!mask && batch > 0 && seq_q > 0 && seq_k > 0)
+    return fail(SP_EINVAL, "%s: NULL mask", fn);
+  if (mask_stride_b < 0 || mask_stride_h < 0 || mask_stride_q < 0)
+    return fail(SP_EINVAL, "%s: negative mask stride", fn);
+  return flash_attention_impl(fn, out, q, k, v, mask, mask_stride_b, mask_stride_h, mask_stride_q,
+                              batch, num_heads, seq_q, seq_k, head_dim, scale, causal, dtype,
+                              stream);
 }
 
 // ---------------------------------------------------------------------------------------------

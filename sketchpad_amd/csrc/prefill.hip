@@ -638,6 +638,8 @@ int launch_prefill(const PrefillArgs& args, sp_dtype dtype, int head_dim, bool p
                    hipStream_t stream) {
   PrefillArgs a = args;
   if (a.nsplit < 1 || !a.partials) a.nsplit = 1;
+  if (a.mask && dtype != SP_F32)
+    return fail(SP_EUNSUPPORTED, "prefill: an additive mask needs f32 tensors");
   if (dtype == SP_F32) {
     a.nsplit = 1;  // the fp32 kernel walks every key tile itself (no split partials)
     return launch_prefill_f32(a, head_dim, paged, stream);

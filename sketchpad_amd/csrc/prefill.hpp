@@ -42,6 +42,11 @@ struct PrefillArgs {
   float* partials;
   int nsplit;
   int max_q;  // max_seqlen_q: the partials' per-sequence row stride
+  // additive mask of the dense f32 path (flash_attention_masked): mask[b][h][i][j] at element
+  // offset b mask_b + h mask_h + i mask_q + j, added to score * scale; nullptr: none
+  const float* mask;
+  int64_t mask_b, mask_h, mask_q;
+  float inv_scale;  // 1 / scale
 };
 
 // Split count for a chunked prefill of base_wgs workgroups whose sequences span up to

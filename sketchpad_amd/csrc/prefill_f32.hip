@@ -177,6 +177,10 @@ __global__ void __launch_bounds__(256, 2) prefill_f32_kernel(PrefillArgs a) {
   const bool wave_active = wq_lo < qe;
   const int qpos = my_q + pos_off;
   const float c2 = a.scale_log2;  // > 0 (checked on the host)
+  // this lane's row of the additive mask (dense path: the sequence index is the batch index)
+  const float* mrow = a.mask ? a.mask + (int64_t)seq * a.mask_b + (int64_t)h * a.mask_h +
+                                   (int64_t)min(my_q, qe - 1) * a.mask_q
+                             : nullptr;
   // masks only on tiles that start before kv_lo or this wave's window edge, or run past the
   // sequence end or this wave's first causal diagonal
   int mask_below = kv_lo, mask_above = Lk - BN;
@@ -203,6 +207,17 @@ __global__ void __launch_bounds__(256, 2) prefill_f32_kernel(PrefillArgs a) {
     }
     s += s1;
     // score r of this lane is key t0 + 4hh + 8(r/4) + r%4
+    if (a.mask) {
+      // additive mask (flash_attention_masked): softmax(q.k scale + mask) = softmax over
+      // (q.k + mask / scale) scale. Keys past the sequence end read its last column; their
+      // scores are masked below (such tiles always take the mask).
+      const int jb = t0 + 4 * hh;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int key = min(jb + 8 * (r >> 2) + (r & 3), Lk - 1);
+        s[r] += mrow[key] * a.inv_scale;
+      }
+    }
     if (t0 < mask_below || t0 > mask_above) {
       int lo = kv_lo, hi = Lk - 1;
       if (a.causal != SP_CAUSAL_NONE) hi = min(hi, qpos);

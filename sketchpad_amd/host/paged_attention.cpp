@@ -4,6 +4,8 @@
 // concatenating KvCache.
 #include "paged_attention.hpp"
 
+#include <optional>
+
 #include <math.h>
 
 #include <numeric>
@@ -332,33 +334,75 @@ std::vector<float> causal_mask(size_t seq_len) {
   return m;
 }
 
-FlashResult flash_attention(const DeviceTensor& query, const DeviceTensor& key,
-                            const DeviceTensor& value, const FlashAttentionOptions& options,
-                            hipStream_t stream) {
-  FlashResult r;
+// Shapes and dtypes flash_attention / flash_attention_masked accept; the message otherwise.
+static std::optional<std::string> flash_shape_error(const DeviceTensor& query,
+                                                    const DeviceTensor& key,
+                                                    const DeviceTensor& value,
+                                                    const FlashAttentionOptions& options) {
   const auto& q = query.dims();
   const auto& k = key.dims();
   const auto& v = value.dims();
   if (q.size() != 4 || k.size() != 4 || v.size() != 4 || k[0] != q[0] || k[1] != q[1] ||
-      k[3] != q[3] || v[0] != k[0] || v[1] != k[1] || v[2] != k[2]) {
-    r.error = AttentionSetupError{"flash_attention: expected q [B,H,Sq,D], k [B,H,Sk,D], "
-                                  "v [B,H,Sk,Dv]"};
-    return r;
-  }
-  if (v[3] != q[3]) {
-    r.error = AttentionSetupError{"flash_attention: value head_dim must equal the query's"};
-    return r;
-  }
+      k[3] != q[3] || v[0] != k[0] || v[1] != k[1] || v[2] != k[2])
+    return std::string("flash_attention: expected q [B,H,Sq,D], k [B,H,Sk,D], v [B,H,Sk,Dv]");
+  if (v[3] != q[3]) return std::string("flash_attention: value head_dim must equal the query's");
   if (key.dtype() != query.dtype() || value.dtype() != query.dtype() ||
-      options.out_dtype.value_or(query.dtype()) != query.dtype()) {
-    r.error = AttentionSetupError{"flash_attention: mixed dtypes are not supported"};
+      options.out_dtype.value_or(query.dtype()) != query.dtype())
+    return std::string("flash_attention: mixed dtypes are not supported");
+  return std::nullopt;
+}
+
+FlashResult flash_attention(const DeviceTensor& query, const DeviceTensor& key,
+                            const DeviceTensor& value, const FlashAttentionOptions& options,
+                            hipStream_t stream) {
+  FlashResult r;
+  if (auto e = flash_shape_error(query, key, value, options)) {
+    r.error = AttentionSetupError{*e};
     return r;
   }
-  DeviceTensor out({q[0], q[1], q[2], v[3]}, query.dtype());
+  const auto& q = query.dims();
+  const auto& k = key.dims();
+  DeviceTensor out({q[0], q[1], q[2], q[3]}, query.dtype());
   const int rc = sp_flash_attention(out.data(), query.data(), key.data(), value.data(),
                                     (int32_t)q[0], (int32_t)q[1], (int32_t)q[2], (int32_t)k[2],
                                     (int32_t)q[3], (float)pow((double)q[3], -0.5),
                                     options.causal ? 1 : 0, query.dtype(), stream);
+  if (rc != SP_OK) {
+    r.error = AttentionSetupError{sp_last_error()};
+    return r;
+  }
+  r.out = out;
+  return r;
+}
+
+FlashResult flash_attention_masked(const DeviceTensor& query, const DeviceTensor& key,
+                                   const DeviceTensor& value, const DeviceTensor& mask,
+                                   const FlashAttentionOptions& options, hipStream_t stream) {
+  FlashResult r;
+  if (auto e = flash_shape_error(query, key, value, options)) {
+    r.error = AttentionSetupError{*e};
+    return r;
+  }
+  const auto& q = query.dims();
+  const auto& k = key.dims();
+  const auto& m = mask.dims();
+  int64_t sb = 0, sh = 0;
+  if (mask.dtype() != SP_F32) {
+    r.error = AttentionSetupError{"flash_attention_masked: the mask must be f32"};
+    return r;
+  }
+  if (m.size() == 4 && m[0] == q[0] && m[1] == q[1] && m[2] == q[2] && m[3] == k[2]) {
+    sb = q[1] * q[2] * k[2];
+    sh = q[2] * k[2];
+  } else if (!(m.size() == 2 && m[0] == q[2] && m[1] == k[2])) {
+    r.error = AttentionSetupError{"flash_attention_masked: mask must be [B,H,Sq,Sk] or [Sq,Sk]"};
+    return r;
+  }
+  DeviceTensor out({q[0], q[1], q[2], q[3]}, query.dtype());
+  const int rc = sp_flash_attention_masked(
+      out.data(), query.data(), key.data(), value.data(), (const float*)mask.data(), sb, sh,
+      k[2], (int32_t)q[0], (int32_t)q[1], (int32_t)q[2], (int32_t)k[2], (int32_t)q[3],
+      (float)pow((double)q[3], -0.5), options.causal ? 1 : 0, query.dtype(), stream);
   if (rc != SP_OK) {
     r.error = AttentionSetupError{sp_last_error()};
     return r;

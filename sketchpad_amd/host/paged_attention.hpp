@@ -346,4 +346,12 @@ FlashResult flash_attention(const DeviceTensor& query, const DeviceTensor& key,
                             const DeviceTensor& value, const FlashAttentionOptions& options,
                             hipStream_t stream = nullptr);
 
+// flash_attention_masked (sketchpad-cubecl attention.rs:119-128): additive f32 mask,
+// [B, H, Sq, Sk] or one [Sq, Sk] mask for every batch and head (the reference's tests expand
+// one [Sq, Sk] mask); f32 tensors.
+FlashResult flash_attention_masked(const DeviceTensor& query, const DeviceTensor& key,
+                                   const DeviceTensor& value, const DeviceTensor& mask,
+                                   const FlashAttentionOptions& options,
+                                   hipStream_t stream = nullptr);
+
 }  // namespace sketchpad

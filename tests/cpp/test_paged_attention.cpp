@@ -310,6 +310,44 @@ TEST(test_flash_attention_f32, true) {
   }
 }
 
+TEST(test_flash_attention_masked_f32, true) {
+  // flash_attention_masked (attention.rs:119-128): an all-zero mask reproduces flash_attention
+  // bit for bit, and the reference tests' additive causal mask (-inf above the diagonal, one
+  // [Sq, Sk] mask expanded over batch and heads) reproduces causal flash_attention bit for bit
+  const int B = 2, H = 2, S = 70, D = 64;
+  const size_t n = (size_t)B * H * S * D;
+  auto qf = randn(n, 700), kf = randn(n, 701), vf = randn(n, 702);
+  const std::vector<int64_t> shape = {B, H, S, D};
+  auto q = DeviceTensor::from_host(qf.data(), shape, SP_F32);
+  auto k = DeviceTensor::from_host(kf.data(), shape, SP_F32);
+  auto v = DeviceTensor::from_host(vf.data(), shape, SP_F32);
+  std::vector<float> zero((size_t)S * S, 0.f), causal((size_t)S * S, 0.f);
+  for (int i = 0; i < S; ++i)
+    for (int j = i + 1; j < S; ++j) causal[(size_t)i * S + j] = -INFINITY;
+  auto mz = DeviceTensor::from_host(zero.data(), {S, S}, SP_F32);
+  auto mc = DeviceTensor::from_host(causal.data(), {S, S}, SP_F32);
+  auto plain = flash_attention(q, k, v, FlashAttentionOptions());
+  auto plain_c = flash_attention(q, k, v, FlashAttentionOptions::causal_());
+  auto masked0 = flash_attention_masked(q, k, v, mz, FlashAttentionOptions());
+  auto maskedc = flash_attention_masked(q, k, v, mc, FlashAttentionOptions());
+  CHECK(plain.is_ok() && plain_c.is_ok() && masked0.is_ok() && maskedc.is_ok());
+  if (!(plain.is_ok() && plain_c.is_ok() && masked0.is_ok() && maskedc.is_ok())) return;
+  CHECK(hipDeviceSynchronize() == hipSuccess);
+  std::vector<float> a(n), b(n), c(n), d(n);
+  plain.out->to_host(a.data());
+  masked0.out->to_host(b.data());
+  plain_c.out->to_host(c.data());
+  maskedc.out->to_host(d.data());
+  CHECK(memcmp(a.data(), b.data(), n * 4) == 0);
+  CHECK(memcmp(c.data(), d.data(), n * 4) == 0);
+  // 16-bit tensors and malformed masks are setup errors, not launches
+  DeviceTensor qb({1, 2, 8, 64}, SP_BF16);
+  auto mb = DeviceTensor::from_host(zero.data(), {8, 8}, SP_F32);
+  CHECK(!flash_attention_masked(qb, qb, qb, mb, FlashAttentionOptions()).is_ok());
+  auto bad = DeviceTensor::from_host(zero.data(), {S, S - 1}, SP_F32);
+  CHECK(!flash_attention_masked(q, k, v, bad, FlashAttentionOptions()).is_ok());
+}
+
 TEST(test_flash_attention_setup_errors, true) {
   DeviceTensor q({1, 2, 8, 64}, SP_BF16), k({1, 2, 8, 32}, SP_BF16);
   auto r = flash_attention(q, k, k, FlashAttentionOptions());

@@ -171,6 +171,18 @@ def test_workspace_size_monotone(sp_lib):
     assert w1 == w2 > 0
 
 
+def test_flash_attention_masked_validation(sp_lib):
+    """The additive mask is an f32 path: 16-bit tensors are unsupported, a NULL mask or a
+    negative stride is invalid (all checked before any launch)."""
+    def call(dtype, mask=1 << 20, sb=0):
+        return sp_lib.sp_flash_attention_masked(16, 16, 16, 16, mask, sb, 0, 8, 1, 2, 8, 8, 64,
+                                                0.125, 0, dtype, None)
+    assert call(_lib.SP_BF16) == _lib.SP_EUNSUPPORTED
+    assert call(_lib.SP_F16) == _lib.SP_EUNSUPPORTED
+    assert call(_lib.SP_F32, mask=None) == _lib.SP_EINVAL
+    assert call(_lib.SP_F32, sb=-1) == _lib.SP_EINVAL
+
+
 def test_paged_prefill_workspace_size(sp_lib):
     """Key splits are planned only for few query blocks over long contexts: C4's shape (4 x 512
     queries, 28 heads, contexts up to 428 blocks of 16) gets 2 splits of fp32 (m, l, acc) records;

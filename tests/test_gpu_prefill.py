@@ -212,6 +212,39 @@ def test_flash_attention_f32(causal, sq, sk, d):
 
 
 @pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("per_head", [False, True])
+def test_flash_attention_masked_f32(causal, per_head):
+    """flash_attention_masked (sketchpad-cubecl attention.rs:119-128): additive f32 mask, either
+    one [Sq, Sk] mask for every batch and head (as the reference's tests expand it) or a full
+    [B, H, Sq, Sk] one; random biases, padded keys at -inf, 1e-5 per row vs the f64 oracle."""
+    B, H, sq, sk, d = 2, 3, 90, 150, 64
+    g = torch.Generator(device="cuda").manual_seed(71 + causal + 2 * per_head)
+    q, k, v = (_rand(g, B, H, n, d, dt=torch.float32) for n in (sq, sk, sk))
+    mshape = (B, H, sq, sk) if per_head else (sq, sk)
+    mask = 2.0 * torch.randn(*mshape, generator=g, device="cuda")
+    mask[..., sk - 7:] = float("-inf")   # padded keys
+    # large finite negatives on half of a row, beside keys that stay visible (were they a row's
+    # only keys, fp32 could not hold score differences next to -1e4, nor could the reference's)
+    mask[..., 5, sk // 2:] = -1e4
+    out = torch.full_like(q, float("nan"))
+    announce(f"flash_attention_masked f32 per_head={per_head} causal={causal}")
+    sp.flash_attention_masked(out, q, k, v, mask, d ** -0.5, causal=causal)
+    torch.cuda.synchronize()
+    qh, kh, vh = (x.cpu().numpy() for x in (q, k, v))
+    mh = mask.expand(B, H, sq, sk).cpu().numpy()
+    if causal:  # the oracle takes an explicit mask instead of its causal predicate: fold it in
+        i, j = np.arange(sq)[:, None], np.arange(sk)[None, :]
+        mh = mh + np.where(j > i, -np.inf, 0.0).astype(np.float32)
+    ref = np.zeros((B, H, sq, d))
+    for bi in range(B):
+        for hi in range(H):
+            ref[bi, hi] = O.attention_f64(qh[bi, hi][:, None], kh[bi, hi][:, None],
+                                          vh[bi, hi][:, None], scale=d ** -0.5, mask=mh[bi, hi],
+                                          q_pos0=0, dtype=O.F32)[:, 0]
+    assert_attention_close(_as_f64(out), ref, "f32", "flash_attention_masked")
+
+
+@pytest.mark.parametrize("causal", [False, True])
 @pytest.mark.parametrize("sq,sk", [(16, 16), (64, 64), (130, 70), (33, 200)])
 def test_flash_attention_dense(causal, sq, sk):
     """flash_attention on [B, H, S, D]; causal is the reference test oracle's j > i mask."""
