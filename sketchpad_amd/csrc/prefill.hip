@@ -555,21 +555,25 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PrefillArgs a) {
     }
 }
 
-// Merge the split partials of one (sequence, query block, head): out = sum_s 2^(m_s - M) acc_s /
-// sum_s 2^(m_s - M) l_s, M = max_s m_s (zeros when no split saw a key). D/4 lanes per row, four
-// output elements each.
+// Merge the split partials of one (sequence, head, group of kCombineRows query rows):
+// out = sum_s 2^(m_s - M) acc_s / sum_s 2^(m_s - M) l_s, M = max_s m_s (zeros when no split saw
+// a key). D/4 lanes per row, four output elements each, one row per lane group, so every row's
+// loads are in flight at once.
+constexpr int kCombineRows = 8;
+
 template <typename T, int D>
 __global__ void __launch_bounds__(256) prefill_combine_kernel(PrefillArgs a) {
   using M = PrefillMfma<T>;
-  constexpr int TPR = D / 4, RPP = 256 / TPR;
+  constexpr int TPR = D / 4, RPP = 256 / TPR;  // lanes per row, rows per workgroup pass
+  static_assert(RPP >= kCombineRows, "a workgroup covers its row group in one pass");
   const int h = blockIdx.x % a.hq;
   const int id = blockIdx.x / a.hq;
-  const int seq = id % a.num_seqs, qblk = id / a.num_seqs;
+  const int seq = id % a.num_seqs, grp = id / a.num_seqs;
   const int q_begin = a.cu_q[seq];
   const int Lq = a.cu_q[seq + 1] - q_begin;
-  const int qs = qblk * kPrefillBM;
+  const int qs = grp * kCombineRows;
   if (qs >= Lq) return;
-  const int qe = min(qs + kPrefillBM, Lq);
+  const int qe = min(qs + kCombineRows, Lq);
   const int c = threadIdx.x % TPR;
   for (int q = qs + (int)threadIdx.x / TPR; q < qe; q += RPP) {
     const float* rec =
@@ -619,7 +623,9 @@ static int launch_td(const PrefillArgs& a, bool paged, hipStream_t stream) {
     hipLaunchKernelGGL((prefill_kernel<T, D, false>), dim3((unsigned)blocks), dim3(256), 0, stream, a);
   if (int rc = check_launch("prefill_kernel")) return rc;
   if (a.nsplit > 1) {
-    hipLaunchKernelGGL((prefill_combine_kernel<T, D>), dim3((unsigned)base), dim3(256), 0, stream, a);
+    const int64_t groups = (int64_t)((a.max_q + kCombineRows - 1) / kCombineRows) * a.num_seqs * a.hq;
+    if (groups > 0x7fffffff) return fail(SP_EINVAL, "prefill: combine grid of %lld", (long long)groups);
+    hipLaunchKernelGGL((prefill_combine_kernel<T, D>), dim3((unsigned)groups), dim3(256), 0, stream, a);
     return check_launch("prefill_combine_kernel");
   }
   return SP_OK;
