@@ -298,6 +298,27 @@ int sp_polar_decompress(void* out, const void* records, int64_t num_vecs, int32_
                         sp_dtype dtype, void* stream);
 
 /*
+ * QJL codec (KvQuantMethod::QJL, kv_cache.rs:300-324, :534-617), the reference's other
+ * compressed cache method: 2 + ceil(proj_dim / 8) bytes per vector, the binary16 magnitude
+ * then bit k = (R[k,:] . x >= 0) (little-endian within each byte); decompression gives
+ * |x| * (pi/2 / proj_dim) * sum_k (+-1)_k R[k,:]. Bit for bit the reference's values.
+ *   sp_qjl_projection : fills host memory out[proj_dim * head_dim] with the reference's fixed
+ *                       projection R ~ N(0, 1/proj_dim) (its seed-42 LCG + Box-Muller,
+ *                       CompressedKvCache::new, kv_cache.rs:371-396, :417-424); copy it to the
+ *                       device for the two calls below.
+ *   sp_qjl_compress   : x [num_vecs, head_dim] (dtype, converted exactly to f32) -> records
+ *                       [num_vecs, sp_qjl_record_bytes(proj_dim)] (qjl_compress, :534-569)
+ *   sp_qjl_decompress : records -> out [num_vecs, head_dim] (f32 value rounded once to dtype;
+ *                       qjl_decompress, :571-617)
+ */
+int64_t sp_qjl_record_bytes(int32_t proj_dim);
+int sp_qjl_projection(float* out, int32_t proj_dim, int32_t head_dim);
+int sp_qjl_compress(void* records, const void* x, int64_t num_vecs, int32_t head_dim,
+                    const float* projection, int32_t proj_dim, sp_dtype dtype, void* stream);
+int sp_qjl_decompress(void* out, const void* records, int64_t num_vecs, int32_t head_dim,
+                      const float* projection, int32_t proj_dim, sp_dtype dtype, void* stream);
+
+/*
  * Encode on append: the PolarQuant form of sp_kv_append (same slot mapping, strides and skip
  * rules). Replaces the compress-and-extend step of CompressedKvCache::update_layer
  * (kv_cache.rs:665-676) for a paged pool and a ragged batch.

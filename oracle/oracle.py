@@ -42,6 +42,12 @@ _SIG = {
     "spo_polar_compress": (None, [c_void_p, c_void_p, c_int64, c_int64]),
     "spo_polar_decompress": (None, [c_void_p, c_void_p, c_int64, c_int64]),
     "spo_polar_compression_ratio": (c_double, [c_int64]),
+    "spo_qjl_lcg_normal": (None, [c_void_p, c_int64, c_float]),
+    "spo_qjl_projection": (None, [c_void_p, c_int64, c_int64]),
+    "spo_qjl_record_bytes": (c_int64, [c_int64]),
+    "spo_qjl_compress": (None, [c_void_p, c_void_p, c_int64, c_int64, c_void_p, c_int64]),
+    "spo_qjl_decompress": (None, [c_void_p, c_void_p, c_int64, c_int64, c_void_p, c_int64]),
+    "spo_qjl_compression_ratio": (c_double, [c_int64, c_int64]),
     "spo_causal_mask": (None, [c_int64, c_void_p]),
     "spo_prefill_causal_mask": (None, [c_int64, c_int64, c_void_p]),
     "spo_sliding_window_mask": (None, [c_int64, c_int64, c_void_p]),
@@ -311,3 +317,49 @@ def polar_decompress(records: np.ndarray, head_dim: int) -> np.ndarray:
 def polar_compression_ratio(head_dim: int) -> float:
     """KvQuantMethod::PolarQuant.compression_ratio (kv_cache.rs:315-318)."""
     return float(lib().spo_polar_compression_ratio(head_dim))
+
+
+def qjl_lcg_normal(count: int, scale: float) -> np.ndarray:
+    """lcg_normal_f32 (kv_cache.rs:373-396): the reference's seed-42 LCG + Box-Muller, float32."""
+    out = np.zeros(count, dtype=np.float32)
+    lib().spo_qjl_lcg_normal(_p(out), count, scale)
+    return out
+
+
+def qjl_projection(proj_dim: int, head_dim: int) -> np.ndarray:
+    """The QJL projection R [proj_dim, head_dim] of CompressedKvCache::new (kv_cache.rs:417-424)."""
+    out = np.zeros((proj_dim, head_dim), dtype=np.float32)
+    lib().spo_qjl_projection(_p(out), proj_dim, head_dim)
+    return out
+
+
+def qjl_record_bytes(proj_dim: int) -> int:
+    return int(lib().spo_qjl_record_bytes(proj_dim))
+
+
+def qjl_compress(x: np.ndarray, proj: np.ndarray) -> np.ndarray:
+    """qjl_compress (kv_cache.rs:534-569) of the float32 rows of x [..., head_dim]."""
+    a = np.ascontiguousarray(x, dtype=np.float32)
+    r = np.ascontiguousarray(proj, dtype=np.float32)
+    p, d = r.shape
+    n = a.size // d if d else 0
+    out = np.zeros(a.shape[:-1] + (qjl_record_bytes(p),), dtype=np.uint8)
+    lib().spo_qjl_compress(_p(out), _p(a), n, d, _p(r), p)
+    return out
+
+
+def qjl_decompress(records: np.ndarray, proj: np.ndarray) -> np.ndarray:
+    """qjl_decompress (kv_cache.rs:571-617): uint8 records -> float32 rows [..., head_dim]."""
+    r = np.ascontiguousarray(proj, dtype=np.float32)
+    p, d = r.shape
+    b = np.ascontiguousarray(records, dtype=np.uint8)
+    assert b.shape[-1] == qjl_record_bytes(p)
+    n = b.size // b.shape[-1]
+    out = np.zeros(b.shape[:-1] + (d,), dtype=np.float32)
+    lib().spo_qjl_decompress(_p(out), _p(b), n, d, _p(r), p)
+    return out
+
+
+def qjl_compression_ratio(proj_dim: int, head_dim: int) -> float:
+    """KvQuantMethod::QJL.compression_ratio (kv_cache.rs:319-321)."""
+    return float(lib().spo_qjl_compression_ratio(proj_dim, head_dim))

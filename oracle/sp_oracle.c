@@ -598,4 +598,84 @@ double spo_polar_compression_ratio(int64_t head_dim) {
   return (2.0 + (double)head_dim / 2.0) / ((double)head_dim * 2.0);
 }
 
+/* ---- QJL (KvQuantMethod::QJL, kv_cache.rs:300-324, :371-396, :534-617) ---- */
+
+/* lcg_normal_f32 (kv_cache.rs:373-396): the 64-bit LCG state from 42 (Numerical Recipes
+ * constants, wrapping), uniforms (state >> 11) as f32 / 2^53 (u1 floored at 1e-10), Box-Muller
+ * r = sqrt(-2 ln u1) * scale giving r cos(2 pi u2) then r sin(2 pi u2), all in f32. */
+void spo_qjl_lcg_normal(float* out, int64_t count, float scale) {
+  uint64_t state = 42u;
+  int64_t i = 0;
+  while (i < count) {
+    state = state * 1664525u + 1013904223u;
+    float u1 = (float)(state >> 11) / (float)(1ull << 53);
+    if (!(u1 > 1e-10f)) u1 = 1e-10f;
+    state = state * 1664525u + 1013904223u;
+    const float u2 = (float)(state >> 11) / (float)(1ull << 53);
+    const float r = sqrtf(-2.0f * logf(u1)) * scale;
+    const float t = 6.28318548f * u2;
+    out[i++] = r * cosf(t);
+    if (i < count) out[i++] = r * sinf(t);
+  }
+}
+
+/* CompressedKvCache::new (kv_cache.rs:417-424): R [proj_dim, head_dim] ~ N(0, 1/proj_dim). */
+void spo_qjl_projection(float* out, int64_t proj_dim, int64_t head_dim) {
+  spo_qjl_lcg_normal(out, proj_dim * head_dim, sqrtf(1.0f / (float)proj_dim));
+}
+
+int64_t spo_qjl_record_bytes(int64_t proj_dim) { return 2 + (proj_dim + 7) / 8; }
+
+/* qjl_compress (kv_cache.rs:534-569): per vector the f16 magnitude (left fold of x*x, sqrt),
+ * then if it is nonzero bit k of the sign bytes = (R[k,:] . x >= 0), the dot a left fold. */
+void spo_qjl_compress(uint8_t* out, const float* x, int64_t num_vecs, int64_t head_dim,
+                      const float* proj, int64_t proj_dim) {
+  const int64_t rec = spo_qjl_record_bytes(proj_dim);
+  memset(out, 0, (size_t)(num_vecs * rec));
+  for (int64_t i = 0; i < num_vecs; ++i) {
+    const float* v = x + i * head_dim;
+    uint8_t* o = out + i * rec;
+    float ss = 0.0f;
+    for (int64_t j = 0; j < head_dim; ++j) ss = ss + v[j] * v[j];
+    const float mag = sqrtf(ss);
+    const uint16_t bits = spo_f32_to_f16_bits(mag);
+    o[0] = (uint8_t)(bits & 0xff);
+    o[1] = (uint8_t)(bits >> 8);
+    if (mag == 0.0f) continue;
+    for (int64_t k = 0; k < proj_dim; ++k) {
+      const float* r = proj + k * head_dim;
+      float dot = 0.0f;
+      for (int64_t j = 0; j < head_dim; ++j) dot = dot + r[j] * v[j];
+      if (dot >= 0.0f) o[2 + k / 8] |= (uint8_t)(1u << (k % 8));
+    }
+  }
+}
+
+/* qjl_decompress (kv_cache.rs:571-617): out[j] = (sum_k s_k R[k, j]) * (|x| * (pi/2 / proj_dim)),
+ * the sum in k order from 0, s_k = +1 for a set bit, -1 otherwise; zeros for a zero magnitude. */
+void spo_qjl_decompress(float* out, const uint8_t* bytes, int64_t num_vecs, int64_t head_dim,
+                        const float* proj, int64_t proj_dim) {
+  const int64_t rec = spo_qjl_record_bytes(proj_dim);
+  const float scale_factor = 1.57079637f / (float)proj_dim; /* FRAC_PI_2 as f32 */
+  for (int64_t i = 0; i < num_vecs; ++i) {
+    const uint8_t* b = bytes + i * rec;
+    float* o = out + i * head_dim;
+    for (int64_t j = 0; j < head_dim; ++j) o[j] = 0.0f;
+    const float mag = spo_f16_bits_to_f32((uint16_t)(b[0] | (b[1] << 8)));
+    if (mag == 0.0f) continue;
+    const float scale = mag * scale_factor;
+    for (int64_t k = 0; k < proj_dim; ++k) {
+      const float sign = ((b[2 + k / 8] >> (k % 8)) & 1) ? 1.0f : -1.0f;
+      const float* r = proj + k * head_dim;
+      for (int64_t j = 0; j < head_dim; ++j) o[j] = o[j] + sign * r[j];
+    }
+    for (int64_t j = 0; j < head_dim; ++j) o[j] = o[j] * scale;
+  }
+}
+
+/* KvQuantMethod::QJL.compression_ratio (kv_cache.rs:319-321): (2 + P/8) / (2 D). */
+double spo_qjl_compression_ratio(int64_t proj_dim, int64_t head_dim) {
+  return (2.0 + (double)proj_dim / 8.0) / ((double)head_dim * 2.0);
+}
+
 #pragma GCC pop_options

@@ -44,6 +44,9 @@
  *               ties, overflow, subnormal and NaN inputs
  *   spo_polar_compress / spo_polar_decompress             kv_cache.rs:437-532 (PolarQuant)
  *   spo_polar_record_bytes / spo_polar_compression_ratio  kv_cache.rs:441-443, :315-318
+ *   spo_qjl_lcg_normal / spo_qjl_projection               kv_cache.rs:373-396, :417-424 (QJL)
+ *   spo_qjl_compress / spo_qjl_decompress                 kv_cache.rs:534-617
+ *   spo_qjl_record_bytes / spo_qjl_compression_ratio      kv_cache.rs:536-540, :319-321
  *       pinned: hand-derived records (one-hot, negative, zero, odd head_dim, a half-way code that
  *               f32::round takes away from zero), decompress(compress(x)) within the closed-form
  *               bound |x_j - x'_j| <= |x|/14 + (f16 rounding of |x|), codes = sign-correct
@@ -144,6 +147,14 @@ int64_t spo_polar_record_bytes(int64_t head_dim);
 void spo_polar_compress(uint8_t* out, const float* x, int64_t num_vecs, int64_t head_dim);
 void spo_polar_decompress(float* out, const uint8_t* bytes, int64_t num_vecs, int64_t head_dim);
 double spo_polar_compression_ratio(int64_t head_dim);
+void spo_qjl_lcg_normal(float* out, int64_t count, float scale);
+void spo_qjl_projection(float* out, int64_t proj_dim, int64_t head_dim);
+int64_t spo_qjl_record_bytes(int64_t proj_dim);
+void spo_qjl_compress(uint8_t* out, const float* x, int64_t num_vecs, int64_t head_dim,
+                      const float* proj, int64_t proj_dim);
+void spo_qjl_decompress(float* out, const uint8_t* bytes, int64_t num_vecs, int64_t head_dim,
+                        const float* proj, int64_t proj_dim);
+double spo_qjl_compression_ratio(int64_t proj_dim, int64_t head_dim);
 
 #ifdef __cplusplus
 }

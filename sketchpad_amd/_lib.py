@@ -84,6 +84,12 @@ _SIGNATURES = {
     "sp_flash_attention": (c_int32, [c_void_p, c_void_p, c_void_p, c_void_p, c_int32, c_int32,
                                      c_int32, c_int32, c_int32, c_float, c_int32, c_int32,
                                      c_void_p]),
+    "sp_qjl_record_bytes": (c_int64, [c_int32]),
+    "sp_qjl_projection": (c_int32, [c_void_p, c_int32, c_int32]),
+    "sp_qjl_compress": (c_int32, [c_void_p, c_void_p, c_int64, c_int32, c_void_p, c_int32,
+                                  c_int32, c_void_p]),
+    "sp_qjl_decompress": (c_int32, [c_void_p, c_void_p, c_int64, c_int32, c_void_p, c_int32,
+                                    c_int32, c_void_p]),
     "sp_flash_attention_masked": (c_int32, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                                             c_int64, c_int64, c_int64, c_int32, c_int32, c_int32,
                                             c_int32, c_int32, c_float, c_int32, c_int32,
@@ -425,3 +431,33 @@ def linear_weight_nk(w_kn, *, stream=None):
     check(load().sp_linear_weight_nk(_ptr(dst), _ptr(w_kn), k, n, sp_dtype(w_kn),
                                      _stream(stream)))
     return dst
+
+
+# ---------------------------------------------------------------------------------------------
+# QJL codec (KvQuantMethod::QJL, kv_cache.rs:300-324, :534-617)
+# ---------------------------------------------------------------------------------------------
+def qjl_record_bytes(proj_dim: int) -> int:
+    return int(load().sp_qjl_record_bytes(proj_dim))
+
+
+def qjl_projection(proj_dim: int, head_dim: int, device="cuda"):
+    """The reference's fixed QJL projection R [proj_dim, head_dim] (sp_qjl_projection on the
+    host), as a float32 tensor on `device`."""
+    torch = _torch()
+    host = torch.empty(proj_dim, head_dim, dtype=torch.float32)
+    check(load().sp_qjl_projection(ctypes.c_void_p(host.data_ptr()), proj_dim, head_dim))
+    return host.to(device)
+
+
+def qjl_compress(records, x, proj, stream=None) -> None:
+    """sp_qjl_compress: x [..., head_dim] -> uint8 records [..., qjl_record_bytes(P)]."""
+    d = x.shape[-1]
+    check(load().sp_qjl_compress(_ptr(records), _ptr(x), x.numel() // d, d, _ptr(proj),
+                                 proj.shape[0], sp_dtype(x), _stream(stream)))
+
+
+def qjl_decompress(out, records, proj, stream=None) -> None:
+    """sp_qjl_decompress: uint8 records -> out [..., head_dim] (out's dtype)."""
+    d = out.shape[-1]
+    check(load().sp_qjl_decompress(_ptr(out), _ptr(records), out.numel() // d, d, _ptr(proj),
+                                   proj.shape[0], sp_dtype(out), _stream(stream)))

@@ -42,7 +42,7 @@ DEVICE_FLAGS = [
 ]
 
 LIB_SOURCES = ["kv_cache.hip", "paged_decode.hip", "prefill.hip", "prefill_f32.hip", "rope_append.hip",
-               "polar_cache.hip", "linear.hip", "capi.cpp"]
+               "polar_cache.hip", "qjl.hip", "linear.hip", "capi.cpp"]
 HOST_SOURCES = ["paged_attention.cpp", "continuous_batching.cpp", "ragged_batch.cpp"]
 
 

@@ -14,6 +14,7 @@
 #include "paged_decode.hpp"
 #include "polar_cache.hpp"
 #include "prefill.hpp"
+#include "qjl.hpp"
 #include "rope_append.hpp"
 #include "sp_common.hpp"
 
@@ -720,6 +721,58 @@ int sp_linear_weight_nk(void* dst, const void* src, int64_t K, int64_t N, sp_dty
   if (((uintptr_t)dst | (uintptr_t)src) % dtype_size(dtype))
     return fail(SP_EINVAL, "%s: pointers are not aligned to the element type", fn);
   return launch_weight_transpose(dst, src, K, N, dtype, (hipStream_t)stream);
+}
+
+
+// ---------------------------------------------------------------------------------------------
+// QJL codec (KvQuantMethod::QJL, kv_cache.rs:300-324, :371-396, :534-617)
+// ---------------------------------------------------------------------------------------------
+int64_t sp_qjl_record_bytes(int32_t proj_dim) {
+  return proj_dim > 0 ? 2 + ((int64_t)proj_dim + 7) / 8 : 0;
+}
+
+int sp_qjl_projection(float* out, int32_t proj_dim, int32_t head_dim) {
+  const char* fn = "sp_qjl_projection";
+  if (proj_dim <= 0 || head_dim <= 0)
+    return fail(SP_EINVAL, "%s: proj_dim %d, head_dim %d", fn, proj_dim, head_dim);
+  if (!out) return fail(SP_EINVAL, "%s: NULL output", fn);
+  const float scale = sqrtf(1.0f / (float)proj_dim);  // R ~ N(0, 1 / proj_dim)
+  qjl_projection_host(out, proj_dim, head_dim, scale);
+  return SP_OK;
+}
+
+static int check_qjl(const char* fn, int64_t num_vecs, int32_t head_dim, const float* proj,
+                     int32_t proj_dim, sp_dtype dtype) {
+  if (int rc = check_dtype(dtype, fn)) return rc;
+  if (num_vecs < 0 || head_dim <= 0 || proj_dim <= 0)
+    return fail(SP_EINVAL, "%s: num_vecs %lld, head_dim %d, proj_dim %d", fn,
+                (long long)num_vecs, head_dim, proj_dim);
+  if (num_vecs > 0 && !proj) return fail(SP_EINVAL, "%s: NULL projection", fn);
+  return SP_OK;
+}
+
+int sp_qjl_compress(void* records, const void* x, int64_t num_vecs, int32_t head_dim,
+                    const float* projection, int32_t proj_dim, sp_dtype dtype, void* stream) {
+  const char* fn = "sp_qjl_compress";
+  if (int rc = check_qjl(fn, num_vecs, head_dim, projection, proj_dim, dtype)) return rc;
+  if (num_vecs == 0) return SP_OK;
+  if (!records || !x) return fail(SP_EINVAL, "%s: NULL pointer argument", fn);
+  if ((uintptr_t)x % dtype_size(dtype) || (uintptr_t)projection % 4)
+    return fail(SP_EINVAL, "%s: x or projection is not aligned to its element type", fn);
+  return launch_qjl_compress(records, x, num_vecs, head_dim, projection, proj_dim, dtype,
+                             (hipStream_t)stream);
+}
+
+int sp_qjl_decompress(void* out, const void* records, int64_t num_vecs, int32_t head_dim,
+                      const float* projection, int32_t proj_dim, sp_dtype dtype, void* stream) {
+  const char* fn = "sp_qjl_decompress";
+  if (int rc = check_qjl(fn, num_vecs, head_dim, projection, proj_dim, dtype)) return rc;
+  if (num_vecs == 0) return SP_OK;
+  if (!records || !out) return fail(SP_EINVAL, "%s: NULL pointer argument", fn);
+  if ((uintptr_t)out % dtype_size(dtype) || (uintptr_t)projection % 4)
+    return fail(SP_EINVAL, "%s: out or projection is not aligned to its element type", fn);
+  return launch_qjl_decompress(out, records, num_vecs, head_dim, projection, proj_dim, dtype,
+                               (hipStream_t)stream);
 }
 
 }  // extern "C"
