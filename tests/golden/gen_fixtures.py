@@ -161,6 +161,48 @@ def polar_case(rng):
     return dict(x=x, records=rec, decompressed=O.polar_decompress(rec, d))
 
 
+def qjl_case(rng):
+    """QJL at the reference test's shape (head_dim 32, proj_dim 8) and at 64 / 16: the fixed
+    projection, the records and the decompressed rows (random, zero and one-hot vectors)."""
+    out = {}
+    for d, p in ((32, 8), (64, 16)):
+        rows = [rng.standard_normal(d, dtype=np.float32) * s for s in (1.0, 1e-2, 50.0)]
+        one_hot = np.zeros(d, np.float32)
+        one_hot[3] = 1.0
+        x = np.stack(rows + [np.zeros(d, np.float32), one_hot])
+        proj = O.qjl_projection(p, d)
+        rec = O.qjl_compress(x, proj)
+        out.update({f"x{d}": x, f"proj{d}": proj, f"records{d}": rec,
+                    f"decompressed{d}": O.qjl_decompress(rec, proj)})
+    return out
+
+
+def flash_f32_case(rng):
+    """Dense f32 flash attention [1, 2, 40, 64] (the reference flash_attention's element type):
+    non-causal, top-left causal, and with an additive [40, 40] mask; outputs from the f64 oracle,
+    each checked against torch float64 SDPA."""
+    h, s, d = 2, 40, 64
+    q, k, v = (rng.standard_normal((s, h, d), dtype=np.float32) for _ in range(3))
+    mask = (2.0 * rng.standard_normal((s, s))).astype(np.float32)
+    mask[:, 33:] = -np.inf
+    scale = d ** -0.5
+    res = {}
+    for name, causal, m in (("out_full", False, None), ("out_causal", True, None),
+                            ("out_masked", False, mask)):
+        o = O.attention_f64(q, k, v, scale=scale, causal=causal, q_pos0=0, mask=m, dtype=O.F32)
+        if m is None:
+            ref = torch_attention_f64(q, k, v, scale, q_pos0=0, causal=causal)
+            assert np.abs(ref - o).max() < 1e-12
+        else:
+            import torch
+            qt, kt, vt = (torch.from_numpy(a).double().transpose(0, 1) for a in (q, k, v))
+            sc = qt @ kt.transpose(1, 2) * scale + torch.from_numpy(m).double()
+            ref = (torch.softmax(sc, -1) @ vt).transpose(0, 1).numpy()
+            assert np.abs(ref - o).max() < 1e-12
+        res[name] = o
+    return dict(q=q, k=k, v=v, mask=mask, scale=np.float64(scale), **res)
+
+
 def kats() -> dict:
     """The reference's unit-test known answers, as data."""
     return {
@@ -218,11 +260,18 @@ FIXTURES = {
                                                                 True, window_left=16),
     "rope_f32.npz": rope_case,
     "polar_f32.npz": polar_case,
+    "qjl_f32.npz": qjl_case,
+    "flash_f32.npz": flash_f32_case,
 }
 
 
+# seed offsets: a fixture's position here (new fixtures go at the end, so existing ones keep theirs)
+SEED_ORDER = ["decode_bf16_window.npz", "decode_f32.npz", "polar_f32.npz", "prefill_bf16.npz",
+              "prefill_bf16_chunked_window.npz", "rope_f32.npz", "qjl_f32.npz", "flash_f32.npz"]
+
+
 def build(name: str) -> dict:
-    rng = np.random.default_rng(SEED + sorted(FIXTURES).index(name))
+    rng = np.random.default_rng(SEED + SEED_ORDER.index(name))
     return FIXTURES[name](rng)
 
 

@@ -120,6 +120,41 @@ def _f(x):
     return -np.inf if x == "-inf" else float(x)
 
 
+def test_qjl_fixture_independent():
+    """QJL records: magnitude bytes are binary16 of the float64 norm (within its rounding), the
+    one-hot row's sign bits are the signs of its projection column, the zero row is all zeros,
+    and the frozen projection has the N(0, 1/P) scale."""
+    f = _load("qjl_f32.npz")
+    for d, p in ((32, 8), (64, 16)):
+        x, proj, rec = f[f"x{d}"], f[f"proj{d}"], f[f"records{d}"]
+        assert rec.shape == (len(x), 2 + (p + 7) // 8)
+        assert abs(proj.std() - p ** -0.5) < 0.25 * p ** -0.5
+        for i, row in enumerate(x):
+            m = O.f16_bits_to_f32(int(rec[i, 0]) | (int(rec[i, 1]) << 8))
+            n = np.linalg.norm(row.astype(np.float64))
+            assert abs(m - n) <= max(n * 2 ** -10, 6e-8)
+        assert not rec[3].any()
+        bits = np.array([(rec[4, 2 + k // 8] >> (k % 8)) & 1 for k in range(p)])
+        assert np.array_equal(bits, (proj[:, 3] >= 0).astype(int))
+
+
+def test_flash_f32_fixture_independent():
+    """The frozen f32 flash outputs against a float64 softmax computed here with numpy."""
+    f = _load("flash_f32.npz")
+    q, k, v, mask = (f[n].astype(np.float64) for n in ("q", "k", "v", "mask"))
+    s_, h, d = q.shape
+    for name, causal, m in (("out_full", False, None), ("out_causal", True, None),
+                            ("out_masked", False, mask)):
+        sc = np.einsum("ihd,jhd->hij", q, k) * d ** -0.5
+        if causal:
+            sc = sc + np.where(np.arange(s_)[None, :] > np.arange(s_)[:, None], -np.inf, 0.0)
+        if m is not None:
+            sc = sc + m
+        w = np.exp(sc - sc.max(-1, keepdims=True))
+        ref = np.einsum("hij,jhd->ihd", w / w.sum(-1, keepdims=True), v)
+        assert np.abs(ref - f[name]).max() < 1e-12
+
+
 def test_kat_block_table():
     k = KATS["block_table"]
     for pos, blk in k["get_block"].items():

@@ -103,3 +103,40 @@ def test_golden_polar_records():
     torch.cuda.synchronize()
     assert np.array_equal(rec.cpu().numpy(), f["records"])
     assert np.array_equal(out.cpu().numpy().view(np.uint32), f["decompressed"].view(np.uint32))
+
+
+def test_golden_qjl_records():
+    f = _load("qjl_f32.npz")
+    for d, p in ((32, 8), (64, 16)):
+        announce(f"golden qjl d={d} p={p}")
+        proj = sp.qjl_projection(p, d)
+        assert np.array_equal(proj.cpu().numpy().view(np.uint32), f[f"proj{d}"].view(np.uint32))
+        x = _dev(f[f"x{d}"])
+        rec = torch.zeros(f[f"records{d}"].shape, dtype=torch.uint8, device="cuda")
+        sp.qjl_compress(rec, x, proj)
+        out = torch.full_like(x, float("nan"))
+        sp.qjl_decompress(out, rec, proj)
+        torch.cuda.synchronize()
+        assert np.array_equal(rec.cpu().numpy(), f[f"records{d}"])
+        assert np.array_equal(out.cpu().numpy().view(np.uint32),
+                              f[f"decompressed{d}"].view(np.uint32))
+
+
+def test_golden_flash_f32():
+    """f32 flash attention (plain, causal, additive mask) within 1e-5 per row of the frozen
+    float64 outputs."""
+    f = _load("flash_f32.npz")
+    q, k, v = (torch.from_numpy(f[n]).transpose(0, 1).contiguous()[None].cuda()
+               for n in ("q", "k", "v"))
+    d = q.shape[-1]
+    for name, causal, mask in (("out_full", False, None), ("out_causal", True, None),
+                               ("out_masked", False, f["mask"])):
+        announce(f"golden flash f32 {name}")
+        out = torch.full_like(q, float("nan"))
+        if mask is None:
+            sp.flash_attention(out, q, k, v, d ** -0.5, causal=causal)
+        else:
+            sp.flash_attention_masked(out, q, k, v, torch.from_numpy(mask).cuda(), d ** -0.5)
+        torch.cuda.synchronize()
+        got = out[0].transpose(0, 1).double().cpu().numpy()
+        assert_attention_close(got, f[name], "f32", name)
