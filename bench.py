@@ -4,7 +4,7 @@
                     [--no-prefill] [--secondary]
     python bench.py --calibrate-copy    # plain 512 MiB device copies (HBM counter calibration)
 
-A step is one decode step of the BASELINE headline workload (C2, Llama-3-8B shape): append the
+A step is one decode step of the headline workload (C2, Llama-3-8B shape): append the
 step's new K/V row of each of the 64 sequences into the paged pool (sp_kv_append), then paged
 decode attention over every sequence's context (sp_paged_decode). Inputs are resident in HBM
 before the timed region starts. Prints one JSON line:

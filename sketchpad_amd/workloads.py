@@ -1,4 +1,4 @@
-"""Seeded synthetic workloads for the five BASELINE configurations.
+"""Seeded synthetic workloads for the five benchmark configurations (C1-C5).
 
 Metadata (context lengths, block tables, sequence offsets) comes from numpy's PCG64 with seed
 0x5EED0000 + config index, so it is identical on every machine. Tensor contents are N(0, 1)

@@ -5,7 +5,7 @@ import sys
 
 import numpy as np
 
-# Output tolerances: f32 within 1e-5 relative, measured per output row
+# Output tolerances of the path: f32 within 1e-5 relative, measured per output row
 # (one sequence x head vector) against the row's largest magnitude; 16-bit types within 2e-2
 # absolute (fp32 softmax / accumulation, one final rounding to the storage type).
 F32_REL_TOL = 1e-5

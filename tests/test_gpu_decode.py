@@ -130,5 +130,5 @@ def test_decode_many_splits_and_repeat_calls():
 
 @pytest.mark.parametrize("name", ["C2", "C4", "C5"])
 def test_decode_full_size_configs(name):
-    """The BASELINE decode configs at full size against the f64 oracle."""
+    """The decode benchmark configs (C1, C2, C4, C5) at full size against the f64 oracle."""
     check(W.DECODE_CONFIGS[name]())
