@@ -43,7 +43,7 @@ DEVICE_FLAGS = [
 
 LIB_SOURCES = ["kv_cache.hip", "paged_decode.hip", "prefill.hip", "prefill_f32.hip", "rope_append.hip",
                "polar_cache.hip", "qjl.hip", "linear.hip", "capi.cpp"]
-HOST_SOURCES = ["paged_attention.cpp", "continuous_batching.cpp", "ragged_batch.cpp"]
+HOST_SOURCES = ["paged_attention.cpp", "ragged_batch.cpp"]
 
 
 def _run(cmd: list[str]) -> None:

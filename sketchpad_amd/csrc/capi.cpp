@@ -365,8 +365,6 @@ static int prefill_splits(int32_t num_seqs, int32_t max_seqlen_q, int32_t num_q_
   const int64_t base = (int64_t)((max_seqlen_q + kPrefillBM - 1) / kPrefillBM) * num_seqs *
                        num_q_heads;
   int s = plan_prefill_splits(base, (max_context + kPrefillBN - 1) / kPrefillBN);
-  const char* env = getenv("SP_PREFILL_SPLITS");  // tuning override, clamped to 1..8
-  if (env && atoi(env) > 0) s = atoi(env) > 8 ? 8 : atoi(env);
   while (s > 1 &&
          prefill_partials_bytes(num_seqs, max_seqlen_q, num_q_heads, head_dim, s) > workspace_bytes)
     --s;

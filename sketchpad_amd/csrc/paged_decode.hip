@@ -430,10 +430,7 @@ DecodePlan plan_decode(int num_seqs, int hq, int hkv, int head_dim, int max_cont
   }
   p.max_tiles = max_tiles < 1 ? 1 : max_tiles;
   int tps = max_tps < kDecodeWaves ? kDecodeWaves : (max_tps > cap ? cap : max_tps);
-  const char* env = getenv("SP_DECODE_TPS");
-  if (env && atoi(env) > 0) {
-    tps = atoi(env) < kDecodeWaves ? kDecodeWaves : (atoi(env) > cap ? cap : atoi(env));
-  } else {
+  {
     // Halve the split while the batch launches fewer than 2048 workgroups, but not below
     // 32 tiles (512 tokens) once there are 512 (two per CU): shorter splits then only add
     // per-workgroup start-up and partials to merge (measured on the windowed C5 batch: 128

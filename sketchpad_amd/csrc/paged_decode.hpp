@@ -19,8 +19,7 @@ struct DecodePlan {
 
 // max_tps: the largest split (in 16-token tiles) the kernel should take; a split is halved
 // while the batch would launch fewer than 2048 workgroups, down to 32 tiles once it launches at
-// least 512. cap: the most tiles per split the kernel can hold (an SP_DECODE_TPS override is
-// clamped to it).
+// least 512. cap: the most tiles per split the kernel can hold.
 DecodePlan plan_decode(int num_seqs, int hq, int hkv, int head_dim, int max_context_len,
                        int window_left, int max_tps = 32, int cap = 64);
 

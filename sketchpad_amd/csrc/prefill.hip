@@ -528,10 +528,13 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PrefillArgs a) {
   if (my_q >= qe) return;
   if (a.nsplit > 1) {
     // partial record (m, l, -, -, acc[D]) of this split; m is the offset the weights are
-    // relative to (0 when the split saw no key, with l = 0 and acc = 0)
+    // relative to, -inf when the split saw no visible key (then l = 0 and acc = 0), so that the
+    // merge never takes an empty split's offset as the row maximum. Rows past max_q (a caller
+    // whose cu_seqlens exceed max_seqlen_q) have no record slot and are not written.
+    if (my_q >= a.max_q) return;
     float* rec = a.partials +
         ((((int64_t)seq * a.max_q + my_q) * a.hq + h) * a.nsplit + split) * (D + 4);
-    if (hh == 0) *(float2*)rec = make_float2(m_used, l);
+    if (hh == 0) *(float2*)rec = make_float2(m_run == -INFINITY ? -INFINITY : m_used, l);
 #pragma unroll
     for (int db = 0; db < DB; ++db)
 #pragma unroll
@@ -570,7 +573,7 @@ __global__ void __launch_bounds__(256) prefill_combine_kernel(PrefillArgs a) {
   const int id = blockIdx.x / a.hq;
   const int seq = id % a.num_seqs, grp = id / a.num_seqs;
   const int q_begin = a.cu_q[seq];
-  const int Lq = a.cu_q[seq + 1] - q_begin;
+  const int Lq = min(a.cu_q[seq + 1] - q_begin, a.max_q);  // rows with a record slot
   const int qs = grp * kCombineRows;
   if (qs >= Lq) return;
   const int qe = min(qs + kCombineRows, Lq);
@@ -578,11 +581,13 @@ __global__ void __launch_bounds__(256) prefill_combine_kernel(PrefillArgs a) {
   for (int q = qs + (int)threadIdx.x / TPR; q < qe; q += RPP) {
     const float* rec =
         a.partials + ((((int64_t)seq * a.max_q + q) * a.hq + h) * a.nsplit) * (D + 4);
+    // M: the largest offset of the splits that saw a key (an empty split records -inf)
     float m = -INFINITY;
     for (int sp = 0; sp < a.nsplit; ++sp) m = fmaxf(m, rec[sp * (D + 4)]);
     float l = 0.f, o0 = 0.f, o1 = 0.f, o2 = 0.f, o3 = 0.f;
-    for (int sp = 0; sp < a.nsplit; ++sp) {
+    for (int sp = 0; sp < a.nsplit && m != -INFINITY; ++sp) {
       const float* r = rec + sp * (D + 4);
+      if (r[0] == -INFINITY) continue;  // no key in this split: weight 0, and no -inf - -inf
       const float w = __builtin_amdgcn_exp2f(r[0] - m);
       const float4 v = *(const float4*)(r + 4 + 4 * c);
       l += w * r[1];

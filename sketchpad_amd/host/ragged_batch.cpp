@@ -22,17 +22,36 @@ Result<RaggedBatch> build_ragged_batch(PagedScheduler& sched,
                                        const std::vector<BatchEntry>& entries) {
   RaggedBatch b;
   const size_t bs = sched.cache.block_size();
+  {
+    std::vector<size_t> ids;
+    for (const BatchEntry& e : entries) {
+      if (e.num_new == 0) return Result<RaggedBatch>::Err("Empty batch entry");
+      ids.push_back(e.seq_id);
+    }
+    std::sort(ids.begin(), ids.end());
+    if (std::adjacent_find(ids.begin(), ids.end()) != ids.end())
+      return Result<RaggedBatch>::Err("Duplicate sequence ID");
+  }
   // grow every table first (allocate_for_tokens, paged_attention.rs:398-415)
   for (const BatchEntry& e : entries) {
     Result<Unit> r = sched.allocate(e.seq_id, e.num_new);
     if (r.is_err()) return Result<RaggedBatch>::Err(r.error());
   }
+  // batch order: chunks first, then one-token entries (stable within each group)
+  std::vector<const BatchEntry*> order;
+  for (const BatchEntry& e : entries)
+    if (e.num_new > 1) order.push_back(&e);
+  const size_t num_chunks = order.size();
+  for (const BatchEntry& e : entries)
+    if (e.num_new == 1) order.push_back(&e);
   size_t max_blocks = 1;
   for (const BatchEntry& e : entries)
     max_blocks = std::max(max_blocks, sched.get_sequence(e.seq_id)->block_table.num_blocks());
   b.max_blocks = (int32_t)max_blocks;
+  b.num_prefill_seqs = (int32_t)num_chunks;
   b.cu_seqlens_q.push_back(0);
-  for (const BatchEntry& e : entries) {
+  for (size_t s = 0; s < order.size(); ++s) {
+    const BatchEntry& e = *order[s];
     const BlockTable& table = sched.get_sequence(e.seq_id)->block_table;
     const size_t start = table.seq_len();
     for (size_t i = 0; i < e.num_new; ++i) {
@@ -44,10 +63,16 @@ Result<RaggedBatch> build_ragged_batch(PagedScheduler& sched,
     }
     b.seq_ids.push_back(e.seq_id);
     b.cu_seqlens_q.push_back((int32_t)b.positions.size());
-    const size_t ctx = start + e.num_new;
-    b.context_lens.push_back((int32_t)ctx);
+    const int32_t ctx = (int32_t)(start + e.num_new);
+    b.context_lens.push_back(ctx);
     b.max_seqlen_q = std::max(b.max_seqlen_q, (int32_t)e.num_new);
-    b.max_context_len = std::max(b.max_context_len, (int32_t)ctx);
+    b.max_context_len = std::max(b.max_context_len, ctx);
+    if (s < num_chunks) {
+      b.num_prefill_tokens = (int32_t)b.positions.size();
+      b.prefill_max_seqlen_q = std::max(b.prefill_max_seqlen_q, (int32_t)e.num_new);
+    } else {
+      b.decode_max_context_len = std::max(b.decode_max_context_len, ctx);
+    }
     std::vector<int32_t> row(max_blocks, 0);
     for (size_t j = 0; j < table.num_blocks(); ++j) row[j] = (int32_t)table.blocks()[j];
     b.block_tables.insert(b.block_tables.end(), row.begin(), row.end());
@@ -123,27 +148,34 @@ void BatchedPagedAttention::forward(size_t layer_idx, const DeviceRaggedBatch& b
                           batch.slot_mapping(), T, cache_.dtype(), stream),
              "sp_kv_append");
   }
-  // 2. attention: decode when every sequence adds one token, chunked prefill otherwise
-  if (hb.decode_only()) {
-    const size_t need = sp_paged_decode_workspace_size((int32_t)hb.num_seqs(), hq,
-                                                       hb.max_context_len, -1, &lay);
-    if (need > workspace_.nbytes())
-      workspace_ = DeviceTensor({(int64_t)((need + 3) / 4)}, SP_F32);  // zero-filled
-    check_sp(sp_paged_decode(out.data(), q.data(), kp, vp, &lay, batch.block_tables(),
-                             hb.max_blocks, batch.context_lens(), hb.max_context_len,
-                             (int32_t)hb.num_seqs(), hq, scale, -1, cache_.dtype(),
-                             workspace_.data(), workspace_.nbytes(), stream),
-             "sp_paged_decode");
-  } else {
-    const size_t need = sp_paged_prefill_workspace_size((int32_t)hb.num_seqs(), hb.max_seqlen_q,
-                                                        hq, &lay, hb.max_blocks);
-    if (need > workspace_.nbytes())
-      workspace_ = DeviceTensor({(int64_t)((need + 3) / 4)}, SP_F32);
+  // 2. attention: chunked prefill over the chunks [0, P), decode over the one-token entries
+  //    [P, B), enqueued in that order on one stream (they share the workspace: stream order
+  //    keeps the prefill's partials merged before the decode writes its own)
+  const int32_t P = hb.num_prefill_seqs, B = (int32_t)hb.num_seqs(), nd = B - P;
+  size_t need = 0;
+  if (P > 0)
+    need = std::max(need, sp_paged_prefill_workspace_size(P, hb.prefill_max_seqlen_q, hq, &lay,
+                                                          hb.max_blocks));
+  if (nd > 0)
+    need = std::max(need, sp_paged_decode_workspace_size(nd, hq, hb.decode_max_context_len, -1,
+                                                         &lay));
+  if (need > workspace_.nbytes())
+    workspace_ = DeviceTensor({(int64_t)((need + 3) / 4)}, SP_F32);  // zero-filled
+  void* ws = workspace_.nbytes() ? workspace_.data() : nullptr;
+  if (P > 0)
     check_sp(sp_paged_prefill(out.data(), q.data(), kp, vp, &lay, batch.block_tables(),
-                              hb.max_blocks, batch.cu_seqlens_q(), batch.context_lens(),
-                              (int32_t)hb.num_seqs(), hb.max_seqlen_q, hq, scale, -1,
-                              cache_.dtype(), workspace_.data(), workspace_.nbytes(), stream),
+                              hb.max_blocks, batch.cu_seqlens_q(), batch.context_lens(), P,
+                              hb.prefill_max_seqlen_q, hq, scale, -1, cache_.dtype(), ws,
+                              workspace_.nbytes(), stream),
              "sp_paged_prefill");
+  if (nd > 0) {
+    const int64_t row = (int64_t)hq * d * (int64_t)dtype_bytes(cache_.dtype());
+    const int64_t tok0 = hb.num_prefill_tokens;
+    check_sp(sp_paged_decode((char*)out.data() + tok0 * row, (const char*)q.data() + tok0 * row,
+                             kp, vp, &lay, batch.block_tables() + (int64_t)P * hb.max_blocks,
+                             hb.max_blocks, batch.context_lens() + P, hb.decode_max_context_len,
+                             nd, hq, scale, -1, cache_.dtype(), ws, workspace_.nbytes(), stream),
+             "sp_paged_decode");
   }
 }
 

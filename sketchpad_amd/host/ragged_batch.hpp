@@ -12,9 +12,13 @@
 //   - slot_mapping[t] = table[pos / BS] * BS + pos % BS (BlockTable::get_block / get_slot,
 //     paged_attention.rs:124-132), positions[t] = pos, cu_seqlens_q, context_lens (old + new
 //     tokens: what each query attends), and the padded block tables;
-//   - one layer appends K/V (rotating K and Q when RoPE tables are given) and runs decode when
-//     every sequence adds one token, chunked prefill otherwise. Both reduce to the reference's
-//     per-sequence forward_cached (transformer.rs:184-254): no mask for one new token, and
+//   - the batch is ordered chunks first (entries adding two or more tokens), then the entries
+//     adding one token, each group in the caller's order, so that both groups are contiguous in
+//     the packed token stream and in the per-sequence arrays;
+//   - one layer appends K/V for every token (rotating K and Q when RoPE tables are given), then
+//     runs chunked prefill over the chunk group and decode over the one-token group: two
+//     launches on one stream. Both reduce to the reference's per-sequence forward_cached
+//     (transformer.rs:184-254): no mask for one new token (llama.rs:255-260), and
 //     prefill_causal_mask (llama.rs:374-388) for a chunk.
 #pragma once
 
@@ -33,9 +37,11 @@ struct BatchEntry {
   size_t num_new;
 };
 
-// Host form of a ragged batch's metadata (int32, as the C ABI takes it).
+// Host form of a ragged batch's metadata (int32, as the C ABI takes it). Sequences
+// [0, num_prefill_seqs) are the chunks (two or more new tokens each) and own tokens
+// [0, num_prefill_tokens); the rest add one token each.
 struct RaggedBatch {
-  std::vector<size_t> seq_ids;        // batch order
+  std::vector<size_t> seq_ids;        // batch order: chunks, then one-token entries
   std::vector<int32_t> cu_seqlens_q;  // [B + 1] token offsets of each sequence's new tokens
   std::vector<int32_t> positions;     // [T] position of each new token in its sequence
   std::vector<int32_t> slot_mapping;  // [T] pool slot of that position
@@ -44,15 +50,23 @@ struct RaggedBatch {
   int32_t max_blocks = 0;
   int32_t max_seqlen_q = 0;
   int32_t max_context_len = 0;
+  int32_t num_prefill_seqs = 0;
+  int32_t num_prefill_tokens = 0;
+  int32_t prefill_max_seqlen_q = 0;     // over the chunks
+  int32_t decode_max_context_len = 0;   // over the one-token entries
 
   size_t num_seqs() const { return seq_ids.size(); }
   size_t num_tokens() const { return positions.size(); }
-  bool decode_only() const { return max_seqlen_q <= 1; }
+  size_t num_decode_seqs() const { return num_seqs() - (size_t)num_prefill_seqs; }
+  // every sequence adds exactly one token
+  bool decode_only() const { return num_prefill_seqs == 0 && num_tokens() == num_seqs(); }
 };
 
 // Grows each entry's block table for its new tokens and reads the metadata off the tables.
 // Errors as the reference: "Invalid sequence ID", "Out of memory: no free blocks" (blocks taken
-// before the failure stay taken, as in allocate_for_tokens).
+// before the failure stay taken, as in allocate_for_tokens). An entry with no new tokens, or a
+// sequence listed twice, is rejected before anything is allocated ("Empty batch entry",
+// "Duplicate sequence ID").
 Result<RaggedBatch> build_ragged_batch(PagedScheduler& sched,
                                        const std::vector<BatchEntry>& entries);
 
@@ -101,5 +115,25 @@ class BatchedPagedAttention {
   PagedKvCache& cache_;
   DeviceTensor workspace_;
 };
+
+// One iteration through every layer: the batched form of the layer loop of Llama::forward
+// with a cache (llama.rs:247-271), where start_pos = cache.seq_len() is read once and every layer
+// attends with it. Builds the ragged batch once (growing the block tables), uploads it on
+// `stream`, calls layer_fn(layer, device_batch) for layer = 0 .. num_layers - 1 (the caller
+// computes that layer's q / k / v and runs BatchedPagedAttention::forward on it), and only then
+// advances every sequence by its new tokens. So all layers append at the same positions and
+// attend the same context lengths (layer-0 semantics for every layer; the reference's
+// PagedAttentionCache advances the length inside layer 0, paged_attention.rs:525-533). Returns
+// the host batch, or the builder's error with nothing advanced.
+template <typename LayerFn>
+Result<RaggedBatch> run_batched_step(PagedScheduler& sched, const std::vector<BatchEntry>& entries,
+                                     size_t num_layers, hipStream_t stream, LayerFn&& layer_fn) {
+  Result<RaggedBatch> r = build_ragged_batch(sched, entries);
+  if (r.is_err()) return r;
+  const DeviceRaggedBatch db(r.unwrap(), stream);
+  for (size_t layer = 0; layer < num_layers; ++layer) layer_fn(layer, db);
+  commit_ragged_batch(sched, r.unwrap());
+  return r;
+}
 
 }  // namespace sketchpad

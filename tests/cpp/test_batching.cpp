@@ -1,193 +1,56 @@
-// Tests of the iteration-level scheduler mirror (sketchpad_amd/host/continuous_batching.hpp) and
-// of ragged batches over the paged cache (sketchpad_amd/host/ragged_batch.hpp). The first group
-// restates the reference's own scheduler tests (crates/sketchpad-core/src/continuous_batching.rs:
-// 419-566) plus its tie-breaking; the second checks batch metadata against the block tables'
-// closed form, and runs a continuous-batching loop on the GPU (sequences join as others finish,
-// prompts are prefilled in chunks next to decoding sequences) whose every attention output is
-// compared with a float64 host computation over the sequence's own history.
+// Tests of ragged batches over the paged cache (sketchpad_amd/host/ragged_batch.hpp): batch
+// metadata against the block tables' closed form (BlockTable::get_block / get_slot,
+// paged_attention.rs:124-132), the builder's input checks, and on the GPU
+//   - a serving loop driven by a small schedule local to this file (sequences join as others
+//     finish, prompts are prefilled in chunks next to decoding sequences, so most steps are
+//     mixed batches that run chunked prefill and decode side by side), and
+//   - a multi-layer step through one interleaved-layer pool (run_batched_step: every layer
+//     appends at the same positions, the lengths advance once per step),
+// whose every attention output is compared with a float64 host computation over the sequence's
+// own history.
 #include <math.h>
 #include <string.h>
 
+#include <algorithm>
+#include <deque>
 #include <map>
 #include <random>
 
-#include "continuous_batching.hpp"
 #include "ragged_batch.hpp"
 #include "test_harness.hpp"
 
 using namespace sketchpad;
-
-// ---- continuous_batching.rs:419-566 -----------------------------------------------------------
-
-TEST(test_sequence_lifecycle, false) {
-  Sequence seq(0, {1, 2, 3}, 5, 0);
-  CHECK(seq.total_len() == 3);
-  CHECK(!seq.is_finished());
-  CHECK(seq.status == SequenceStatus::Waiting);
-  seq.add_token(4);
-  seq.add_token(5);
-  CHECK(seq.total_len() == 5);
-  CHECK(seq.generated_len == 2);
-  seq.add_token(6);
-  seq.add_token(7);
-  seq.add_token(8);
-  CHECK(seq.is_finished());
-}
-
-TEST(test_scheduler_add_and_schedule, false) {
-  ContinuousBatchingConfig config;
-  config.max_batch_size = 2;
-  config.total_blocks = 100;
-  config.block_size = 4;
-  ContinuousBatchingScheduler scheduler(config);
-  const size_t id0 = scheduler.add_sequence({1, 2, 3}, 10);
-  scheduler.add_sequence({4, 5}, 10);
-  scheduler.add_sequence({6, 7, 8, 9}, 10);
-  CHECK(scheduler.num_sequences() == 3);
-  CHECK(scheduler.num_waiting() == 3);
-  ScheduleOutput out = scheduler.schedule();
-  CHECK(out.running.size() == 2);
-  CHECK(scheduler.num_waiting() == 1);
-  scheduler.finish_sequence(id0);
-  out = scheduler.schedule();
-  CHECK(std::find(out.finished.begin(), out.finished.end(), id0) != out.finished.end());
-  CHECK(out.running.size() == 2);
-}
-
-TEST(test_scheduler_memory_limits, false) {
-  ContinuousBatchingConfig config;
-  config.max_batch_size = 10;
-  config.total_blocks = 5;
-  config.block_size = 4;
-  config.enable_preemption = false;
-  ContinuousBatchingScheduler scheduler(config);
-  for (int i = 0; i < 10; ++i) scheduler.add_sequence(std::vector<int64_t>(3, i), 10);
-  const ScheduleOutput out = scheduler.schedule();
-  CHECK(out.running.size() <= 5);
-  CHECK(out.running.size() == 5);  // each needs ceil(4/4) = 1 block: exactly five fit
-}
-
-TEST(test_scheduler_preemption, false) {
-  ContinuousBatchingConfig config;
-  config.max_batch_size = 10;
-  config.total_blocks = 10;
-  config.block_size = 4;
-  config.enable_preemption = true;
-  ContinuousBatchingScheduler scheduler(config);
-  const size_t id0 = scheduler.add_sequence(std::vector<int64_t>(15, 1), 100);
-  ScheduleOutput out = scheduler.schedule();
-  CHECK(std::find(out.running.begin(), out.running.end(), id0) != out.running.end());
-  for (int i = 0; i < 30; ++i) scheduler.update_sequence(id0, 99);
-  for (int i = 0; i < 10; ++i) scheduler.add_sequence(std::vector<int64_t>(10, 1), 50);
-  out = scheduler.schedule();
-  CHECK(!out.preempted.empty() || out.running.size() < 10);
-}
-
-TEST(test_scheduling_policies, false) {
-  ContinuousBatchingConfig config;
-  config.max_batch_size = 1;
-  config.total_blocks = 100;
-  config.policy = SchedulingPolicy::ShortestFirst;
-  ContinuousBatchingScheduler scheduler(config);
-  scheduler.add_sequence({1}, 100);
-  const size_t short_id = scheduler.add_sequence({2}, 10);
-  const ScheduleOutput out = scheduler.schedule();
-  CHECK(out.running.size() == 1 && out.running[0] == short_id);
-}
-
-TEST(test_stats, false) {
-  ContinuousBatchingScheduler scheduler((ContinuousBatchingConfig()));
-  scheduler.add_sequence({1, 2, 3}, 10);
-  scheduler.add_sequence({4, 5}, 10);
-  scheduler.schedule();
-  const BatchingStats stats = scheduler.stats();
-  CHECK(stats.num_running == 2);
-  CHECK(stats.total_running_tokens == 5);
-  CHECK(stats.utilization > 0.0f);
-  // each needs ceil((len + 1) / 16) = 1 block of the default 1000
-  CHECK(stats.free_blocks == 998);
-}
-
-// ---- tie-breaking and bookkeeping the reference fixes through Rust's iterator semantics --------
-
-TEST(test_policy_ties, false) {
-  // max_by_key keeps the last maximum, min_by_key the first minimum
-  for (SchedulingPolicy p : {SchedulingPolicy::LongestFirst, SchedulingPolicy::ShortestFirst}) {
-    ContinuousBatchingConfig config;
-    config.max_batch_size = 1;
-    config.policy = p;
-    ContinuousBatchingScheduler scheduler(config);
-    const size_t a = scheduler.add_sequence({1}, 7);
-    const size_t b = scheduler.add_sequence({2}, 7);
-    const ScheduleOutput out = scheduler.schedule();
-    CHECK(out.running.size() == 1);
-    CHECK(out.running[0] == (p == SchedulingPolicy::LongestFirst ? b : a));
-  }
-}
-
-TEST(test_preemption_order_and_requeue, false) {
-  // Two running sequences hold 2 blocks each and none is free; a's growth to 3 blocks fails, so
-  // the preemption loop (while no block is free) evicts the last of the two with the most blocks,
-  // b, which frees 2 blocks and ends the loop. b goes to the front of the queue and is admitted
-  // again in the same call (it still needs 2 blocks); a keeps its 2.
-  ContinuousBatchingConfig config;
-  config.max_batch_size = 4;
-  config.total_blocks = 4;
-  config.block_size = 4;
-  ContinuousBatchingScheduler s(config);
-  const size_t a = s.add_sequence(std::vector<int64_t>(7, 1), 100);  // ceil(8/4) = 2 blocks
-  const size_t b = s.add_sequence(std::vector<int64_t>(7, 1), 100);
-  ScheduleOutput out = s.schedule();
-  CHECK(out.running.size() == 2 && out.free_blocks == 0);
-  s.update_sequence(a, 0);  // a now needs ceil(9/4) = 3 blocks
-  out = s.schedule();
-  CHECK(out.preempted.size() == 1 && out.preempted[0] == b);
-  CHECK((out.running == std::vector<size_t>{a, b}));
-  CHECK(s.get_sequence(b)->status == SequenceStatus::Running);
-  CHECK(s.get_sequence(a)->num_blocks == 2 && s.get_sequence(b)->num_blocks == 2);
-  CHECK(out.free_blocks == 0);
-}
-
-TEST(test_finished_blocks_return, false) {
-  ContinuousBatchingConfig config;
-  config.max_batch_size = 8;
-  config.total_blocks = 10;
-  config.block_size = 4;
-  ContinuousBatchingScheduler s(config);
-  const size_t a = s.add_sequence({1, 2, 3, 4, 5}, 1);  // ceil(6/4) = 2 blocks
-  s.schedule();
-  CHECK(s.stats().free_blocks == 8);
-  s.update_sequence(a, 9);  // generated 1 of 1: finished
-  const ScheduleOutput out = s.schedule();
-  CHECK(out.finished.size() == 1 && out.finished[0] == a);
-  CHECK(out.free_blocks == 10);
-  CHECK(s.remove_sequence(a).has_value() && s.is_empty());
-}
 
 // ---- ragged batches: metadata from the block tables --------------------------------------------
 
 TEST(test_ragged_batch_metadata, true) {
   PagedScheduler ps(PagedKvCacheConfig(4, 32, 2, 64, 1), SP_BF16);
   std::vector<size_t> ids;
-  for (int i = 0; i < 3; ++i) ids.push_back(ps.add_sequence().unwrap());
+  for (int i = 0; i < 4; ++i) ids.push_back(ps.add_sequence().unwrap());
   // interleave growth so the tables are not contiguous
   CHECK(ps.allocate(ids[0], 5).is_ok());
   CHECK(ps.allocate(ids[1], 2).is_ok());
   ps.get_sequence_mut(ids[0])->block_table.increment_seq_len(5);
   ps.get_sequence_mut(ids[1])->block_table.increment_seq_len(2);
-  const std::vector<BatchEntry> entries = {{ids[0], 1}, {ids[1], 7}, {ids[2], 3}};
+  const std::vector<BatchEntry> entries = {{ids[0], 1}, {ids[1], 7}, {ids[3], 1}, {ids[2], 3}};
   Result<RaggedBatch> r = build_ragged_batch(ps, entries);
   CHECK(r.is_ok());
   const RaggedBatch& b = r.unwrap();
-  CHECK(b.num_seqs() == 3 && b.num_tokens() == 11);
-  CHECK((b.cu_seqlens_q == std::vector<int32_t>{0, 1, 8, 11}));
-  CHECK((b.context_lens == std::vector<int32_t>{6, 9, 3}));
+  // chunks first (ids[1], ids[2]), then the one-token entries (ids[0], ids[3]), each group in
+  // the caller's order
+  CHECK((b.seq_ids == std::vector<size_t>{ids[1], ids[2], ids[0], ids[3]}));
+  CHECK(b.num_seqs() == 4 && b.num_tokens() == 12);
+  CHECK(b.num_prefill_seqs == 2 && b.num_prefill_tokens == 10 && b.num_decode_seqs() == 2);
+  CHECK((b.cu_seqlens_q == std::vector<int32_t>{0, 7, 10, 11, 12}));
+  CHECK((b.context_lens == std::vector<int32_t>{9, 3, 6, 1}));
   CHECK(b.max_seqlen_q == 7 && b.max_context_len == 9 && !b.decode_only());
+  CHECK(b.prefill_max_seqlen_q == 7 && b.decode_max_context_len == 6);
   size_t t = 0;
-  for (size_t s = 0; s < 3; ++s) {
-    const BlockTable& table = ps.get_sequence(ids[s])->block_table;
+  for (size_t s = 0; s < b.num_seqs(); ++s) {
+    const BlockTable& table = ps.get_sequence(b.seq_ids[s])->block_table;
     const size_t start = table.seq_len();
-    for (size_t i = 0; i < entries[s].num_new; ++i, ++t) {
+    const size_t n = (size_t)(b.cu_seqlens_q[s + 1] - b.cu_seqlens_q[s]);
+    for (size_t i = 0; i < n; ++i, ++t) {
       const size_t pos = start + i;
       CHECK(b.positions[t] == (int32_t)pos);
       CHECK(b.slot_mapping[t] == (int32_t)(table.blocks()[pos / 4] * 4 + pos % 4));
@@ -201,6 +64,24 @@ TEST(test_ragged_batch_metadata, true) {
   CHECK(std::adjacent_find(sl.begin(), sl.end()) == sl.end());
   commit_ragged_batch(ps, b);
   CHECK(ps.get_sequence(ids[1])->block_table.seq_len() == 9);
+  CHECK(ps.get_sequence(ids[0])->block_table.seq_len() == 6);
+  // a batch of one-token entries only is a decode batch
+  Result<RaggedBatch> d = build_ragged_batch(ps, {{ids[2], 1}, {ids[3], 1}});
+  CHECK(d.is_ok() && d.unwrap().decode_only() && d.unwrap().num_prefill_seqs == 0);
+}
+
+TEST(test_ragged_batch_rejects_bad_entries, true) {
+  PagedScheduler ps(PagedKvCacheConfig(4, 8, 1, 64, 1), SP_BF16);
+  const size_t a = ps.add_sequence().unwrap();
+  const size_t b = ps.add_sequence().unwrap();
+  const size_t free0 = ps.cache.num_free_blocks();
+  Result<RaggedBatch> r0 = build_ragged_batch(ps, {{a, 1}, {b, 0}});
+  CHECK(r0.is_err() && strcmp(r0.error(), "Empty batch entry") == 0);
+  Result<RaggedBatch> r1 = build_ragged_batch(ps, {{a, 2}, {b, 1}, {a, 1}});
+  CHECK(r1.is_err() && strcmp(r1.error(), "Duplicate sequence ID") == 0);
+  CHECK(ps.cache.num_free_blocks() == free0);  // rejected before anything was allocated
+  Result<RaggedBatch> r2 = build_ragged_batch(ps, {});
+  CHECK(r2.is_ok() && r2.unwrap().num_seqs() == 0);
 }
 
 TEST(test_ragged_batch_out_of_memory, true) {
@@ -212,7 +93,7 @@ TEST(test_ragged_batch_out_of_memory, true) {
   CHECK(r2.is_err() && strcmp(r2.error(), "Invalid sequence ID") == 0);
 }
 
-// ---- a continuous-batching loop on the GPU ------------------------------------------------------
+// ---- GPU loops ----------------------------------------------------------------------------------
 
 namespace {
 
@@ -238,123 +119,186 @@ float bf16_value(uint16_t h) {
   return f;
 }
 
-struct History {  // one sequence's appended K/V rows, [pos][Hkv][D]
+struct History {  // one sequence's appended K/V rows of one layer, [pos][Hkv][D]
   std::vector<float> k, v;
-  size_t len = 0;
+};
+
+// Random bf16 q / k / v rows of one layer of a batch, on the host and the device.
+struct LayerInputs {
+  std::vector<uint16_t> qh, kh, vh;
+  DeviceTensor q, k, v, o;
+  LayerInputs(size_t T, int hq, int hkv, int d, std::mt19937& rng) {
+    std::normal_distribution<float> nd(0.f, 1.f);
+    qh.resize(T * hq * d);
+    kh.resize(T * hkv * d);
+    vh.resize(T * hkv * d);
+    for (auto& x : qh) x = bf16_bits(nd(rng));
+    for (auto& x : kh) x = bf16_bits(nd(rng));
+    for (auto& x : vh) x = bf16_bits(nd(rng));
+    q = DeviceTensor::from_host(qh.data(), {(int64_t)T, hq, d}, SP_BF16);
+    k = DeviceTensor::from_host(kh.data(), {(int64_t)T, hkv, d}, SP_BF16);
+    v = DeviceTensor::from_host(vh.data(), {(int64_t)T, hkv, d}, SP_BF16);
+    o = DeviceTensor({(int64_t)T, hq, d}, SP_BF16);
+  }
+};
+
+// Appends the batch's new rows to each sequence's history, then checks every output row against
+// float64 attention over the history up to the row's position (no mask for one new token, the
+// causal rule inside a chunk), GQA head h -> KV head h / (hq / hkv). Returns the worst |error|.
+double check_layer(const RaggedBatch& b, const LayerInputs& in, const std::vector<uint16_t>& oh,
+                   std::map<size_t, History>& hist, int hq, int hkv, int d, float scale) {
+  double worst = 0.0;
+  for (size_t s = 0; s < b.num_seqs(); ++s) {
+    History& H = hist[b.seq_ids[s]];
+    for (int t = b.cu_seqlens_q[s]; t < b.cu_seqlens_q[s + 1]; ++t)
+      for (int x = 0; x < hkv * d; ++x) {
+        H.k.push_back(bf16_value(in.kh[(size_t)t * hkv * d + x]));
+        H.v.push_back(bf16_value(in.vh[(size_t)t * hkv * d + x]));
+      }
+    for (int t = b.cu_seqlens_q[s]; t < b.cu_seqlens_q[s + 1]; ++t) {
+      const size_t pos = (size_t)b.positions[t];
+      for (int h = 0; h < hq; ++h) {
+        const int g = h / (hq / hkv);
+        std::vector<double> sc(pos + 1);
+        double mx = -1e300;
+        for (size_t j = 0; j <= pos; ++j) {
+          double acc = 0;
+          for (int e = 0; e < d; ++e)
+            acc += (double)bf16_value(in.qh[((size_t)t * hq + h) * d + e]) *
+                   H.k[(j * hkv + g) * d + e];
+          sc[j] = acc * scale;
+          mx = std::max(mx, sc[j]);
+        }
+        double den = 0;
+        for (auto& x : sc) den += (x = exp(x - mx));
+        for (int e = 0; e < d; ++e) {
+          double num = 0;
+          for (size_t j = 0; j <= pos; ++j) num += sc[j] * H.v[(j * hkv + g) * d + e];
+          worst = std::max(worst, fabs(num / den - bf16_value(oh[((size_t)t * hq + h) * d + e])));
+        }
+      }
+    }
+  }
+  return worst;
+}
+
+// A request of the serving loop below: prompt tokens still to prefill, tokens still to generate.
+struct Request {
+  size_t prompt_left;
+  size_t gen_left;
+  size_t paged_id = 0;
+  bool admitted = false;
 };
 
 }  // namespace
 
-TEST(test_continuous_batching_loop, true) {
-  const int hq = 8, hkv = 2, d = 64, bs = 16, chunk = 24;
+// Serving loop: at most `slots` requests run at once; each step gives every running request its
+// next prompt chunk (up to `chunk` tokens) or one decode token, retires requests whose last
+// token was produced (their blocks go back to the pool) and admits waiting requests in arrival
+// order into the freed slots. Steps therefore mix chunks and decode tokens in one batch.
+TEST(test_serving_loop_mixed_batches, true) {
+  const int hq = 8, hkv = 2, d = 64, bs = 16, chunk = 24, slots = 4;
   const float scale = 1.0f / sqrtf((float)d);
   PagedScheduler ps(PagedKvCacheConfig(bs, 96, hkv, d, 1), SP_BF16);
   BatchedPagedAttention attn(ps.cache);
-  ContinuousBatchingConfig cfg;
-  cfg.max_batch_size = 4;
-  cfg.block_size = bs;
-  cfg.total_blocks = 96;
-  cfg.enable_preemption = false;
-  ContinuousBatchingScheduler cb(cfg);
   std::mt19937 rng(1234);
-  std::normal_distribution<float> nd(0.f, 1.f);
-  std::map<size_t, size_t> paged_id;    // scheduler id -> PagedScheduler id
-  std::map<size_t, size_t> prompt_left;  // prompt tokens not yet in the cache
+  std::deque<Request> waiting;
+  for (int i = 0; i < 7; ++i) waiting.push_back({1 + rng() % 57, 2 + rng() % 5});
+  std::vector<Request> running;
   std::map<size_t, History> hist;
-  for (int i = 0; i < 7; ++i) {
-    const size_t plen = 1 + rng() % 57;
-    const size_t id = cb.add_sequence(std::vector<int64_t>(plen, 1), 2 + rng() % 5);
-    prompt_left[id] = plen;
-  }
-  int iterations = 0, prefill_steps = 0, decode_steps = 0;
+  int steps = 0, mixed_steps = 0, prefill_only = 0, decode_only = 0;
   double worst = 0.0;
-  while (!cb.is_empty() && iterations < 200) {
-    ++iterations;
-    const ScheduleOutput so = cb.schedule();
-    for (size_t f : so.finished) {
-      ps.free_sequence(paged_id.at(f));
-      cb.remove_sequence(f);
+  while ((!waiting.empty() || !running.empty()) && steps < 200) {
+    ++steps;
+    while ((int)running.size() < slots && !waiting.empty()) {
+      running.push_back(waiting.front());
+      waiting.pop_front();
+      running.back().paged_id = ps.add_sequence().unwrap();
     }
-    if (so.running.empty()) continue;
     std::vector<BatchEntry> entries;
-    std::vector<size_t> sched_ids;
-    for (size_t id : so.running) {
-      if (!paged_id.count(id)) paged_id[id] = ps.add_sequence().unwrap();
-      const size_t n = prompt_left[id] > 0 ? std::min<size_t>(prompt_left[id], chunk) : 1;
-      entries.push_back({paged_id[id], n});
-      sched_ids.push_back(id);
-    }
+    for (const Request& r : running)
+      entries.push_back({r.paged_id, r.prompt_left > 0 ? std::min<size_t>(r.prompt_left, chunk)
+                                                       : (size_t)1});
     Result<RaggedBatch> rb = build_ragged_batch(ps, entries);
     CHECK(rb.is_ok());
     if (rb.is_err()) return;
     const RaggedBatch& b = rb.unwrap();
-    const size_t T = b.num_tokens();
-    std::vector<uint16_t> qh(T * hq * d), kh(T * hkv * d), vh(T * hkv * d);
-    for (auto& x : qh) x = bf16_bits(nd(rng));
-    for (auto& x : kh) x = bf16_bits(nd(rng));
-    for (auto& x : vh) x = bf16_bits(nd(rng));
-    DeviceTensor q = DeviceTensor::from_host(qh.data(), {(int64_t)T, hq, d}, SP_BF16);
-    DeviceTensor k = DeviceTensor::from_host(kh.data(), {(int64_t)T, hkv, d}, SP_BF16);
-    DeviceTensor v = DeviceTensor::from_host(vh.data(), {(int64_t)T, hkv, d}, SP_BF16);
-    DeviceTensor o({(int64_t)T, hq, d}, SP_BF16);
+    LayerInputs in(b.num_tokens(), hq, hkv, d, rng);
     DeviceRaggedBatch db(b, ps.cache.stream());
-    attn.forward(0, db, q, k, v, o, scale);
-    std::vector<uint16_t> oh(T * hq * d);
-    o.to_host(oh.data());
-    (b.decode_only() ? decode_steps : prefill_steps) += 1;
-    // host reference: each new token attends its sequence's keys 0..pos (the history plus the
-    // new rows up to itself), GQA head h -> kv head h / (hq / hkv)
-    for (size_t s = 0; s < b.num_seqs(); ++s) {
-      History& H = hist[sched_ids[s]];
-      for (int t = b.cu_seqlens_q[s]; t < b.cu_seqlens_q[s + 1]; ++t) {
-        for (int x = 0; x < hkv * d; ++x) {
-          H.k.push_back(bf16_value(kh[(size_t)t * hkv * d + x]));
-          H.v.push_back(bf16_value(vh[(size_t)t * hkv * d + x]));
-        }
-        H.len += 1;
-      }
-      for (int t = b.cu_seqlens_q[s]; t < b.cu_seqlens_q[s + 1]; ++t) {
-        const size_t pos = (size_t)b.positions[t];
-        for (int h = 0; h < hq; ++h) {
-          const int g = h / (hq / hkv);
-          std::vector<double> sc(pos + 1);
-          double mx = -1e300;
-          for (size_t j = 0; j <= pos; ++j) {
-            double acc = 0;
-            for (int e = 0; e < d; ++e)
-              acc += (double)bf16_value(qh[((size_t)t * hq + h) * d + e]) *
-                     H.k[(j * hkv + g) * d + e];
-            sc[j] = acc * scale;
-            mx = std::max(mx, sc[j]);
-          }
-          double den = 0;
-          for (auto& x : sc) den += (x = exp(x - mx));
-          for (int e = 0; e < d; ++e) {
-            double num = 0;
-            for (size_t j = 0; j <= pos; ++j) num += sc[j] * H.v[(j * hkv + g) * d + e];
-            const double err =
-                fabs(num / den - bf16_value(oh[((size_t)t * hq + h) * d + e]));
-            worst = std::max(worst, err);
-          }
-        }
-      }
-    }
+    attn.forward(0, db, in.q, in.k, in.v, in.o, scale);
+    std::vector<uint16_t> oh(b.num_tokens() * hq * d);
+    in.o.to_host(oh.data());
+    if (b.decode_only()) ++decode_only;
+    else if (b.num_decode_seqs() == 0) ++prefill_only;
+    else ++mixed_steps;
+    worst = std::max(worst, check_layer(b, in, oh, hist, hq, hkv, d, scale));
     commit_ragged_batch(ps, b);
-    for (size_t s = 0; s < b.num_seqs(); ++s) {
-      const size_t id = sched_ids[s];
-      const size_t n = (size_t)(b.cu_seqlens_q[s + 1] - b.cu_seqlens_q[s]);
-      if (prompt_left[id] > 0) {
-        prompt_left[id] -= n;
-        if (prompt_left[id] == 0) cb.update_sequence(id, 0);  // the prompt's last step emits one
+    // the step's outputs: a prompt's last chunk and every decode step produce one token
+    std::vector<Request> still;
+    for (Request& r : running) {
+      const size_t n = entries[&r - running.data()].num_new;
+      if (r.prompt_left > 0) {
+        r.prompt_left -= n;
+        if (r.prompt_left == 0) --r.gen_left;
       } else {
-        cb.update_sequence(id, 0);
+        --r.gen_left;
       }
+      if (r.gen_left == 0) ps.free_sequence(r.paged_id);
+      else still.push_back(r);
     }
+    running.swap(still);
   }
-  printf("  %d iterations (%d with prompt chunks, %d decode-only), worst |err| %.3g\n",
-         iterations, prefill_steps, decode_steps, worst);
-  CHECK(cb.is_empty());
-  CHECK(prefill_steps > 0 && decode_steps > 0);
+  printf("  %d steps (%d mixed, %d chunks only, %d decode only), worst |err| %.3g\n", steps,
+         mixed_steps, prefill_only, decode_only, worst);
+  CHECK(waiting.empty() && running.empty());
+  CHECK(mixed_steps > 0 && decode_only > 0);
   CHECK(worst <= 2e-2);
   CHECK(ps.cache.num_free_blocks() == 96);  // every block returned
+}
+
+// Three layers interleaved in one pool ([num_blocks][3][Hkv][BS][D]): each step appends every
+// layer's rows at the same positions and attends the same lengths, the sequence lengths advance
+// once per step, and no layer's rows overwrite another's.
+TEST(test_multi_layer_step, true) {
+  const int hq = 8, hkv = 2, d = 128, bs = 16, layers = 3;
+  const float scale = 1.0f / sqrtf((float)d);
+  PagedScheduler ps(PagedKvCacheConfig(bs, 64, hkv, d, layers), SP_BF16);
+  BatchedPagedAttention attn(ps.cache);
+  std::mt19937 rng(99);
+  std::vector<size_t> ids;
+  for (int i = 0; i < 3; ++i) ids.push_back(ps.add_sequence().unwrap());
+  std::vector<std::map<size_t, History>> hist(layers);
+  // a prefill step (two prompts and an empty-history one-token start), then mixed and decode
+  const std::vector<std::vector<BatchEntry>> plan = {
+      {{ids[0], 37}, {ids[1], 70}, {ids[2], 1}},
+      {{ids[0], 1}, {ids[1], 1}, {ids[2], 45}},
+      {{ids[0], 1}, {ids[1], 1}, {ids[2], 1}},
+      {{ids[0], 19}, {ids[1], 1}, {ids[2], 1}},
+  };
+  double worst = 0.0;
+  for (const auto& entries : plan) {
+    std::vector<size_t> before;
+    for (size_t id : ids) before.push_back(ps.get_sequence(id)->block_table.seq_len());
+    Result<RaggedBatch> r = run_batched_step(
+        ps, entries, layers, ps.cache.stream(), [&](size_t layer, const DeviceRaggedBatch& db) {
+          const RaggedBatch& b = db.host();
+          // lengths are not advanced while the layers run
+          for (size_t i = 0; i < ids.size(); ++i)
+            CHECK(ps.get_sequence(ids[i])->block_table.seq_len() == before[i]);
+          LayerInputs in(b.num_tokens(), hq, hkv, d, rng);
+          attn.forward(layer, db, in.q, in.k, in.v, in.o, scale);
+          std::vector<uint16_t> oh(b.num_tokens() * hq * d);
+          in.o.to_host(oh.data());
+          worst = std::max(worst, check_layer(b, in, oh, hist[layer], hq, hkv, d, scale));
+        });
+    CHECK(r.is_ok());
+    for (size_t i = 0; i < ids.size(); ++i) {
+      size_t add = 0;
+      for (const BatchEntry& e : entries)
+        if (e.seq_id == ids[i]) add = e.num_new;
+      CHECK(ps.get_sequence(ids[i])->block_table.seq_len() == before[i] + add);
+    }
+  }
+  printf("  %zu steps x %d layers, worst |err| %.3g\n", plan.size(), layers, worst);
+  CHECK(worst <= 2e-2);
 }

@@ -267,10 +267,16 @@ def test_flash_attention_dense(causal, sq, sk):
     assert_attention_close(_as_f64(out), ref, "bf16", "flash_attention")
 
 
-def run_chunked(w: W.ChunkedPrefillWorkload, sample_rows=None, split=False):
+def run_chunked(w: W.ChunkedPrefillWorkload, sample_rows=None, split=False, shift=None):
     """split: hand sp_paged_prefill the workspace it asks for, so long contexts are split over
-    several workgroups per query block (the test asserts that a split is planned)."""
+    several workgroups per query block (the test asserts that a split is planned).
+    shift: (q_mean, k_mean) moves q and every cached / new key off N(0,1) (q = q_mean + x/2,
+    k = k_mean + x/2), so the scores sit far from zero."""
     t = W.make_chunked_tensors(w)
+    if shift is not None:
+        qm, km = shift
+        for name, m in (("q", qm), ("k_pool", km), ("k_new", km)):
+            t[name].copy_((m + 0.5 * t[name].float()).to(t[name].dtype))
     lay = sp.layout(t["num_blocks"], 1, 0, w.hkv, w.block_size, w.head_dim)
     ws = None
     if split:
@@ -343,6 +349,17 @@ def test_paged_prefill_split_keys(window):
                                  np.array([3000, 2100, 5000], np.int32), 8, 2, 128, "bf16",
                                  window_left=window)
     run_chunked(w, split=True)
+
+
+@pytest.mark.parametrize("shift", [None, (2.0, -12.0)])
+def test_paged_prefill_split_with_empty_splits(shift):
+    """A key split planned from the table width (one long context) over a batch that also holds
+    a short context (48 keys) and a fresh 128-query chunk: their later splits see no key. With
+    (2, -12) every score sits near x = q.k * scale * log2(e) = -390, so a split that saw no key
+    must not lend its offset to the merge. Every row against the f64 oracle."""
+    w = W.ChunkedPrefillWorkload("chunked-split-empty", 48, np.array([64, 32, 128], np.int32),
+                                 np.array([3000, 16, 0], np.int32), 8, 2, 128, "bf16")
+    run_chunked(w, split=True, shift=shift)
 
 
 @pytest.mark.parametrize("split", [False, True])
