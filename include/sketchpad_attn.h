@@ -188,6 +188,24 @@ int sp_paged_decode(void* out, const void* q,
                     void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * sp_paged_decode without a workspace argument: the split partials go to a scratch array the
+ * library holds on each GPU it runs on (32 MiB, kept until the process ends), so the call
+ * allocates nothing. No counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * allocation). Same arguments and results as sp_paged_decode with the workspace it asks for
+ * (the same split plan, so the same kernels and merge order). A batch whose partials exceed the
+ * scratch (sp_paged_decode_workspace_size() > 32 MiB) returns SP_ENOSPACE before any launch.
+ * Every call on one GPU shares that GPU's scratch: calls that overlap on one GPU (other streams,
+ * other threads) race and must be serialised by the caller.
+ */
+int sp_paged_decode_noalloc(void* out, const void* q,
+                            const void* k_pool, const void* v_pool, const sp_cache_layout* layout,
+                            const int32_t* block_tables, int32_t max_blocks_per_seq,
+                            const int32_t* context_lens, int32_t max_context_len,
+                            int32_t num_seqs, int32_t num_q_heads,
+                            float scale, int32_t window_left, sp_dtype dtype, void* stream);
+
+/*
  * Prefill attention over packed variable-length sequences (FlashAttention-2 style, MFMA).
  * Replaces MultiHeadAttention::forward with causal_mask / sliding_window_mask
  * (transformer.rs:103-168, :415-451) and flash_attention (sketchpad-cubecl attention.rs:97-178),

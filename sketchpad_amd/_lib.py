@@ -72,6 +72,10 @@ _SIGNATURES = {
     "sp_paged_decode": (c_int32, [c_void_p, c_void_p, c_void_p, c_void_p, POINTER(CacheLayout),
                                   c_void_p, c_int32, c_void_p, c_int32, c_int32, c_int32,
                                   c_float, c_int32, c_int32, c_void_p, c_size_t, c_void_p]),
+    "sp_paged_decode_noalloc": (c_int32, [c_void_p, c_void_p, c_void_p, c_void_p,
+                                          POINTER(CacheLayout), c_void_p, c_int32, c_void_p,
+                                          c_int32, c_int32, c_int32, c_float, c_int32, c_int32,
+                                          c_void_p]),
     "sp_varlen_prefill": (c_int32, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                                     c_int32, c_int32, c_int32, c_int32, c_int32, c_float,
                                     c_int32, c_int32, c_int32, c_void_p]),
@@ -246,6 +250,19 @@ def paged_decode(out, q, k_pool, v_pool, lay: CacheLayout, block_tables, context
                                  _ptr(context_lens), max_context_len, num_seqs, hq, scale,
                                  window_left, sp_dtype(q), _ptr(workspace), ws_bytes,
                                  _stream(stream)))
+
+
+def paged_decode_noalloc(out, q, k_pool, v_pool, lay: CacheLayout, block_tables, context_lens,
+                         max_context_len: int, scale: float, *, window_left: int = -1,
+                         stream=None) -> None:
+    """sp_paged_decode_noalloc: sp_paged_decode with the split partials in the library's own
+    per-GPU scratch (no workspace argument, no allocation)."""
+    num_seqs, hq = q.shape[0], q.shape[1]
+    check(load().sp_paged_decode_noalloc(_ptr(out), _ptr(q), _ptr(k_pool), _ptr(v_pool),
+                                         ctypes.byref(lay), _ptr(block_tables),
+                                         block_tables.shape[1], _ptr(context_lens),
+                                         max_context_len, num_seqs, hq, scale, window_left,
+                                         sp_dtype(q), _stream(stream)))
 
 
 def alloc_decode_workspace(num_seqs: int, num_q_heads: int, max_context_len: int,

@@ -299,6 +299,28 @@ int sp_paged_decode(void* out, const void* q, const void* k_pool, const void* v_
   return launch_paged_decode(a, dtype, layout->head_dim, (hipStream_t)stream);
 }
 
+int sp_paged_decode_noalloc(void* out, const void* q, const void* k_pool, const void* v_pool,
+                            const sp_cache_layout* layout, const int32_t* block_tables,
+                            int32_t max_blocks_per_seq, const int32_t* context_lens,
+                            int32_t max_context_len, int32_t num_seqs, int32_t num_q_heads,
+                            float scale, int32_t window_left, sp_dtype dtype, void* stream) {
+  const char* fn = "sp_paged_decode_noalloc";
+  // The split plan (and so the partials' size) is sp_paged_decode's for the same shape, so both
+  // entry points run the same kernels on the same split boundaries.
+  const size_t need = sp_paged_decode_workspace_size(num_seqs, num_q_heads, max_context_len,
+                                                     window_left, layout);
+  if (need > kDecodeScratchBytes)
+    return fail(SP_ENOSPACE,
+                "%s: this batch needs %zu bytes of split partials, past the library's %zu-byte "
+                "scratch; call sp_paged_decode with a workspace instead",
+                fn, need, kDecodeScratchBytes);
+  void* ws = nullptr;
+  if (need > 0 && !(ws = decode_scratch_on_current_device())) return SP_EHIP;
+  return sp_paged_decode(out, q, k_pool, v_pool, layout, block_tables, max_blocks_per_seq,
+                         context_lens, max_context_len, num_seqs, num_q_heads, scale,
+                         window_left, dtype, ws, need > 0 ? kDecodeScratchBytes : 0, stream);
+}
+
 static int check_prefill_common(const char* fn, int32_t num_seqs, int32_t max_seqlen_q,
                                 int32_t hq, int32_t hkv, int32_t D, float scale,
                                 int32_t causal, int32_t window_left, sp_dtype dtype) {

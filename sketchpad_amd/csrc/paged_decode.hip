@@ -27,7 +27,43 @@
 
 #include <math.h>
 
+#include <mutex>
+
 namespace sp {
+
+// Scratch of the entry point that allocates nothing (sp_paged_decode_noalloc). Each GPU the
+// library runs on holds its own copy at its own address; host code reaches it only through the
+// address hipGetSymbolAddress returns on that device (the array's name is a host-side stand-in).
+static __device__ __align__(256) char scratch[kDecodeScratchBytes];
+
+void* decode_scratch_on_current_device() {
+  constexpr int kMaxDevices = 64;
+  static std::mutex mu;
+  static void* addr[kMaxDevices] = {};
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    fail(SP_EHIP, "decode scratch: hipGetDevice: %s", hipGetErrorString(e));
+    return nullptr;
+  }
+  if (dev < 0 || dev >= kMaxDevices) {
+    fail(SP_EUNSUPPORTED, "decode scratch: device %d past the %d the library tracks", dev,
+         kMaxDevices);
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(mu);
+  if (!addr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      fail(SP_EHIP, "decode scratch: hipGetSymbolAddress on device %d: %s", dev,
+           hipGetErrorString(e));
+      return nullptr;
+    }
+    addr[dev] = p;
+  }
+  return addr[dev];
+}
 
 typedef __bf16 bf16x8_v __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8_v __attribute__((ext_vector_type(8)));

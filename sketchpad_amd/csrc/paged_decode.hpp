@@ -49,6 +49,13 @@ struct DecodeArgs {
 
 int launch_paged_decode(const DecodeArgs& a, sp_dtype dtype, int head_dim, hipStream_t stream);
 
+// Library-owned scratch for the decode partials of sp_paged_decode_noalloc: a file-scope device
+// array of kDecodeScratchBytes per GPU, held until the process ends. Returns its device address
+// on the current device (looked up once per device with hipGetSymbolAddress), or nullptr with
+// the error recorded.
+constexpr size_t kDecodeScratchBytes = (size_t)32 << 20;
+void* decode_scratch_on_current_device();
+
 // The split merge alone (no-op when a.max_splits <= 1): for kernels that write the same
 // (m, l, acc[D]) partials in 16-token tiles.
 int launch_decode_combine(const DecodeArgs& a, sp_dtype dtype, int head_dim, hipStream_t stream);
