@@ -397,7 +397,8 @@ size_t sp_paged_prefill_workspace_size(int32_t num_seqs, int32_t max_seqlen_q,
                                        int32_t num_q_heads, const sp_cache_layout* layout,
                                        int32_t max_blocks_per_seq) {
   if (!layout || num_seqs <= 0 || max_seqlen_q <= 0 || num_q_heads <= 0 ||
-      max_blocks_per_seq <= 0 || (layout->head_dim != 64 && layout->head_dim != 128))
+      layout->num_kv_heads <= 0 || max_blocks_per_seq <= 0 ||
+      (layout->head_dim != 64 && layout->head_dim != 128))
     return 0;
   const int64_t max_context = (int64_t)max_blocks_per_seq * layout->block_size;
   const int s = prefill_splits(num_seqs, max_seqlen_q, num_q_heads, layout->head_dim,

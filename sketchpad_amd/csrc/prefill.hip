@@ -18,10 +18,16 @@
 //   O^T[32 d, 32 q]   += V^T P^T B = P^T straight from the S^T registers (the 16 tokens of one
 //                                MFMA are taken in the order the S^T layout hands them out); A = V^T
 //                                from row-major V in LDS through ds_read_tr16_b64.
-// K/V tiles go HBM -> LDS with global_load_lds_dwordx4 (no register staging) into a double
-// buffer; the load of tile t+1 is issued right after the barrier that opens tile t. Rows are
-// stored with the 16-byte chunks XOR-swizzled so that the K reads (16 rows x one chunk) and the
-// V transpose reads (4 rows x 64 bytes) are bank-conflict free.
+// The key loop is software-pipelined inside each wave: while the QK MFMAs of tile j+1 run, the
+// same wave computes tile j's softmax (one slice of exponentials, packs and row sums after each
+// MFMA, in an order sched_barriers pin), then issues tile j's PV MFMAs. So the wave keeps the
+// MFMA and VALU pipes busy at once instead of leaving the overlap to the other wave on its SIMD.
+// K/V tiles go HBM -> LDS with global_load_lds_dwordx4 (no register staging) into double
+// buffers: K runs two tiles ahead of the PV product (its QK product runs one tile early), V one
+// tile ahead; interior tiles take one scalar base per tile (per block when paged, with the block
+// ids fetched a tile ahead). Rows are stored with the 16-byte chunks XOR-swizzled so that the K
+// reads (16 rows x one chunk) and the V transpose reads (4 rows x 64 bytes) are bank-conflict
+// free.
 // Only tiles that cross the causal diagonal, the window edge or the sequence end are masked.
 // Workgroups are ordered with the KV head fastest (all query heads of one KV head share an XCD's
 // L2) and the heaviest causal query blocks first.
@@ -108,17 +114,34 @@ __device__ __forceinline__ void swap_halves(float x, float& a, float& b) {
   b = __uint_as_float(r[1]);
 }
 
+// global_load_lds_dwordx4 from a base the compiler keeps in SGPRs (wave-uniform, computed by
+// scalar code) plus a per-lane byte offset; the s_nop covers the M0 write -> LDS DMA wait state.
+// Completion is awaited explicitly (s_waitcnt vmcnt(0) + barrier) before the data is read.
+__device__ __forceinline__ void lds_dma16_sbase(const char* sbase, int voff, char* lds_dst) {
+  const unsigned m0 = (unsigned)(uintptr_t)(lds_void*)lds_dst;
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "{m0}"(m0)
+               : "memory");
+}
+
 template <typename T, int D, bool PAGED>
 __global__ void __launch_bounds__(256, 2) prefill_kernel(PrefillArgs a) {
   using C = PrefillCfg<D>;
   using M = PrefillMfma<T>;
-  constexpr int BN = kPrefillBN, RB = C::RB, CPR = C::CPR, TILE = C::TILE, NLD = C::NLD;
+  constexpr int BN = kPrefillBN, RB = C::RB, CPR = C::CPR, TILE = C::TILE;
   constexpr int KC = C::KC, DB = C::DB;
+  constexpr int RPI = 1024 / RB;       // rows per 1 KiB load
+  constexpr int NLD = TILE / 2048;     // loads per wave per tile: waves 0-1 fill K, 2-3 fill V
+  constexpr int WROWS = NLD * RPI;     // rows of a tile one wave loads (half the tile)
   static_assert(BN == 64, "the S^T layout below assumes two 32-key MFMA blocks per tile");
-  __shared__ __attribute__((aligned(1024))) char lds0[C::BUF];
-  __shared__ __attribute__((aligned(1024))) char lds1[C::BUF];
+  static_assert(WROWS * 2 == BN, "two waves fill one tile");
+  __shared__ __attribute__((aligned(1024))) char kl[2][TILE];
+  __shared__ __attribute__((aligned(1024))) char vl[2][TILE];
 
-  // ---- workgroup -> (kv head, group member, sequence, query block), heavy query blocks first
+  // ---- workgroup -> (kv head, group member, sequence, split, query block), heavy query blocks
+  // first; wave w takes queries 32w .. 32w + 31 of the block
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = wave_uniform(tid >> 6);
   int id = blockIdx.x;
   const int kvh = id % a.hkv;
   id /= a.hkv;
@@ -157,9 +180,6 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PrefillArgs a) {
     kv_end = min(kv_hi, t_first + tps * BN);
   }
 
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = wave_uniform(tid >> 6);
   const int l32 = lane & 31, hh = lane >> 5;        // MFMA column (query) and half
   const int i16 = lane & 15, g4 = lane >> 4;        // 16-lane group for the transpose reads
 
@@ -182,12 +202,10 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PrefillArgs a) {
     vbase = (const char*)a.v + kv0 * 2;
   }
 
-  // ---- Q^T operand (B of the S^T MFMA): query wq0 + l32, dims 16c + 8hh .. +7. Q stays
-  // unscaled (its 16-bit values exactly): the scale is applied to the fp32 scores.
+  // ---- Q^T operand (B of the S^T MFMA): query wq0 + l32, dims 16c + 8hh .. +7, unscaled.
   const int wq0 = qs + 32 * wave;
   const int my_q = wq0 + l32;
   const float c2 = a.scale_log2;  // > 0 (checked on the host)
-  const float inv_c2 = 1.f / c2;
   uint4 qreg[KC];
   {
     const char* qp = qbase + (int64_t)min(my_q, qe - 1) * a.q_tok * 2;
@@ -196,59 +214,62 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PrefillArgs a) {
       qreg[c] = my_q < qe ? *(const uint4*)(qp + (16 * c + 8 * hh) * 2) : make_uint4(0, 0, 0, 0);
   }
 
-  // ---- HBM -> LDS tile load: wave instruction g moves 1 KiB = RPI rows; lane `lane` takes
-  // physical chunk p of row R and fetches the logical chunk that the swizzle puts there.
-  // Interior tiles (every row inside [kv_lo, kv_hi)) take the fast path: the row group of each
-  // instruction is wave-uniform, so its base address is scalar and the lane part is a constant
-  // offset computed once here. Edge tiles clamp rows outside [kv_lo, kv_hi) to a valid row
-  // (their scores are masked) and compute per-lane addresses.
-  constexpr int RPI = 64 / CPR;  // rows per 1 KiB load
+  // ---- HBM -> LDS tile loads. Waves 0-1 fill K tiles, running two tiles ahead of the PV product
+  // (the QK product of tile j+1 runs while tile j's softmax is computed); waves 2-3 fill V tiles,
+  // one tile ahead. Wave w's load u moves 1 KiB = RPI rows, r_u = (w & 1) * WROWS + u * RPI ..;
+  // lane `lane` takes physical chunk p = lane % CPR of row r_u + lane / CPR and fetches the
+  // logical chunk that the swizzle puts there. Interior tiles (every row inside [kv_lo, kv_hi))
+  // take the fast path: one scalar base per tile (non-paged) or per block (paged) plus a constant
+  // lane offset per load. Edge tiles clamp rows outside [kv_lo, kv_hi) to a valid row (their
+  // scores are masked) and compute per-lane addresses.
+  const bool v_wave = wave >= 2;
+  const int lead = v_wave ? 1 : 2;  // tiles ahead of the PV product this wave loads
+  const int wrow0 = (wave & 1) * WROWS;
   const int64_t row_pitch = PAGED ? (int64_t)RB : (int64_t)a.kv_tok * 2;
-  int voff[NLD];                  // lane part of each load's source offset (bytes)
+  const char* src_base = PAGED ? (v_wave ? a.vpool : a.kpool) : (v_wave ? vbase : kbase);
+  // paged fast path: a wave's WROWS rows of a tile lie in whole blocks (block_size divides the
+  // 64-row tile, and a load never straddles blocks)
+  const bool paged_fast = PAGED && a.block_size % RPI == 0 && BN % a.block_size == 0;
+  int voff[NLD];  // lane part of each load's source offset (bytes), row offset included
 #pragma unroll
   for (int u = 0; u < NLD; ++u) {
-    const int g = wave * NLD + u;
-    const int R = ((g * 1024) % TILE) / RB + lane / CPR;
-    voff[u] = (int)((lane / CPR) * row_pitch) + 16 * ((lane % CPR) ^ C::swz(R));
+    const int r = wrow0 + u * RPI + lane / CPR;  // tile row
+    const int64_t row_b = PAGED ? (int64_t)(r % max(a.block_size, 1)) * RB : (int64_t)r * row_pitch;
+    voff[u] = (int)row_b + 16 * ((lane % CPR) ^ C::swz(r));
   }
-  // Paged fast path: one block-table entry per load, fetched one tile ahead.
-  const bool paged_fast = PAGED && (a.block_size % RPI == 0);
-  int nblk[NLD];
-#pragma unroll
-  for (int u = 0; u < NLD; ++u) nblk[u] = 0;
   auto tile_interior = [&](int t0) __attribute__((always_inline)) {
     return t0 >= kv_lo && t0 + BN <= kv_hi;
   };
-  // block ids of tile t0's row groups (paged fast path)
+  // Paged fast path: the block ids of the rows of the next tile this wave loads, fetched one
+  // tile ahead (scalar loads) so that no load waits on a dependent block-table read.
+  int nblk[NLD];
+#pragma unroll
+  for (int u = 0; u < NLD; ++u) nblk[u] = 0;
   auto fetch_blocks = [&](int t0) __attribute__((always_inline)) {
     if constexpr (PAGED) {
-      if (paged_fast && t0 < kv_hi && tile_interior(t0)) {
+      if (paged_fast && t0 < kv_end && tile_interior(t0)) {
 #pragma unroll
-        for (int u = 0; u < NLD; ++u) {
-          const int g = wave * NLD + u;
-          const int row0 = t0 + ((g * 1024) % TILE) / RB;
-          nblk[u] = table[row0 / a.block_size];
-        }
+        for (int u = 0; u < NLD; ++u) nblk[u] = table[(t0 + wrow0 + u * RPI) / a.block_size];
       }
     }
   };
   auto issue_tile = [&](int t0, char* buf) __attribute__((always_inline)) {
+    char* dst = buf + wrow0 * RB;
     if (tile_interior(t0) && (!PAGED || paged_fast)) {
+      if constexpr (PAGED) {
+        // block ids fetched by fetch_blocks(t0); the readfirstlane keeps the base scalar (a no-op
+        // when the id is already in an SGPR), and the asm's wait states cover it otherwise
 #pragma unroll
-      for (int u = 0; u < NLD; ++u) {
-        const int g = wave * NLD + u;
-        const bool is_v = g * 1024 >= TILE;
-        const int row0 = t0 + ((g * 1024) % TILE) / RB;
-        const char* sb;
-        if constexpr (PAGED) {
+        for (int u = 0; u < NLD; ++u) {
           int blk = __builtin_amdgcn_readfirstlane(nblk[u]);
           blk = (blk >= 0 && blk < a.num_blocks) ? blk : 0;  // never outside the pool
-          sb = (is_v ? a.vpool : a.kpool) + (int64_t)blk * a.block_stride_b + head_off +
-               (int64_t)(row0 % a.block_size) * RB;
-        } else {
-          sb = (is_v ? vbase : kbase) + (int64_t)row0 * row_pitch;
+          const char* sb = src_base + (int64_t)blk * a.block_stride_b + head_off;
+          lds_dma16_s(sb, voff[u], dst + u * 1024);
         }
-        lds_dma16_s(sb, voff[u], buf + g * 1024);
+      } else {
+        const char* sb = src_base + (int64_t)t0 * row_pitch;
+#pragma unroll
+        for (int u = 0; u < NLD; ++u) lds_dma16_sbase(sb, voff[u], dst + u * 1024);
       }
       return;
     }
@@ -258,38 +279,34 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PrefillArgs a) {
     asm volatile("" : "+v"(ln));
 #pragma unroll
     for (int u = 0; u < NLD; ++u) {
-      const int g = wave * NLD + u;             // 0 .. BUF/1024 - 1 (K tiles first)
-      const bool is_v = g * 1024 >= TILE;
-      const int q = ((g * 1024) % TILE) / 16 + ln;
-      const int R = q / CPR, p = q % CPR;
+      const int R = wrow0 + u * RPI + ln / CPR, p = ln % CPR;
       const int c = p ^ C::swz(R);
       const int j = min(max(t0 + R, kv_lo), kv_hi - 1);
       const char* src;
       if constexpr (PAGED) {
         int blk = table[j / a.block_size];
         blk = (blk >= 0 && blk < a.num_blocks) ? blk : 0;  // never dereference outside the pool
-        const int64_t off = (int64_t)blk * a.block_stride_b + head_off +
-                            (int64_t)(j % a.block_size) * RB + c * 16;
-        src = (is_v ? a.vpool : a.kpool) + off;
+        src = src_base + (int64_t)blk * a.block_stride_b + head_off +
+              (int64_t)(j % a.block_size) * RB + c * 16;
       } else {
-        src = (is_v ? vbase : kbase) + (int64_t)j * a.kv_tok * 2 + c * 16;
+        src = src_base + (int64_t)j * row_pitch + c * 16;
       }
-      lds_dma16(src, buf + g * 1024);
+      lds_dma16(src, dst + u * 1024);
     }
   };
+
   // Online softmax state of query l32 (both lanes of a query hold the same values).
   // m_run: running maximum of the exponents x = q.k * scale * log2(e) seen (-inf before the
-  // first visible key); m_used: the offset subtracted from x (m_run once that is finite, else 0),
-  // applied through the QK accumulator input minit.
+  // first visible key); m_used: the offset subtracted from x (m_run once that is finite, else 0).
   float m_run = -INFINITY, m_used = 0.f, l_run = 0.f;
-  pf_f32x16 minit;  // -m_used / (scale * log2 e): accumulator input of the QK MFMAs
-#pragma unroll
-  for (int r = 0; r < 16; ++r) minit[r] = 0.f;
   pf_f32x16 acc[DB];
 #pragma unroll
   for (int db = 0; db < DB; ++db)
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[db][r] = 0.f;
+  pf_f32x16 zero16;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) zero16[r] = 0.f;
 
   const int wq_lo = wq0, wq_hi = min(wq0 + 32, qe) - 1;  // this wave's queries (inclusive)
   const bool wave_active = wq_lo < qe;
@@ -313,56 +330,47 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PrefillArgs a) {
   const int v_lane0 = rl * RB + 16 * (chl ^ C::swz(rl)) + 8 * (i16 & 1);
   const int v_lane1 = (rl + 8) * RB + 16 * (chl ^ C::swz(rl + 8)) + 8 * (i16 & 1);
 
-  // Causal diagonal at 32-key granularity. When the diagonal key of this wave's first query,
-  // diag0 = wq_lo + pos_off, is 32-aligned with the key tiles (always so for self-attention:
-  // wq_lo is a multiple of 32 and pos_off = 0), the diagonal 32x32 block of a tile is a fixed
-  // triangle: query l32 sees block keys 0..l32, i.e. score r of the lane iff
-  // 8(r/4) + r%4 <= l32 - 4hh; such tiles take one compare per score of that block instead of
-  // the general two-sided test on all 32. Every valid query's diagonal key is inside the
-  // sequence (checked below), so these tiles need no sequence-end mask either.
+  // Causal diagonal at 32-key granularity (see the mask below).
   const int diag0 = wave_uniform(wq_lo + pos_off);
   const bool tri_ok = a.causal != SP_CAUSAL_NONE && pos_off >= 0 && (pos_off & 31) == 0 &&
                       qe - 1 + pos_off < Lk;
   const int tri_lim = l32 - 4 * hh;
 
-  auto compute_tile = [&](int t0, const char* kl) __attribute__((always_inline)) {
-    const char* vl = kl + TILE;
-    // S^T = K Q^T: two 32-key blocks, interleaved so that consecutive MFMAs are independent.
-    // K operand i (k-step i/2, key block i%2) is row 32(i%2) + l32, chunk 2(i/2) + hh, i.e.
-    // (k_lane ^ 32(i/2)) + 32(i%2) RB; reads run AH operands ahead of the MFMAs, an order the
-    // sched_barriers pin. The lane base goes through an empty asm so the compiler derives the
-    // addresses inside the tile (one v_xor each) instead of keeping them all live.
-    // The first k-step of each key block takes minit (= -m_used / (scale * log2 e)) as its
-    // accumulator input, so s = q.k - m_used / (scale * log2 e) and the softmax weight of a
-    // score is 2^(s * scale * log2 e): one multiply and one exp per score.
-    pf_f32x16 s[2];
-    {
-      int kb = k_lane;
-      asm volatile("" : "+v"(kb));
-      constexpr int NK = 2 * KC, AH = 4;
-      auto read_k = [&](int i) __attribute__((always_inline)) {
-        return *(const uint4*)(kl + (i & 1) * 32 * RB + (kb ^ (32 * (i >> 1))));
-      };
-      uint4 kop[AH];
+  // ---- the pieces of one key tile -------------------------------------------------------------
+  // QK product S^T = K Q^T of the tile in LDS buffer kb into s (two 32-key blocks). K operand i
+  // (k-step i/2, key block i%2) is row 32(i%2) + l32, chunk 2(i/2) + hh: (k_lane ^ 32(i/2)) +
+  // 32(i%2) RB. `between(i)` runs after MFMA i: the softmax of the previous tile is interleaved
+  // with these MFMAs, one slice per MFMA, in an order the sched_barriers pin.
+  constexpr int NK = 2 * KC, AHK = 4;
+  auto qk = [&](const char* kb, pf_f32x16 (&s)[2], auto&& between) __attribute__((always_inline)) {
+    int kbl = k_lane;
+    asm volatile("" : "+v"(kbl));
+    auto read_k = [&](int i) __attribute__((always_inline)) {
+      return *(const uint4*)(kb + (i & 1) * 32 * RB + (kbl ^ (32 * (i >> 1))));
+    };
+    uint4 kop[AHK];
 #pragma unroll
-      for (int i = 0; i < AH; ++i) kop[i] = read_k(i);
+    for (int i = 0; i < AHK; ++i) kop[i] = read_k(i);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < NK; ++i) {
+      const uint4 cur = kop[i % AHK];
+      if (i + AHK < NK) kop[i % AHK] = read_k(i + AHK);
+      s[i & 1] = M::mma(cur, qreg[i >> 1], i < 2 ? zero16 : s[i & 1]);
+      between(i);
       __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int i = 0; i < NK; ++i) {
-        const uint4 cur = kop[i % AH];
-        if (i + AH < NK) kop[i % AH] = read_k(i + AH);
-        s[i & 1] = M::mma(cur, qreg[i >> 1], i < 2 ? minit : s[i & 1]);
-        __builtin_amdgcn_sched_barrier(0);
-      }
     }
-    // Masks, only on tiles that cross the sequence end, the window edge, kv_lo or the causal
-    // diagonal. Score (mb, r) of this lane is key t0 + 4hh + off, off = 32mb + 8(r/4) + r%4.
+  };
+
+  // Masks, only on tiles that cross the sequence end, the window edge, kv_lo or the causal
+  // diagonal. Score (mb, r) of this lane is key t0 + 4hh + off, off = 32mb + 8(r/4) + r%4.
+  auto apply_mask = [&](int t0, pf_f32x16 (&s)[2]) __attribute__((always_inline)) {
     if (t0 < mask_below || t0 > mask_above) {
       if (tri_ok && t0 >= mask_below && (t0 == diag0 || t0 + 32 == diag0)) {
         // 32-aligned causal diagonal: the diagonal block is the triangle 8(r/4) + r%4 <=
         // l32 - 4hh; with the diagonal at the tile start, block 1 lies wholly above it.
         int tl = tri_lim;
-        asm volatile("" : "+v"(tl));  // compare inside the tile (hoisted, 16 masks pin SGPRs)
+        asm volatile("" : "+v"(tl));
         if (t0 == diag0) {
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
@@ -390,40 +398,41 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PrefillArgs a) {
           }
       }
     }
-    // Online softmax for query l32 (FlashAttention-2, Dao 2023) with a lazily raised maximum.
-    // The weights are p = 2^(x - m_used), x = q.k * scale * log2(e), with the offset m_used
-    // already inside s (above). m_run only ever holds a maximum actually seen (m_used = m_run
-    // once it is finite), so the largest weight of the row never underflows; it is raised
-    // only when this lane's 32 weights of the tile sum past 2^kLazy (so every weight that enters
-    // the accumulators is <= 2^kLazy, far inside fp32 and bf16 range) or while the query has no
-    // maximum yet. Otherwise the tile costs one exp per score and no max reduction.
-    // The row sum adds the 16-bit P values the PV product uses (v_dot2 against ones).
-    uint4 pb[4];
-    float lsum;
-    auto weights = [&](float delta) __attribute__((always_inline)) {
+  };
+
+  // Softmax weights of one tile for query l32 (FlashAttention-2 online softmax, Dao 2023) with a
+  // lazily raised maximum: p = 2^(s * scale * log2 e - m_used), packed to 16 bits for the PV
+  // product; the row sum adds the 16-bit values the PV product uses (v_dot2 against ones).
+  // Slice e (of 16) computes the two scores 2e, 2e+1 (score k of the lane is s[k/16][k%16]).
+  uint4 pb[4];
+  float la = 0.f, lb = 0.f;
+  auto weights_slice = [&](const pf_f32x16 (&s)[2], int e, float off) __attribute__((always_inline)) {
+    const int k0 = 2 * e;
+    const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[k0 >> 4][k0 & 15], c2, -off));
+    const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[(k0 + 1) >> 4][(k0 + 1) & 15], c2, -off));
+    const uint32_t w = M::pack(p0, p1);
+    const int ks = k0 >> 3, c = (k0 >> 1) & 3;  // pb[ks] word c holds scores 8ks + 2c, +1
+    if (c == 0) pb[ks].x = w;
+    else if (c == 1) pb[ks].y = w;
+    else if (c == 2) pb[ks].z = w;
+    else pb[ks].w = w;
+    if (ks < 2) la = M::sum2(w, la);
+    else lb = M::sum2(w, lb);
+  };
+  auto weights_all = [&](const pf_f32x16 (&s)[2], float off) __attribute__((always_inline)) {
+    la = 0.f;
+    lb = 0.f;
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        float p[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e)
-          p[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[ks >> 1][(ks & 1) * 8 + e], c2, -delta));
-        pb[ks] = make_uint4(M::pack(p[0], p[1]), M::pack(p[2], p[3]), M::pack(p[4], p[5]),
-                            M::pack(p[6], p[7]));
-      }
-      float la = 0.f, lb = 0.f;  // two independent dot2 chains
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        la = M::sum2(pb[ks].w, M::sum2(pb[ks].z, M::sum2(pb[ks].y, M::sum2(pb[ks].x, la))));
-        lb = M::sum2(pb[ks + 2].w,
-                     M::sum2(pb[ks + 2].z, M::sum2(pb[ks + 2].y, M::sum2(pb[ks + 2].x, lb))));
-      }
-      lsum = la + lb;
-    };
-    weights(0.f);
-    constexpr float kLazyBound = 4096.f;  // 2^kLazy, kLazy = 12
+    for (int e = 0; e < 16; ++e) weights_slice(s, e, off);
+  };
+  constexpr float kLazyBound = 4096.f;  // 2^kLazy, kLazy = 12
+  // After the weights of a tile: raise the maximum when this lane's weights of the tile sum past
+  // 2^kLazy (so every weight that enters the accumulators is <= 2^kLazy) or while the query has
+  // no maximum yet; the weights are then recomputed against the exact new maximum, so the largest
+  // weight of a row never underflows whatever the score range.
+  auto finish_weights = [&](const pf_f32x16 (&s)[2]) __attribute__((always_inline)) {
+    float lsum = la + lb;
     if (__any(lsum > kLazyBound || m_run == -INFINITY)) {
-      // Exact maximum of the tile for this query (both halves of the wave), then the new
-      // offset; the weights are recomputed against it and the running state rescaled.
       float mq[4];
 #pragma unroll
       for (int k = 0; k < 4; ++k) {  // four independent max3 chains over 8 scores each
@@ -436,88 +445,127 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PrefillArgs a) {
       float mx = __builtin_fmaxf(max3f(mq[0], mq[1], mq[2]), mq[3]);
       float x0, x1;
       swap_halves(mx, x0, x1);
-      const float m_new = __builtin_fmaxf(m_run, __builtin_fmaf(__builtin_fmaxf(x0, x1), c2, m_used));
+      const float m_new = __builtin_fmaxf(m_run, __builtin_fmaxf(x0, x1) * c2);
       const float used_new = (m_new == -INFINITY) ? 0.f : m_new;
       const float alpha = __builtin_amdgcn_exp2f(m_run - used_new);  // 0 while m_run = -inf
-      weights(used_new - m_used);
+      weights_all(s, used_new);
+      lsum = la + lb;
       m_run = m_new;
       m_used = used_new;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) minit[r] = -used_new * inv_c2;
       l_run *= alpha;
 #pragma unroll
       for (int db = 0; db < DB; ++db) acc[db] *= alpha;
     }
     l_run += lsum;
-    // O^T += V^T P^T: K-step ks covers tile tokens 16ks .. 16ks+15 in the S^T order. The V^T
-    // operand (ks, db) is rows 16ks + rl (+ 8), chunk 4db + chl: (v_lane0 ^ 64db) + 16ks RB
-    // (v_lane1 for the second row group), read AH operands ahead.
-    {
-      int vb0 = v_lane0, vb1 = v_lane1;
-      asm volatile("" : "+v"(vb0), "+v"(vb1));
-      auto read_v = [&](int ks, int db) __attribute__((always_inline)) {
-        const char* a0 = vl + 16 * ks * RB + (vb0 ^ (64 * db));
-        const char* a1 = vl + 16 * ks * RB + (vb1 ^ (64 * db));
-        const pf_s16x4 v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(a0));
-        const pf_s16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(a1));
-        return __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7);
-      };
-      constexpr int NV = 4 * DB, AH = 4;
-      pf_s16x8 vop[AH];
+  };
+
+  // PV product O^T += V^T P^T of the tile in LDS buffer vb: K-step ks covers tile tokens
+  // 16ks .. 16ks+15 in the S^T order. The V^T operand (ks, db) is rows 16ks + rl (+ 8), chunk
+  // 4db + chl: (v_lane0 ^ 64db) + 16ks RB (v_lane1 for the second row group), read AH ahead.
+  auto pv = [&](const char* vb) __attribute__((always_inline)) {
+    int vb0 = v_lane0, vb1 = v_lane1;
+    asm volatile("" : "+v"(vb0), "+v"(vb1));
+    auto read_v = [&](int ks, int db) __attribute__((always_inline)) {
+      const char* a0 = vb + 16 * ks * RB + (vb0 ^ (64 * db));
+      const char* a1 = vb + 16 * ks * RB + (vb1 ^ (64 * db));
+      const pf_s16x4 v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(a0));
+      const pf_s16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(a1));
+      return __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7);
+    };
+    constexpr int NV = 4 * DB, AH = 4;
+    pf_s16x8 vop[AH];
 #pragma unroll
-      for (int i = 0; i < AH; ++i) vop[i] = read_v(i / DB, i % DB);
+    for (int i = 0; i < AH; ++i) vop[i] = read_v(i / DB, i % DB);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const pf_s16x8 cur = vop[i % AH];
+      if (i + AH < NV) vop[i % AH] = read_v((i + AH) / DB, (i + AH) % DB);
+      acc[i % DB] = M::mma(cur, pb[i / DB], acc[i % DB]);
       __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int i = 0; i < NV; ++i) {
-        const pf_s16x8 cur = vop[i % AH];
-        if (i + AH < NV) vop[i % AH] = read_v((i + AH) / DB, (i + AH) % DB);
-        acc[i % DB] = M::mma(cur, pb[i / DB], acc[i % DB]);
-        __builtin_amdgcn_sched_barrier(0);
-      }
     }
   };
 
   // wave-uniform: does this wave see any key of the tile
   auto visits = [&](int t0) __attribute__((always_inline)) {
-    bool v = wave_active;
+    bool v = wave_active && t0 < kv_end;
     if (a.causal != SP_CAUSAL_NONE) v = v && t0 <= wq_hi + pos_off;
     if (a.window_left >= 0) v = v && t0 + BN - 1 >= wq_lo + pos_off - a.window_left;
     return v;
   };
 
-  // One pipeline step: wait for this tile's rows (own loads, then everyone's), start the next
-  // tile's loads into the other buffer, compute on this one. The barrier also guarantees every
-  // wave is done reading `nxt` (its previous tile) before the loads overwrite it.
-  auto step = [&](int t0, char* cur, char* nxt) __attribute__((always_inline)) {
+  // One pipeline step on tile t0 (its K in kcur's tile one step ago, now its S^T in sc; its V
+  // in vcur): wait until this step's tiles are in (own loads, then everyone's), start the loads
+  // that run ahead (K of t0 + 2 BN into kload, V of t0 + BN into vload; the barrier also
+  // guarantees every wave is done reading both buffers), then the QK product of the next tile
+  // (K in knext, S^T into sn) with this tile's softmax interleaved, and this tile's PV product.
+  auto step = [&](int t0, pf_f32x16 (&sc)[2], pf_f32x16 (&sn)[2], const char* knext,
+                  const char* vcur, char* kload, char* vload) __attribute__((always_inline)) {
     __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
     __syncthreads();
-    if (t0 + BN < kv_end) {
-      issue_tile(t0 + BN, nxt);
-      fetch_blocks(t0 + 2 * BN);
+    {
+      const int lt = t0 + lead * BN;
+      if (lt < kv_end) {
+        issue_tile(lt, v_wave ? vload : kload);
+        fetch_blocks(lt + BN);
+      }
     }
-    if (visits(t0)) {
-      compute_tile(t0, cur);
+    const bool vis_c = visits(t0), vis_n = visits(t0 + BN);
+    if (vis_c) {
+      apply_mask(t0, sc);
+      la = 0.f;
+      lb = 0.f;
+      // The offset goes through an empty asm in each branch so that the compiler cannot hoist
+      // the (identical) weight computations of both branches above them, which would take the
+      // exponentials out of the MFMA slots they are meant to fill.
+      float off = m_used;
+      if (vis_n) {
+        asm volatile("" : "+v"(off));
+        // 16 weight slices over the NK MFMAs of the QK product (NK = 16 at D = 128, 8 at D = 64)
+        qk(knext, sn, [&](int i) __attribute__((always_inline)) {
+#pragma unroll
+          for (int e = i * 16 / NK; e < (i + 1) * 16 / NK; ++e) weights_slice(sc, e, off);
+        });
+      } else {
+        asm volatile("" : "+v"(off));
+#pragma unroll
+        for (int e = 0; e < 16; ++e) weights_slice(sc, e, off);
+      }
+      finish_weights(sc);
+      pv(vcur);
+    } else if (vis_n) {
+      qk(knext, sn, [](int) {});
     }
   };
 
-  // Prologue: the first tile's loads go out while the Q loads are still in flight. The wait
-  // below covers both, so no wait inside the key loop refers to Q (the tile loads issued there
-  // are awaited explicitly).
+  // Prologue: K of the first two tiles and V of the first go out while the Q loads are still in
+  // flight; the wait below covers both, so no wait inside the key loop refers to Q (the tile
+  // loads issued there are awaited explicitly). Then the first tile's QK product.
+  pf_f32x16 sa[2], sb[2];
   int t0 = t_first;
   if (t0 < kv_end) {
-    if constexpr (PAGED) {
-      fetch_blocks(t0);
-      __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+    fetch_blocks(t0);
+    if (v_wave) {
+      issue_tile(t0, vl[0]);
+      fetch_blocks(t0 + BN);
+    } else {
+      issue_tile(t0, kl[0]);
+      fetch_blocks(t0 + BN);
+      if (t0 + BN < kv_end) {
+        issue_tile(t0 + BN, kl[1]);
+        fetch_blocks(t0 + 2 * BN);
+      }
     }
-    issue_tile(t0, lds0);
-    fetch_blocks(t0 + BN);
   }
   __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+  __syncthreads();
+  if (visits(t0)) qk(kl[0], sa, [](int) {});
+  // the loop's first barrier has nothing to wait for but keeps the step uniform
   while (t0 < kv_end) {
-    step(t0, lds0, lds1);
+    step(t0, sa, sb, kl[1], vl[0], kl[0], vl[1]);
     t0 += BN;
     if (t0 >= kv_end) break;
-    step(t0, lds1, lds0);
+    step(t0, sb, sa, kl[0], vl[1], kl[1], vl[0]);
     t0 += BN;
   }
 
