@@ -252,10 +252,35 @@ int sp_paged_prefill(void* out, const void* q,
                      void* workspace, size_t workspace_bytes, void* stream);
 
 /*
- * Dense attention on [batch, heads, seq, head_dim] tensors: flash_attention(q, k, v,
- * FlashAttentionOptions{causal}) (sketchpad-cubecl attention.rs:97-178). Equal head counts for
- * q and k/v (the reference has no GQA there). causal uses the reference's test-oracle mask
- * j > i (top-left, correctness_cpu.rs:1066-1074). The reference scales by head_dim^-0.5.
+ * Dense attention on [batch, heads, seq, dim] tensors with every option of the reference's
+ * flash_attention_impl (sketchpad-cubecl attention.rs:130-178; FlashAttentionOptions
+ * :39-69): q, k [batch, heads, seq_q / seq_k, head_dim], v [batch, heads, seq_k, v_head_dim],
+ * out [batch, heads, seq_q, v_head_dim] of out_dtype (FlashAttentionOptions.out_dtype; the
+ * reference defaults it to q's dtype), out = softmax(q k^T scale + mask) v with fp32 softmax and
+ * accumulation. Equal head counts for q and k/v (the reference has no GQA there). causal != 0
+ * masks key j > query i (the reference's test oracle, correctness_cpu.rs:1066-1074, top-left).
+ *   mask : optional additive f32 mask (NULL: none; flash_attention_masked's argument),
+ *          element (b, h, i, j) at b*mask_stride_b + h*mask_stride_h + i*mask_stride_q + j
+ *          (stride 0 broadcasts, as the reference's tests expand one [seq_q, seq_k] mask).
+ *          Masked entries are -inf or large negatives; a query whose every key is masked gets
+ *          zeros.
+ * f32 tensors (the element type the reference's flash_attention runs, attention.rs:21-25):
+ * head_dim 40, 64, 80, 128, 160 or 256 (so the SD-1.x UNet's head dims 40 / 80 / 160 run
+ * without padding, sketchpad-unet/src/cubecl.rs:256-316), v_head_dim a multiple of 4 up to
+ * 256. bf16 / f16 tensors: head_dim == v_head_dim, 64 or 128. out_dtype any of f32 / bf16 / f16.
+ * The reference scales by head_dim^-0.5.
+ */
+int sp_flash_attention_ex(void* out, const void* q, const void* k, const void* v,
+                          const float* mask, int64_t mask_stride_b, int64_t mask_stride_h,
+                          int64_t mask_stride_q, int32_t batch, int32_t num_heads,
+                          int32_t seq_q, int32_t seq_k, int32_t head_dim, int32_t v_head_dim,
+                          float scale, int32_t causal, sp_dtype dtype, sp_dtype out_dtype,
+                          void* stream);
+
+/*
+ * flash_attention(q, k, v, FlashAttentionOptions{causal}) (sketchpad-cubecl
+ * attention.rs:97-104): sp_flash_attention_ex with no mask, v_head_dim = head_dim and out of
+ * q's dtype.
  */
 int sp_flash_attention(void* out, const void* q, const void* k, const void* v,
                        int32_t batch, int32_t num_heads, int32_t seq_q, int32_t seq_k,
@@ -263,13 +288,9 @@ int sp_flash_attention(void* out, const void* q, const void* k, const void* v,
                        void* stream);
 
 /*
- * flash_attention_masked (sketchpad-cubecl attention.rs:119-128): sp_flash_attention plus an
- * additive mask, out = softmax(q k^T scale + mask) v, f32 tensors (the element type the
- * reference's flash_attention runs; 16-bit inputs return SP_EUNSUPPORTED). mask is f32
- * [batch, heads, seq_q, seq_k] addressed as b*mask_stride_b + h*mask_stride_h + i*mask_stride_q
- * + j elements: stride 0 broadcasts (the reference's tests expand one [seq_q, seq_k] mask).
- * Masked entries are -inf or large negatives; causal != 0 also applies the j > i mask. A query
- * whose every key is masked gets zeros.
+ * flash_attention_masked (sketchpad-cubecl attention.rs:119-128): sp_flash_attention_ex with a
+ * required mask, v_head_dim = head_dim and out of q's dtype. mask is f32 for every dtype of
+ * q / k / v; causal != 0 also applies the j > i mask.
  */
 int sp_flash_attention_masked(void* out, const void* q, const void* k, const void* v,
                               const float* mask, int64_t mask_stride_b, int64_t mask_stride_h,

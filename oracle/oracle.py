@@ -52,6 +52,10 @@ _SIG = {
     "spo_prefill_causal_mask": (None, [c_int64, c_int64, c_void_p]),
     "spo_sliding_window_mask": (None, [c_int64, c_int64, c_void_p]),
     "spo_sliding_window_prefill_mask": (None, [c_int64, c_int64, c_int64, c_void_p]),
+    "spo_attention_f64_v": (None, [c_void_p, c_int64, c_int64, c_void_p, c_int64, c_int64,
+                                   c_void_p, c_int64, c_int64, c_int32, c_int64, c_int64, c_int32,
+                                   c_int32, c_int32, c_double, c_void_p, c_int32, c_int64,
+                                   c_int64, c_int32, c_void_p]),
     "spo_attention_f64": (None, [c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_int64,
                                  c_int64, c_int64, c_int64, c_int, c_int, c_int, c_double,
                                  c_void_p, c_int, c_int64, c_int64, c_int, c_void_p]),
@@ -190,15 +194,24 @@ def sliding_window_prefill_mask(new_len: int, total_len: int, window: int) -> np
 
 def attention_f64(q, k, v, *, scale: float, mask=None, causal: bool = False, q_pos0: int = 0,
                   window_left: int = -1, dtype: int | None = None) -> np.ndarray:
-    """q [Sq, Hq, D], k/v [Lk, Hkv, D] (float32, or uint16 bf16 bits) -> float64 [Sq, Hq, D]."""
+    """q [Sq, Hq, D], k [Lk, Hkv, D], v [Lk, Hkv, Dv] (float32, or uint16 bf16 bits) ->
+    float64 [Sq, Hq, Dv]. mask: additive [Sq, Lk] (replaces the causal / window predicate)."""
     q, k, v = _c(q), _c(k), _c(v)
     dt = _dtype_code(q, dtype)
     sq, hq, d = q.shape
     lk, hkv, _ = k.shape
-    out = np.empty((sq, hq, d), dtype=np.float64)
+    dv = v.shape[2]
+    if dv == d:
+        out = np.empty((sq, hq, d), dtype=np.float64)
+        m = None if mask is None else _c(mask, np.float32)
+        lib().spo_attention_f64(_p(q), hq * d, d, _p(k), _p(v), hkv * d, d, sq, lk, hq, hkv, d,
+                                scale, _p(m), int(causal), q_pos0, window_left, dt, _p(out))
+        return out
+    out = np.empty((sq, hq, dv), dtype=np.float64)
     m = None if mask is None else _c(mask, np.float32)
-    lib().spo_attention_f64(_p(q), hq * d, d, _p(k), _p(v), hkv * d, d, sq, lk, hq, hkv, d,
-                            scale, _p(m), int(causal), q_pos0, window_left, dt, _p(out))
+    lib().spo_attention_f64_v(_p(q), hq * d, d, _p(k), hkv * d, d, _p(v), hkv * dv, dv, dv, sq,
+                              lk, hq, hkv, d, scale, _p(m), int(causal), q_pos0, window_left, dt,
+                              _p(out))
     return out
 
 

@@ -205,6 +205,15 @@ void spo_attention_f64(const void* q, int64_t q_tok, int64_t q_head, const void*
                        const void* v, int64_t kv_tok, int64_t kv_head, int64_t sq, int64_t lk,
                        int hq, int hkv, int d, double scale, const float* mask, int causal,
                        int64_t q_pos0, int64_t window_left, int dtype, double* out) {
+  spo_attention_f64_v(q, q_tok, q_head, k, kv_tok, kv_head, v, kv_tok, kv_head, d, sq, lk, hq,
+                      hkv, d, scale, mask, causal, q_pos0, window_left, dtype, out);
+}
+
+void spo_attention_f64_v(const void* q, int64_t q_tok, int64_t q_head, const void* k,
+                         int64_t k_tok, int64_t k_head, const void* v, int64_t v_tok,
+                         int64_t v_head, int dv, int64_t sq, int64_t lk, int hq, int hkv, int d,
+                         double scale, const float* mask, int causal, int64_t q_pos0,
+                         int64_t window_left, int dtype, double* out) {
   const int rep = hq / hkv; /* repeat_kv: head h reads KV head h / rep (transformer.rs:263-270) */
   double* s = (double*)malloc(sizeof(double) * (size_t)(lk > 0 ? lk : 1));
   for (int h = 0; h < hq; ++h) {
@@ -215,7 +224,7 @@ void spo_attention_f64(const void* q, int64_t q_tok, int64_t q_head, const void*
         double acc = 0.0;
         for (int c = 0; c < d; ++c)
           acc += (double)load_elem(q, i * q_tok + h * q_head + c, dtype) *
-                 (double)load_elem(k, j * kv_tok + g * kv_head + c, dtype);
+                 (double)load_elem(k, j * k_tok + g * k_head + c, dtype);
         acc *= scale; /* scale after the product (transformer.rs:234-235) */
         if (mask)
           acc += (double)mask[i * lk + j];
@@ -224,8 +233,8 @@ void spo_attention_f64(const void* q, int64_t q_tok, int64_t q_head, const void*
         s[j] = acc;
         if (acc > m) m = acc;
       }
-      double* o = out + (i * hq + h) * d;
-      for (int c = 0; c < d; ++c) o[c] = 0.0;
+      double* o = out + (i * hq + h) * dv;
+      for (int c = 0; c < dv; ++c) o[c] = 0.0;
       if (m == -INFINITY) continue; /* no visible key (or no keys): zeros */
       double sum = 0.0;
       for (int64_t j = 0; j < lk; ++j) {
@@ -235,7 +244,8 @@ void spo_attention_f64(const void* q, int64_t q_tok, int64_t q_head, const void*
       for (int64_t j = 0; j < lk; ++j) {
         if (s[j] == 0.0) continue;
         const double pj = s[j] / sum;
-        for (int c = 0; c < d; ++c) o[c] += pj * (double)load_elem(v, j * kv_tok + g * kv_head + c, dtype);
+        for (int c = 0; c < dv; ++c)
+          o[c] += pj * (double)load_elem(v, j * v_tok + g * v_head + c, dtype);
       }
     }
   }

@@ -109,6 +109,13 @@ void spo_attention_f64(const void* q, int64_t q_tok, int64_t q_head, const void*
                        const void* v, int64_t kv_tok, int64_t kv_head, int64_t sq, int64_t lk,
                        int hq, int hkv, int d, double scale, const float* mask, int causal,
                        int64_t q_pos0, int64_t window_left, int dtype, double* out);
+/* spo_attention_f64 with V of its own head dim dv and strides (out [sq][hq][dv]): the value
+ * head dim of flash_attention (sketchpad-cubecl attention.rs:135-143). */
+void spo_attention_f64_v(const void* q, int64_t q_tok, int64_t q_head, const void* k,
+                         int64_t k_tok, int64_t k_head, const void* v, int64_t v_tok,
+                         int64_t v_head, int dv, int64_t sq, int64_t lk, int hq, int hkv, int d,
+                         double scale, const float* mask, int causal, int64_t q_pos0,
+                         int64_t window_left, int dtype, double* out);
 void spo_attention_f32_refops(const void* q, int64_t q_tok, int64_t q_head, const void* k,
                               const void* v, int64_t kv_tok, int64_t kv_head, int64_t sq,
                               int64_t lk, int hq, int hkv, int d, float scale, const float* mask,

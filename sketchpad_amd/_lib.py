@@ -88,6 +88,10 @@ _SIGNATURES = {
     "sp_flash_attention": (c_int32, [c_void_p, c_void_p, c_void_p, c_void_p, c_int32, c_int32,
                                      c_int32, c_int32, c_int32, c_float, c_int32, c_int32,
                                      c_void_p]),
+    "sp_flash_attention_ex": (c_int32, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+                                        c_int64, c_int64, c_int64, c_int32, c_int32, c_int32,
+                                        c_int32, c_int32, c_int32, c_float, c_int32, c_int32,
+                                        c_int32, c_void_p]),
     "sp_qjl_record_bytes": (c_int64, [c_int32]),
     "sp_qjl_projection": (c_int32, [c_void_p, c_int32, c_int32]),
     "sp_qjl_compress": (c_int32, [c_void_p, c_void_p, c_int64, c_int32, c_void_p, c_int32,
@@ -330,6 +334,24 @@ def flash_attention(out, q, k, v, scale: float, *, causal: bool = False, stream=
     b, h, sq, d = q.shape
     check(load().sp_flash_attention(_ptr(out), _ptr(q), _ptr(k), _ptr(v), b, h, sq, k.shape[2],
                                     d, scale, int(bool(causal)), sp_dtype(q), _stream(stream)))
+
+
+def flash_attention_ex(out, q, k, v, scale: float, *, mask=None, causal: bool = False,
+                       stream=None) -> None:
+    """sp_flash_attention_ex: q, k [B, H, S, D], v [B, H, Sk, Dv], out [B, H, Sq, Dv] of any
+    supported dtype (FlashAttentionOptions.out_dtype), optional f32 additive mask that expands to
+    [B, H, Sq, Sk] (last stride 1)."""
+    b, h, sq, d = q.shape
+    sk, dv = v.shape[2], v.shape[3]
+    mp, ms = None, (0, 0, 0)
+    if mask is not None:
+        m = mask.expand(b, h, sq, sk)
+        if sk > 1 and m.stride(3) != 1:
+            raise ValueError("mask: the key dimension must be contiguous")
+        mp, ms = _ptr(m), (m.stride(0), m.stride(1), m.stride(2))
+    check(load().sp_flash_attention_ex(_ptr(out), _ptr(q), _ptr(k), _ptr(v), mp, *ms, b, h, sq,
+                                       sk, d, dv, scale, int(bool(causal)), sp_dtype(q),
+                                       sp_dtype(out), _stream(stream)))
 
 
 # ---------------------------------------------------------------------------------------------

@@ -321,17 +321,32 @@ int sp_paged_decode_noalloc(void* out, const void* q, const void* k_pool, const 
                          window_left, dtype, ws, need > 0 ? kDecodeScratchBytes : 0, stream);
 }
 
+// dense_f32: the dense f32 path (flash_attention), which also takes head dims 40, 80, 160 and
+// 256 and a value head dim of its own; everything else runs head_dim 64 or 128, Dv == D.
 static int check_prefill_common(const char* fn, int32_t num_seqs, int32_t max_seqlen_q,
                                 int32_t hq, int32_t hkv, int32_t D, float scale,
-                                int32_t causal, int32_t window_left, sp_dtype dtype) {
+                                int32_t causal, int32_t window_left, sp_dtype dtype,
+                                int32_t Dv = -1, bool dense = false) {
   if (int rc = check_dtype(dtype, fn)) return rc;
   if (num_seqs < 0 || max_seqlen_q < 0 || hq <= 0 || hkv <= 0)
     return fail(SP_EINVAL, "%s: invalid sizes (num_seqs=%d max_seqlen_q=%d hq=%d hkv=%d)", fn,
                 num_seqs, max_seqlen_q, hq, hkv);
   if (hq % hkv != 0)
     return fail(SP_EINVAL, "%s: num_q_heads %d is not a multiple of num_kv_heads %d", fn, hq, hkv);
-  if (D != 64 && D != 128)
-    return fail(SP_EUNSUPPORTED, "%s: head_dim %d has no kernel (64, 128)", fn, D);
+  if (Dv < 0) Dv = D;
+  if (D <= 0 || Dv <= 0)
+    return fail(SP_EINVAL, "%s: head_dim %d / value head_dim %d must be positive", fn, D, Dv);
+  if (dense && dtype == SP_F32) {
+    if (!prefill_f32_supports(D, Dv, false))
+      return fail(SP_EUNSUPPORTED,
+                  "%s: f32 head_dim %d / value head_dim %d has no kernel (head_dim 40, 64, 80, "
+                  "128, 160 or 256; value head_dim a multiple of 4 up to 256)",
+                  fn, D, Dv);
+  } else if ((D != 64 && D != 128) || Dv != D) {
+    return fail(SP_EUNSUPPORTED,
+                "%s: head_dim %d / value head_dim %d has no %s kernel (64 or 128, equal)", fn, D,
+                Dv, dtype_name(dtype));
+  }
   if (causal < SP_CAUSAL_NONE || causal > SP_CAUSAL_TOP_LEFT)
     return fail(SP_EINVAL, "%s: unknown causal mode %d", fn, causal);
   if (window_left < -1) return fail(SP_EINVAL, "%s: window_left %d < -1", fn, window_left);
@@ -365,8 +380,10 @@ int sp_varlen_prefill(void* out, const void* q, const void* k, const void* v,
   a.v = v;
   a.q_tok = a.o_tok = (int64_t)num_q_heads * head_dim;
   a.q_head = a.o_head = head_dim;
-  a.kv_tok = (int64_t)num_kv_heads * head_dim;
-  a.kv_head = head_dim;
+  a.kv_tok = a.v_tok = (int64_t)num_kv_heads * head_dim;
+  a.kv_head = a.v_head = head_dim;
+  a.dv = head_dim;
+  a.out_dtype = dtype;
   a.cu_q = cu_seqlens_q;
   a.cu_k = cu_seqlens_k;
   a.num_seqs = num_seqs;
@@ -439,6 +456,8 @@ int sp_paged_prefill(void* out, const void* q, const void* k_pool, const void* v
   a.causal = SP_CAUSAL_BOTTOM_RIGHT;
   a.window_left = window_left;
   a.scale_log2 = scale * 1.4426950408889634f;
+  a.dv = D;
+  a.out_dtype = dtype;
   a.kpool = (const char*)k_pool;
   a.vpool = (const char*)v_pool;
   a.block_tables = block_tables;
@@ -462,27 +481,41 @@ static int flash_attention_impl(const char* fn, void* out, const void* q, const 
                                 const void* v, const float* mask, int64_t mask_stride_b,
                                 int64_t mask_stride_h, int64_t mask_stride_q, int32_t batch,
                                 int32_t num_heads, int32_t seq_q, int32_t seq_k, int32_t head_dim,
-                                float scale, int32_t causal, sp_dtype dtype, void* stream) {
+                                int32_t v_head_dim, float scale, int32_t causal, sp_dtype dtype,
+                                sp_dtype out_dtype, void* stream) {
   if (int rc = check_prefill_common(fn, batch, seq_q, num_heads, num_heads, head_dim, scale,
-                                    causal ? SP_CAUSAL_TOP_LEFT : SP_CAUSAL_NONE, -1, dtype))
+                                    causal ? SP_CAUSAL_TOP_LEFT : SP_CAUSAL_NONE, -1, dtype,
+                                    v_head_dim, true))
     return rc;
+  if (int rc = check_dtype(out_dtype, fn)) return rc;
   if (seq_k < 0) return fail(SP_EINVAL, "%s: seq_k %d < 0", fn, seq_k);
+  if (mask_stride_b < 0 || mask_stride_h < 0 || mask_stride_q < 0)
+    return fail(SP_EINVAL, "%s: negative mask stride", fn);
   if (batch == 0 || seq_q == 0) return SP_OK;
   if (!out || !q || !k || !v) return fail(SP_EINVAL, "%s: NULL pointer argument", fn);
   if (misaligned16(out) || misaligned16(q) || misaligned16(k) || misaligned16(v))
     return fail(SP_EINVAL, "%s: q, k, v and out must be 16-byte aligned", fn);
+  if (mask && ((uintptr_t)mask & 3)) return fail(SP_EINVAL, "%s: mask is not 4-byte aligned", fn);
   PrefillArgs a{};
   a.out = out;
   a.q = q;
   a.k = k;
   a.v = v;
-  // [B, H, S, D]: token stride D, head stride S*D, batch stride H*S*D
-  a.q_tok = a.o_tok = head_dim;
-  a.q_head = a.o_head = (int64_t)seq_q * head_dim;
-  a.q_batch = a.o_batch = (int64_t)num_heads * seq_q * head_dim;
+  // [B, H, S, D] (q, k) and [B, H, S, Dv] (v, out): token stride D or Dv, head stride S * that
+  a.q_tok = head_dim;
+  a.q_head = (int64_t)seq_q * head_dim;
+  a.q_batch = (int64_t)num_heads * seq_q * head_dim;
+  a.o_tok = v_head_dim;
+  a.o_head = (int64_t)seq_q * v_head_dim;
+  a.o_batch = (int64_t)num_heads * seq_q * v_head_dim;
   a.kv_tok = head_dim;
   a.kv_head = (int64_t)seq_k * head_dim;
   a.kv_batch = (int64_t)num_heads * seq_k * head_dim;
+  a.v_tok = v_head_dim;
+  a.v_head = (int64_t)seq_k * v_head_dim;
+  a.v_batch = (int64_t)num_heads * seq_k * v_head_dim;
+  a.dv = v_head_dim;
+  a.out_dtype = out_dtype;
   a.lq = seq_q;
   a.lk = seq_k;
   a.num_seqs = batch;
@@ -500,11 +533,22 @@ static int flash_attention_impl(const char* fn, void* out, const void* q, const 
   return launch_prefill(a, dtype, head_dim, false, (hipStream_t)stream);
 }
 
+int sp_flash_attention_ex(void* out, const void* q, const void* k, const void* v,
+                          const float* mask, int64_t mask_stride_b, int64_t mask_stride_h,
+                          int64_t mask_stride_q, int32_t batch, int32_t num_heads, int32_t seq_q,
+                          int32_t seq_k, int32_t head_dim, int32_t v_head_dim, float scale,
+                          int32_t causal, sp_dtype dtype, sp_dtype out_dtype, void* stream) {
+  return flash_attention_impl("sp_flash_attention_ex", out, q, k, v, mask, mask_stride_b,
+                              mask_stride_h, mask_stride_q, batch, num_heads, seq_q, seq_k,
+                              head_dim, v_head_dim, scale, causal, dtype, out_dtype, stream);
+}
+
 int sp_flash_attention(void* out, const void* q, const void* k, const void* v, int32_t batch,
                        int32_t num_heads, int32_t seq_q, int32_t seq_k, int32_t head_dim,
                        float scale, int32_t causal, sp_dtype dtype, void* stream) {
   return flash_attention_impl("sp_flash_attention", out, q, k, v, nullptr, 0, 0, 0, batch,
-                              num_heads, seq_q, seq_k, head_dim, scale, causal, dtype, stream);
+                              num_heads, seq_q, seq_k, head_dim, head_dim, scale, causal, dtype,
+                              dtype, stream);
 }
 
 int sp_flash_attention_masked(void* out, const void* q, const void* k, const void* v,
@@ -513,18 +557,11 @@ int sp_flash_attention_masked(void* out, const void* q, const void* k, const voi
                               int32_t seq_q, int32_t seq_k, int32_t head_dim, float scale,
                               int32_t causal, sp_dtype dtype, void* stream) {
   const char* fn = "sp_flash_attention_masked";
-  if (dtype != SP_F32)
-    return fail(dtype == SP_BF16 || dtype == SP_F16 ? SP_EUNSUPPORTED : SP_EINVAL,
-                "%s: the additive mask is supported for f32 tensors only (the reference's "
-                "flash_attention element type), got %s",
-                fn, dtype_name(dtype));
   if (!mask && batch > 0 && seq_q > 0 && seq_k > 0)
     return fail(SP_EINVAL, "%s: NULL mask", fn);
-  if (mask_stride_b < 0 || mask_stride_h < 0 || mask_stride_q < 0)
-    return fail(SP_EINVAL, "%s: negative mask stride", fn);
   return flash_attention_impl(fn, out, q, k, v, mask, mask_stride_b, mask_stride_h, mask_stride_q,
-                              batch, num_heads, seq_q, seq_k, head_dim, scale, causal, dtype,
-                              stream);
+                              batch, num_heads, seq_q, seq_k, head_dim, head_dim, scale, causal,
+                              dtype, dtype, stream);
 }
 
 // ---------------------------------------------------------------------------------------------

@@ -35,6 +35,8 @@
 
 #include <math.h>
 
+#include <type_traits>
+
 namespace sp {
 
 typedef __bf16 pf_bf16x8 __attribute__((ext_vector_type(8)));
@@ -187,7 +189,8 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PrefillArgs a) {
   const char* qbase = (const char*)a.q +
       ((a.cu_q ? (int64_t)q_begin * a.q_tok : (int64_t)seq * a.q_batch) + (int64_t)h * a.q_head) * 2;
   char* obase = (char*)a.out +
-      ((a.cu_q ? (int64_t)q_begin * a.o_tok : (int64_t)seq * a.o_batch) + (int64_t)h * a.o_head) * 2;
+      ((a.cu_q ? (int64_t)q_begin * a.o_tok : (int64_t)seq * a.o_batch) + (int64_t)h * a.o_head) *
+          dtype_size((sp_dtype)a.out_dtype);
   const char* kbase = nullptr;
   const char* vbase = nullptr;
   const int32_t* table = nullptr;
@@ -364,7 +367,24 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PrefillArgs a) {
 
   // Masks, only on tiles that cross the sequence end, the window edge, kv_lo or the causal
   // diagonal. Score (mb, r) of this lane is key t0 + 4hh + off, off = 32mb + 8(r/4) + r%4.
+  // this lane's row of the additive mask (dense path: the sequence index is the batch index)
+  const float* mrow = a.mask ? a.mask + (int64_t)seq * a.mask_b + (int64_t)h * a.mask_h +
+                                   (int64_t)min(my_q, qe - 1) * a.mask_q
+                             : nullptr;
   auto apply_mask = [&](int t0, pf_f32x16 (&s)[2]) __attribute__((always_inline)) {
+    if (mrow) {
+      // additive mask (flash_attention_masked): softmax(q.k scale + mask) = softmax over
+      // (q.k + mask / scale) scale. Keys past the sequence end read its last column; their
+      // scores are masked below (such tiles always take the mask).
+      const int jb = t0 + 4 * hh;
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int key = min(jb + 32 * mb + 8 * (r >> 2) + (r & 3), Lk - 1);
+          s[mb][r] += mrow[key] * a.inv_scale;
+        }
+    }
     if (t0 < mask_below || t0 > mask_above) {
       if (tri_ok && t0 >= mask_below && (t0 == diag0 || t0 + 32 == diag0)) {
         // 32-aligned causal diagonal: the diagonal block is the triangle 8(r/4) + r%4 <=
@@ -593,16 +613,24 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PrefillArgs a) {
     return;
   }
   const float inv = l > 0.f ? 1.f / l : 0.f;
-  char* op = obase + (int64_t)my_q * a.o_tok * 2;
+  constexpr int kSelf = std::is_same<T, bf16_t>::value ? SP_BF16 : SP_F16;  // out = in type
+  const int oes = dtype_size((sp_dtype)a.out_dtype);
+  char* op = obase + (int64_t)my_q * a.o_tok * oes;
 #pragma unroll
   for (int db = 0; db < DB; ++db)
 #pragma unroll
     for (int rg = 0; rg < 4; ++rg) {
       const int d0 = db * 32 + rg * 8 + hh * 4;
-      uint2 w;
-      w.x = M::pack(acc[db][rg * 4 + 0] * inv, acc[db][rg * 4 + 1] * inv);
-      w.y = M::pack(acc[db][rg * 4 + 2] * inv, acc[db][rg * 4 + 3] * inv);
-      *(uint2*)(op + d0 * 2) = w;
+      const float o0 = acc[db][rg * 4 + 0] * inv, o1 = acc[db][rg * 4 + 1] * inv;
+      const float o2 = acc[db][rg * 4 + 2] * inv, o3 = acc[db][rg * 4 + 3] * inv;
+      if (a.out_dtype == SP_F32) {
+        *(float4*)(op + d0 * 4) = make_float4(o0, o1, o2, o3);
+      } else if (a.out_dtype == kSelf) {
+        *(uint2*)(op + d0 * 2) = make_uint2(M::pack(o0, o1), M::pack(o2, o3));
+      } else {  // the other 16-bit type
+        using O = PrefillMfma<typename std::conditional<kSelf == SP_BF16, f16_t, bf16_t>::type>;
+        *(uint2*)(op + d0 * 2) = make_uint2(O::pack(o0, o1), O::pack(o2, o3));
+      }
     }
 }
 
@@ -697,8 +725,6 @@ int launch_prefill(const PrefillArgs& args, sp_dtype dtype, int head_dim, bool p
                    hipStream_t stream) {
   PrefillArgs a = args;
   if (a.nsplit < 1 || !a.partials) a.nsplit = 1;
-  if (a.mask && dtype != SP_F32)
-    return fail(SP_EUNSUPPORTED, "prefill: an additive mask needs f32 tensors");
   if (dtype == SP_F32) {
     a.nsplit = 1;  // the fp32 kernel walks every key tile itself (no split partials)
     return launch_prefill_f32(a, head_dim, paged, stream);

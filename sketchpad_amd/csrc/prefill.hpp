@@ -16,7 +16,10 @@ struct PrefillArgs {
   // element strides
   int64_t q_tok, q_head, q_batch;
   int64_t o_tok, o_head, o_batch;
-  int64_t kv_tok, kv_head, kv_batch;
+  int64_t kv_tok, kv_head, kv_batch;  // K (and V unless v_* differ)
+  int64_t v_tok, v_head, v_batch;     // V element strides
+  int dv;                             // value head dim (== head_dim except dense f32)
+  int out_dtype;                      // sp_dtype of out
   const int32_t* cu_q;  // [num_seqs + 1] token offsets, or nullptr for dense batches
   const int32_t* cu_k;  // [num_seqs + 1] key offsets (packed K/V), or nullptr
   int lq, lk;           // dense lengths (cu_q / cu_k == nullptr)
@@ -59,5 +62,8 @@ int launch_prefill(const PrefillArgs& a, sp_dtype dtype, int head_dim, bool page
                    hipStream_t stream);
 // fp32 tensors (prefill_f32.hip); called by launch_prefill for SP_F32.
 int launch_prefill_f32(const PrefillArgs& a, int head_dim, bool paged, hipStream_t stream);
+// Head dims the fp32 kernel covers: dense K/V any of 40, 64, 80, 128, 160, 256 with a value head
+// dim <= 256 (a multiple of 4); paged / packed K/V 64 or 128 with equal value head dim.
+bool prefill_f32_supports(int head_dim, int v_head_dim, bool paged);
 
 }  // namespace sp

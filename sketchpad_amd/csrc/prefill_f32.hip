@@ -32,18 +32,20 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kF32BN = 32;  // keys per tile
 
-template <int D>
+template <int D, int DB>
 struct F32Cfg {
   // LDS row pitches in floats: K rows are read 16 bytes per lane down a column (pitch = 4 mod 64
-  // banks spreads 16 lanes over all banks), V rows by two lane halves four rows apart (4 pitch =
-  // 32 mod 64 puts the halves on disjoint banks).
+  // banks spreads 16 lanes over all banks at D = 64 / 128), V rows by two lane halves four rows
+  // apart (4 pitch = 32 mod 64 puts the halves on disjoint banks). V rows hold DB * 32 columns:
+  // the PV product works in 32-column blocks, and columns past the value head dim only feed
+  // output columns that are never stored.
   static constexpr int PITCH_K = D + 4;
-  static constexpr int PITCH_V = D + 8;
+  static constexpr int PITCH_V = DB * 32 + 8;
   static constexpr int TILE_K = kF32BN * PITCH_K;
   static constexpr int BUF = TILE_K + kF32BN * PITCH_V;  // K tile then V tile
-  static constexpr int CPR = D / 4;              // float4 chunks per row
-  static constexpr int LOADS = kF32BN * CPR / 256;  // float4 loads per thread per K (or V) tile
-  static constexpr int DB = D / 32;              // PV output blocks
+  static constexpr int CPR = D / 4;                 // float4 chunks per K row
+  static constexpr int LOADS_K = (kF32BN * CPR + 255) / 256;       // per thread per K tile
+  static constexpr int LOADS_V = (kF32BN * DB * 8 + 255) / 256;    // at most, per V tile
 };
 
 __device__ __forceinline__ f32x16 mfma_f32(float a, float b, f32x16 c) {
@@ -57,14 +59,16 @@ __device__ __forceinline__ void swap_halves_f32(float x, float& a, float& b) {
   b = __uint_as_float(r[1]);
 }
 
-template <int D, bool PAGED>
-__global__ void __launch_bounds__(256, 2) prefill_f32_kernel(PrefillArgs a) {
-  using C = F32Cfg<D>;
-  constexpr int BN = kF32BN, CPR = C::CPR, LOADS = C::LOADS, DB = C::DB;
+template <int D, int DB, bool PAGED>
+__global__ void __launch_bounds__(256, (DB >= 8 || D >= 256) ? 1 : 2) prefill_f32_kernel(PrefillArgs a) {
+  using C = F32Cfg<D, DB>;
+  constexpr int BN = kF32BN, CPR = C::CPR;
   constexpr int PITCH_K = C::PITCH_K, PITCH_V = C::PITCH_V;
-  constexpr int RB = D * 4;  // bytes per K/V row in memory
-  static_assert(C::LOADS * 256 == kF32BN * C::CPR, "tile load split");
+  constexpr int RB = D * 4;  // bytes per K row in memory (paged pools: K and V rows alike)
+  static_assert(D % 8 == 0, "the QK steps split a row into two halves of float4 chunks");
   __shared__ __attribute__((aligned(16))) float lds[2][C::BUF];
+  const int dv = a.dv;           // value head dim (<= 32 DB, a multiple of 4)
+  const int cprv = dv / 4;       // float4 chunks per V row
 
   // ---- workgroup -> (kv head, group member, sequence, query block), heavy query blocks first
   int id = blockIdx.x;
@@ -103,8 +107,10 @@ __global__ void __launch_bounds__(256, 2) prefill_f32_kernel(PrefillArgs a) {
   // ---- per-sequence base addresses (elements are 4 bytes)
   const char* qbase = (const char*)a.q +
       ((a.cu_q ? (int64_t)q_begin * a.q_tok : (int64_t)seq * a.q_batch) + (int64_t)h * a.q_head) * 4;
+  const int oes = dtype_size((sp_dtype)a.out_dtype);
   char* obase = (char*)a.out +
-      ((a.cu_q ? (int64_t)q_begin * a.o_tok : (int64_t)seq * a.o_batch) + (int64_t)h * a.o_head) * 4;
+      ((a.cu_q ? (int64_t)q_begin * a.o_tok : (int64_t)seq * a.o_batch) + (int64_t)h * a.o_head) *
+          oes;
   const char* kbase = nullptr;
   const char* vbase = nullptr;
   const int32_t* table = nullptr;
@@ -113,10 +119,12 @@ __global__ void __launch_bounds__(256, 2) prefill_f32_kernel(PrefillArgs a) {
     table = a.block_tables + (int64_t)seq * a.max_blocks_per_seq;
     head_off = a.layer_off_b + (int64_t)kvh * a.block_size * RB;
   } else {
-    const int64_t kv0 = (a.cu_k ? (int64_t)k_begin * a.kv_tok : (int64_t)seq * a.kv_batch) +
-                        (int64_t)kvh * a.kv_head;
-    kbase = (const char*)a.k + kv0 * 4;
-    vbase = (const char*)a.v + kv0 * 4;
+    kbase = (const char*)a.k +
+            ((a.cu_k ? (int64_t)k_begin * a.kv_tok : (int64_t)seq * a.kv_batch) +
+             (int64_t)kvh * a.kv_head) * 4;
+    vbase = (const char*)a.v +
+            ((a.cu_k ? (int64_t)k_begin * a.v_tok : (int64_t)seq * a.v_batch) +
+             (int64_t)kvh * a.v_head) * 4;
   }
 
   // ---- Q^T operand: query my_q, dims hh D/2 .. hh D/2 + D/2 - 1 (step s reads qreg[s])
@@ -145,24 +153,32 @@ __global__ void __launch_bounds__(256, 2) prefill_f32_kernel(PrefillArgs a) {
       return (is_v ? a.vpool : a.kpool) + (int64_t)blk * a.block_stride_b + head_off +
              (int64_t)(j % a.block_size) * RB;
     } else {
-      return (is_v ? vbase : kbase) + (int64_t)j * a.kv_tok * 4;
+      return is_v ? vbase + (int64_t)j * a.v_tok * 4 : kbase + (int64_t)j * a.kv_tok * 4;
     }
   };
-  float4 kreg[LOADS], vreg[LOADS];
+  float4 kreg[C::LOADS_K], vreg[C::LOADS_V];
   auto load_tile = [&](int t0) __attribute__((always_inline)) {
 #pragma unroll
-    for (int u = 0; u < LOADS; ++u) {
+    for (int u = 0; u < C::LOADS_K; ++u) {
       const int ch = tid + 256 * u, r = ch / CPR, c = ch % CPR;
-      kreg[u] = *(const float4*)(row_src(t0 + r, false) + c * 16);
-      vreg[u] = *(const float4*)(row_src(t0 + r, true) + c * 16);
+      if (ch < BN * CPR) kreg[u] = *(const float4*)(row_src(t0 + r, false) + c * 16);
+    }
+#pragma unroll
+    for (int u = 0; u < C::LOADS_V; ++u) {
+      const int ch = tid + 256 * u, r = ch / cprv, c = ch % cprv;
+      if (ch < BN * cprv) vreg[u] = *(const float4*)(row_src(t0 + r, true) + c * 16);
     }
   };
   auto store_tile = [&](float* buf) __attribute__((always_inline)) {
 #pragma unroll
-    for (int u = 0; u < LOADS; ++u) {
+    for (int u = 0; u < C::LOADS_K; ++u) {
       const int ch = tid + 256 * u, r = ch / CPR, c = ch % CPR;
-      *(float4*)(buf + r * PITCH_K + 4 * c) = kreg[u];
-      *(float4*)(buf + C::TILE_K + r * PITCH_V + 4 * c) = vreg[u];
+      if (ch < BN * CPR) *(float4*)(buf + r * PITCH_K + 4 * c) = kreg[u];
+    }
+#pragma unroll
+    for (int u = 0; u < C::LOADS_V; ++u) {
+      const int ch = tid + 256 * u, r = ch / cprv, c = ch % cprv;
+      if (ch < BN * cprv) *(float4*)(buf + C::TILE_K + r * PITCH_V + 4 * c) = vreg[u];
     }
   };
 
@@ -289,36 +305,87 @@ __global__ void __launch_bounds__(256, 2) prefill_f32_kernel(PrefillArgs a) {
   const float l = x0 + x1;
   if (my_q >= qe) return;
   const float inv = l > 0.f ? 1.f / l : 0.f;
-  float* op = (float*)(obase + (int64_t)my_q * a.o_tok * 4);
+  char* op = obase + (int64_t)my_q * a.o_tok * oes;
 #pragma unroll
   for (int db = 0; db < DB; ++db)
 #pragma unroll
-    for (int rg = 0; rg < 4; ++rg)
-      *(float4*)(op + db * 32 + rg * 8 + hh * 4) =
-          make_float4(acc[db][rg * 4] * inv, acc[db][rg * 4 + 1] * inv,
-                      acc[db][rg * 4 + 2] * inv, acc[db][rg * 4 + 3] * inv);
+    for (int rg = 0; rg < 4; ++rg) {
+      const int d0 = db * 32 + rg * 8 + hh * 4;  // four consecutive columns, all < dv or none
+      if (d0 >= dv) continue;
+      const float o0 = acc[db][rg * 4] * inv, o1 = acc[db][rg * 4 + 1] * inv;
+      const float o2 = acc[db][rg * 4 + 2] * inv, o3 = acc[db][rg * 4 + 3] * inv;
+      if (a.out_dtype == SP_F32) {
+        *(float4*)(op + d0 * 4) = make_float4(o0, o1, o2, o3);
+      } else if (a.out_dtype == SP_BF16) {
+        *(uint2*)(op + d0 * 2) =
+            make_uint2(f32_to_bf16_bits(o0) | ((uint32_t)f32_to_bf16_bits(o1) << 16),
+                       f32_to_bf16_bits(o2) | ((uint32_t)f32_to_bf16_bits(o3) << 16));
+      } else {
+        *(uint2*)(op + d0 * 2) =
+            make_uint2(f32_to_f16_bits(o0) | ((uint32_t)f32_to_f16_bits(o1) << 16),
+                       f32_to_f16_bits(o2) | ((uint32_t)f32_to_f16_bits(o3) << 16));
+      }
+    }
 }
 
-template <int D>
+template <int D, int DB>
 int launch_f32_d(const PrefillArgs& a, bool paged, hipStream_t stream) {
   const int64_t blocks = (int64_t)a.num_qblocks * a.num_seqs * a.hq;
   if (blocks <= 0) return SP_OK;
   if (blocks > 0x7fffffff) return fail(SP_EINVAL, "prefill: grid of %lld workgroups", (long long)blocks);
-  if (paged)
-    hipLaunchKernelGGL((prefill_f32_kernel<D, true>), dim3((unsigned)blocks), dim3(256), 0, stream, a);
-  else
-    hipLaunchKernelGGL((prefill_f32_kernel<D, false>), dim3((unsigned)blocks), dim3(256), 0, stream, a);
+  if (paged) {
+    // paged pools hold K and V rows of one head dim: only the matching instantiations exist
+    if constexpr ((D == 64 && DB == 2) || (D == 128 && DB == 4))
+      hipLaunchKernelGGL((prefill_f32_kernel<D, DB, true>), dim3((unsigned)blocks), dim3(256), 0,
+                         stream, a);
+    else
+      return fail(SP_EUNSUPPORTED, "prefill: paged f32 head_dim %d has no kernel", D);
+  } else {
+    hipLaunchKernelGGL((prefill_f32_kernel<D, DB, false>), dim3((unsigned)blocks), dim3(256), 0,
+                       stream, a);
+  }
   return check_launch("prefill_f32_kernel");
 }
 
 }  // namespace
 
+bool prefill_f32_supports(int head_dim, int v_head_dim, bool paged) {
+  if (paged) return (head_dim == 64 || head_dim == 128) && v_head_dim == head_dim;
+  const bool dk = head_dim == 40 || head_dim == 64 || head_dim == 80 || head_dim == 128 ||
+                  head_dim == 160 || head_dim == 256;
+  return dk && v_head_dim > 0 && v_head_dim % 4 == 0 && v_head_dim <= 256;
+}
+
 int launch_prefill_f32(const PrefillArgs& a, int head_dim, bool paged, hipStream_t stream) {
+  if (!prefill_f32_supports(head_dim, a.dv, paged))
+    return fail(SP_EUNSUPPORTED,
+                "prefill: f32 head_dim %d / value head_dim %d has no kernel (head_dim 40, 64, 80, "
+                "128, 160 or 256 with a value head_dim <= 256, a multiple of 4; paged and packed "
+                "K/V: 64 or 128 with equal value head_dim)",
+                head_dim, a.dv);
+  // V blocks of 32 columns: 2, 4 or 8 (value head dims up to 64, 128, 256)
+  const int db = a.dv <= 64 ? 2 : (a.dv <= 128 ? 4 : 8);
   switch (head_dim) {
-    case 64: return launch_f32_d<64>(a, paged, stream);
-    case 128: return launch_f32_d<128>(a, paged, stream);
-    default: return fail(SP_EUNSUPPORTED, "prefill: head_dim %d has no kernel (64, 128)", head_dim);
+    case 40: return db == 2 ? launch_f32_d<40, 2>(a, paged, stream)
+                   : db == 4 ? launch_f32_d<40, 4>(a, paged, stream)
+                             : launch_f32_d<40, 8>(a, paged, stream);
+    case 64: return db == 2 ? launch_f32_d<64, 2>(a, paged, stream)
+                   : db == 4 ? launch_f32_d<64, 4>(a, paged, stream)
+                             : launch_f32_d<64, 8>(a, paged, stream);
+    case 80: return db == 2 ? launch_f32_d<80, 2>(a, paged, stream)
+                   : db == 4 ? launch_f32_d<80, 4>(a, paged, stream)
+                             : launch_f32_d<80, 8>(a, paged, stream);
+    case 128: return db == 2 ? launch_f32_d<128, 2>(a, paged, stream)
+                    : db == 4 ? launch_f32_d<128, 4>(a, paged, stream)
+                              : launch_f32_d<128, 8>(a, paged, stream);
+    case 160: return db == 2 ? launch_f32_d<160, 2>(a, paged, stream)
+                    : db == 4 ? launch_f32_d<160, 4>(a, paged, stream)
+                              : launch_f32_d<160, 8>(a, paged, stream);
+    case 256: return db == 2 ? launch_f32_d<256, 2>(a, paged, stream)
+                    : db == 4 ? launch_f32_d<256, 4>(a, paged, stream)
+                              : launch_f32_d<256, 8>(a, paged, stream);
   }
+  return fail(SP_EUNSUPPORTED, "prefill: f32 head_dim %d has no kernel", head_dim);
 }
 
 }  // namespace sp

@@ -18,7 +18,7 @@ void set_error(const std::string& msg);
 int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
 int check_launch(const char* what);
 
-inline int dtype_size(sp_dtype dt) {
+__host__ __device__ inline int dtype_size(sp_dtype dt) {
   switch (dt) {
     case SP_F32: return 4;
     case SP_BF16: return 2;

@@ -334,88 +334,88 @@ std::vector<float> causal_mask(size_t seq_len) {
   return m;
 }
 
-// Shapes and dtypes flash_attention / flash_attention_masked accept; the message otherwise.
+DeviceTensor causal_mask_tensor(size_t seq_len) {
+  const std::vector<float> m = causal_mask(seq_len);
+  return DeviceTensor::from_host(m.data(), {(int64_t)seq_len, (int64_t)seq_len}, SP_F32);
+}
+
+// Shapes and dtypes flash_attention / flash_attention_masked accept; the message otherwise (the
+// kernels' own head-dim limits are reported by the library).
 static std::optional<std::string> flash_shape_error(const DeviceTensor& query,
                                                     const DeviceTensor& key,
-                                                    const DeviceTensor& value,
-                                                    const FlashAttentionOptions& options) {
+                                                    const DeviceTensor& value) {
   const auto& q = query.dims();
   const auto& k = key.dims();
   const auto& v = value.dims();
   if (q.size() != 4 || k.size() != 4 || v.size() != 4 || k[0] != q[0] || k[1] != q[1] ||
       k[3] != q[3] || v[0] != k[0] || v[1] != k[1] || v[2] != k[2])
     return std::string("flash_attention: expected q [B,H,Sq,D], k [B,H,Sk,D], v [B,H,Sk,Dv]");
-  if (v[3] != q[3]) return std::string("flash_attention: value head_dim must equal the query's");
-  if (key.dtype() != query.dtype() || value.dtype() != query.dtype() ||
-      options.out_dtype.value_or(query.dtype()) != query.dtype())
-    return std::string("flash_attention: mixed dtypes are not supported");
+  if (key.dtype() != query.dtype() || value.dtype() != query.dtype())
+    return std::string("flash_attention: q, k and v must share one dtype");
   return std::nullopt;
+}
+
+// flash_attention_impl (sketchpad-cubecl attention.rs:130-178): out [B, H, Sq, Dv] of
+// out_dtype (or q's), then the kernel; mask strides 0 broadcast one [Sq, Sk] mask.
+static FlashResult flash_impl(const DeviceTensor& query, const DeviceTensor& key,
+                              const DeviceTensor& value, const DeviceTensor* mask,
+                              const FlashAttentionOptions& options, hipStream_t stream) {
+  FlashResult r;
+  if (auto e = flash_shape_error(query, key, value)) {
+    r.error = AttentionSetupError{*e};
+    return r;
+  }
+  const auto& q = query.dims();
+  const auto& k = key.dims();
+  const auto& v = value.dims();
+  int64_t sb = 0, sh = 0, sq = 0;
+  if (mask) {
+    const auto& m = mask->dims();
+    if (mask->dtype() != SP_F32) {
+      r.error = AttentionSetupError{"flash_attention_masked: the mask must be f32"};
+      return r;
+    }
+    if (m.size() == 4 && m[0] == q[0] && m[1] == q[1] && m[2] == q[2] && m[3] == k[2]) {
+      sb = q[1] * q[2] * k[2];
+      sh = q[2] * k[2];
+    } else if (!(m.size() == 2 && m[0] == q[2] && m[1] == k[2])) {
+      r.error = AttentionSetupError{"flash_attention_masked: mask must be [B,H,Sq,Sk] or [Sq,Sk]"};
+      return r;
+    }
+    sq = k[2];
+  }
+  const sp_dtype out_dtype = options.out_dtype.value_or(query.dtype());
+  DeviceTensor out({q[0], q[1], q[2], v[3]}, out_dtype);
+  const int rc = sp_flash_attention_ex(
+      out.data(), query.data(), key.data(), value.data(),
+      mask ? (const float*)mask->data() : nullptr, sb, sh, sq, (int32_t)q[0], (int32_t)q[1],
+      (int32_t)q[2], (int32_t)k[2], (int32_t)q[3], (int32_t)v[3], (float)pow((double)q[3], -0.5),
+      options.causal ? 1 : 0, query.dtype(), out_dtype, stream);
+  if (rc != SP_OK) {
+    r.error = AttentionSetupError{sp_last_error()};
+    return r;
+  }
+  r.out = out;
+  return r;
 }
 
 FlashResult flash_attention(const DeviceTensor& query, const DeviceTensor& key,
                             const DeviceTensor& value, const FlashAttentionOptions& options,
                             hipStream_t stream) {
-  FlashResult r;
-  if (auto e = flash_shape_error(query, key, value, options)) {
-    r.error = AttentionSetupError{*e};
-    return r;
-  }
-  const auto& q = query.dims();
-  const auto& k = key.dims();
-  DeviceTensor out({q[0], q[1], q[2], q[3]}, query.dtype());
-  const int rc = sp_flash_attention(out.data(), query.data(), key.data(), value.data(),
-                                    (int32_t)q[0], (int32_t)q[1], (int32_t)q[2], (int32_t)k[2],
-                                    (int32_t)q[3], (float)pow((double)q[3], -0.5),
-                                    options.causal ? 1 : 0, query.dtype(), stream);
-  if (rc != SP_OK) {
-    r.error = AttentionSetupError{sp_last_error()};
-    return r;
-  }
-  r.out = out;
-  return r;
+  return flash_impl(query, key, value, nullptr, options, stream);
 }
 
 FlashResult flash_attention_masked(const DeviceTensor& query, const DeviceTensor& key,
                                    const DeviceTensor& value, const DeviceTensor& mask,
                                    const FlashAttentionOptions& options, hipStream_t stream) {
-  FlashResult r;
-  if (auto e = flash_shape_error(query, key, value, options)) {
-    r.error = AttentionSetupError{*e};
-    return r;
-  }
-  const auto& q = query.dims();
-  const auto& k = key.dims();
-  const auto& m = mask.dims();
-  int64_t sb = 0, sh = 0;
-  if (mask.dtype() != SP_F32) {
-    r.error = AttentionSetupError{"flash_attention_masked: the mask must be f32"};
-    return r;
-  }
-  if (m.size() == 4 && m[0] == q[0] && m[1] == q[1] && m[2] == q[2] && m[3] == k[2]) {
-    sb = q[1] * q[2] * k[2];
-    sh = q[2] * k[2];
-  } else if (!(m.size() == 2 && m[0] == q[2] && m[1] == k[2])) {
-    r.error = AttentionSetupError{"flash_attention_masked: mask must be [B,H,Sq,Sk] or [Sq,Sk]"};
-    return r;
-  }
-  DeviceTensor out({q[0], q[1], q[2], q[3]}, query.dtype());
-  const int rc = sp_flash_attention_masked(
-      out.data(), query.data(), key.data(), value.data(), (const float*)mask.data(), sb, sh,
-      k[2], (int32_t)q[0], (int32_t)q[1], (int32_t)q[2], (int32_t)k[2], (int32_t)q[3],
-      (float)pow((double)q[3], -0.5), options.causal ? 1 : 0, query.dtype(), stream);
-  if (rc != SP_OK) {
-    r.error = AttentionSetupError{sp_last_error()};
-    return r;
-  }
-  r.out = out;
-  return r;
+  return flash_impl(query, key, value, &mask, options, stream);
 }
 
 DeviceTensor qkv_attention(const DeviceTensor& q, const DeviceTensor& k, const DeviceTensor& v,
-                           MaskKind mask, hipStream_t stream) {
-  FlashAttentionOptions o;
-  o.causal = mask == MaskKind::Causal;
-  FlashResult r = flash_attention(q, k, v, o, stream);
+                           const std::optional<DeviceTensor>& mask, hipStream_t stream) {
+  if (mask && mask->dims().size() != 2)
+    throw std::runtime_error("qkv_attention: the mask must be [seq_q, seq_k]");
+  FlashResult r = flash_impl(q, k, v, mask ? &*mask : nullptr, FlashAttentionOptions(), stream);
   if (!r.is_ok()) throw std::runtime_error(r.error->message);
   return *r.out;
 }

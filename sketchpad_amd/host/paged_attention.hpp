@@ -294,19 +294,17 @@ class PagedAttentionCache : public AttentionCache {
 // attention.rs / sketchpad-cubecl attention.rs
 // ---------------------------------------------------------------------------------------------
 
-// The masks the reference builds as additive [seq_q, seq_k] tensors, by structure.
-enum class MaskKind {
-  None,    // no mask
-  Causal,  // causal_mask (attention.rs:33-42, transformer.rs:415-424): key j > query i masked
-};
-
 // causal_mask (attention.rs:33-42): host copy of the [seq_len, seq_len] additive mask.
 std::vector<float> causal_mask(size_t seq_len);
+// causal_mask as the reference returns it: an f32 device tensor [seq_len, seq_len].
+DeviceTensor causal_mask_tensor(size_t seq_len);
 
 // qkv_attention (attention.rs:4-27): softmax((q d^-1/4)(k d^-1/4)^T + mask) v on
-// [batch, heads, seq, head_dim] tensors, i.e. scale d^-1/2 on the product.
+// [batch, heads, seq, head_dim] tensors, i.e. scale d^-1/2 on the product; mask is the
+// reference's Option<Tensor<B, 2>>: an additive f32 [seq_q, seq_k] tensor added to every batch
+// and head (std::nullopt: none). Throws on shapes or dtypes the kernels do not cover.
 DeviceTensor qkv_attention(const DeviceTensor& q, const DeviceTensor& k, const DeviceTensor& v,
-                           MaskKind mask, hipStream_t stream = nullptr);
+                           const std::optional<DeviceTensor>& mask, hipStream_t stream = nullptr);
 
 // FlashAttentionOptions (sketchpad-cubecl attention.rs:39-69).
 struct FlashAttentionOptions {
@@ -334,9 +332,10 @@ struct AttentionSetupError {
   std::string message;
 };
 
-// flash_attention (sketchpad-cubecl attention.rs:97-104): [batch, heads, seq_q, head_dim] x
-// [batch, heads, seq_k, head_dim]; causal masks key j > query i. Errors (instead of launching)
-// on shapes or dtypes the kernels do not cover.
+// flash_attention (sketchpad-cubecl attention.rs:97-104): q, k [batch, heads, seq, head_dim],
+// v [batch, heads, seq_k, val_dim] -> out [batch, heads, seq_q, val_dim] of options.out_dtype
+// (q's dtype when unset); causal masks key j > query i. Errors (instead of launching) on shapes
+// or dtypes the kernels do not cover.
 struct FlashResult {
   std::optional<DeviceTensor> out;
   std::optional<AttentionSetupError> error;
@@ -348,7 +347,7 @@ FlashResult flash_attention(const DeviceTensor& query, const DeviceTensor& key,
 
 // flash_attention_masked (sketchpad-cubecl attention.rs:119-128): additive f32 mask,
 // [B, H, Sq, Sk] or one [Sq, Sk] mask for every batch and head (the reference's tests expand
-// one [Sq, Sk] mask); f32 tensors.
+// one [Sq, Sk] mask).
 FlashResult flash_attention_masked(const DeviceTensor& query, const DeviceTensor& key,
                                    const DeviceTensor& value, const DeviceTensor& mask,
                                    const FlashAttentionOptions& options,

@@ -267,11 +267,22 @@ TEST(test_flash_attention_causal_bf16, true) {
       worst = fmax(worst, fabs((double)f - ref[i]));
     }
     CHECK(worst <= 2e-2);
-    // qkv_attention with the causal mask is the same computation
-    auto o2 = qkv_attention(q, k, v, MaskKind::Causal);
+    // qkv_attention with the causal mask tensor (attention.rs:4-42) is the same computation,
+    // bit for bit: masked keys get zero weight either way
+    auto o2 = qkv_attention(q, k, v, causal_mask_tensor(S));
     std::vector<uint16_t> oh2(n);
     o2.to_host(oh2.data());
     CHECK(oh2 == oh);
+    // and without a mask it is the bidirectional flash_attention
+    auto o3 = qkv_attention(q, k, v, std::nullopt);
+    auto r3 = flash_attention(q, k, v, FlashAttentionOptions());
+    CHECK(r3.is_ok());
+    if (r3.is_ok()) {
+      std::vector<uint16_t> a3(n), b3(n);
+      o3.to_host(a3.data());
+      r3.out->to_host(b3.data());
+      CHECK(a3 == b3);
+    }
   }
 }
 
@@ -340,18 +351,76 @@ TEST(test_flash_attention_masked_f32, true) {
   maskedc.out->to_host(d.data());
   CHECK(memcmp(a.data(), b.data(), n * 4) == 0);
   CHECK(memcmp(c.data(), d.data(), n * 4) == 0);
-  // 16-bit tensors and malformed masks are setup errors, not launches
-  DeviceTensor qb({1, 2, 8, 64}, SP_BF16);
-  auto mb = DeviceTensor::from_host(zero.data(), {8, 8}, SP_F32);
-  CHECK(!flash_attention_masked(qb, qb, qb, mb, FlashAttentionOptions()).is_ok());
+  // malformed masks are setup errors, not launches
   auto bad = DeviceTensor::from_host(zero.data(), {S, S - 1}, SP_F32);
   CHECK(!flash_attention_masked(q, k, v, bad, FlashAttentionOptions()).is_ok());
+  DeviceTensor m16({S, S}, SP_BF16);
+  CHECK(!flash_attention_masked(q, k, v, m16, FlashAttentionOptions()).is_ok());
 }
 
 TEST(test_flash_attention_setup_errors, true) {
   DeviceTensor q({1, 2, 8, 64}, SP_BF16), k({1, 2, 8, 32}, SP_BF16);
   auto r = flash_attention(q, k, k, FlashAttentionOptions());
   CHECK(!r.is_ok() && r.error.has_value());
+  // a head dim no kernel covers is reported by the library
+  DeviceTensor q48({1, 2, 8, 48}, SP_F32);
+  auto r48 = flash_attention(q48, q48, q48, FlashAttentionOptions());
+  CHECK(!r48.is_ok() && r48.error->message.find("head_dim") != std::string::npos);
+}
+
+TEST(test_flash_attention_options, true) {
+  // FlashAttentionOptions.out_dtype and a value head dim of its own (attention.rs:39-69,
+  // :140-147): out is [B, H, Sq, Dv] of out_dtype; bf16 / f16 outputs are the f32 result rounded
+  // once, bit for bit
+  const int B = 1, H = 2, Sq = 40, Sk = 57, D = 80, Dv = 48;
+  auto qf = randn((size_t)B * H * Sq * D, 801), kf = randn((size_t)B * H * Sk * D, 802);
+  auto vf = randn((size_t)B * H * Sk * Dv, 803);
+  auto q = DeviceTensor::from_host(qf.data(), {B, H, Sq, D}, SP_F32);
+  auto k = DeviceTensor::from_host(kf.data(), {B, H, Sk, D}, SP_F32);
+  auto v = DeviceTensor::from_host(vf.data(), {B, H, Sk, Dv}, SP_F32);
+  auto r32 = flash_attention(q, k, v, FlashAttentionOptions());
+  auto rbf = flash_attention(q, k, v, FlashAttentionOptions().with_dtype(SP_BF16));
+  CHECK(r32.is_ok() && rbf.is_ok());
+  if (!(r32.is_ok() && rbf.is_ok())) return;
+  CHECK((r32.out->dims() == std::vector<int64_t>{B, H, Sq, Dv}) && rbf.out->dtype() == SP_BF16);
+  std::vector<float> o32((size_t)B * H * Sq * Dv);
+  std::vector<uint16_t> obf(o32.size());
+  r32.out->to_host(o32.data());
+  rbf.out->to_host(obf.data());
+  size_t same = 0;
+  for (size_t i = 0; i < o32.size(); ++i) {
+    uint32_t u;
+    memcpy(&u, &o32[i], 4);
+    u += 0x7fff + ((u >> 16) & 1);
+    same += (uint16_t)(u >> 16) == obf[i];
+  }
+  CHECK(same == o32.size());
+  // against double precision, per row at 1e-5 relative (Dv != D: the host loop takes Dv rows)
+  double worst = 0;
+  for (int bh = 0; bh < B * H; ++bh)
+    for (int i = 0; i < Sq; ++i) {
+      std::vector<double> sc(Sk);
+      double mx = -1e300;
+      for (int j = 0; j < Sk; ++j) {
+        double acc = 0;
+        for (int e = 0; e < D; ++e)
+          acc += (double)qf[((size_t)bh * Sq + i) * D + e] * kf[((size_t)bh * Sk + j) * D + e];
+        sc[j] = acc / sqrt((double)D);
+        mx = fmax(mx, sc[j]);
+      }
+      double l = 0;
+      for (auto& x : sc) l += (x = exp(x - mx));
+      double scale = 1e-30, err = 0;
+      for (int e = 0; e < Dv; ++e) {
+        double o = 0;
+        for (int j = 0; j < Sk; ++j) o += sc[j] * vf[((size_t)bh * Sk + j) * Dv + e];
+        o /= l;
+        scale = fmax(scale, fabs(o));
+        err = fmax(err, fabs(o - o32[((size_t)bh * Sq + i) * Dv + e]));
+      }
+      worst = fmax(worst, err / scale);
+    }
+  CHECK(worst <= 1e-5);
 }
 
 int main(int argc, char** argv) {

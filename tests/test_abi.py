@@ -172,15 +172,32 @@ def test_workspace_size_monotone(sp_lib):
 
 
 def test_flash_attention_masked_validation(sp_lib):
-    """The additive mask is an f32 path: 16-bit tensors are unsupported, a NULL mask or a
-    negative stride is invalid (all checked before any launch)."""
-    def call(dtype, mask=1 << 20, sb=0):
-        return sp_lib.sp_flash_attention_masked(16, 16, 16, 16, mask, sb, 0, 8, 1, 2, 8, 8, 64,
+    """A NULL or misaligned mask, a negative stride and head dims without a kernel are
+    rejected before any launch (the mask itself is f32 for every tensor dtype)."""
+    def call(dtype, mask=1 << 20, sb=0, d=64):
+        return sp_lib.sp_flash_attention_masked(16, 16, 16, 16, mask, sb, 0, 8, 1, 2, 8, 8, d,
                                                 0.125, 0, dtype, None)
-    assert call(_lib.SP_BF16) == _lib.SP_EUNSUPPORTED
-    assert call(_lib.SP_F16) == _lib.SP_EUNSUPPORTED
     assert call(_lib.SP_F32, mask=None) == _lib.SP_EINVAL
+    assert call(_lib.SP_BF16, mask=None) == _lib.SP_EINVAL
+    assert call(_lib.SP_F32, mask=(1 << 20) + 2) == _lib.SP_EINVAL
     assert call(_lib.SP_F32, sb=-1) == _lib.SP_EINVAL
+    assert call(_lib.SP_BF16, d=80) == _lib.SP_EUNSUPPORTED  # 16-bit kernels: 64 / 128
+    assert call(_lib.SP_F32, d=48) == _lib.SP_EUNSUPPORTED
+
+
+def test_flash_attention_ex_validation(sp_lib):
+    """sp_flash_attention_ex: value head dims and output dtypes checked before any launch."""
+    def call(d=80, dv=80, dtype=_lib.SP_F32, out_dtype=_lib.SP_F32):
+        return sp_lib.sp_flash_attention_ex(16, 16, 16, 16, None, 0, 0, 0, 1, 2, 8, 8, d, dv,
+                                            0.125, 0, dtype, out_dtype, None)
+    assert call(dv=82) == _lib.SP_EUNSUPPORTED        # not a multiple of 4
+    assert call(dv=260) == _lib.SP_EUNSUPPORTED       # past 256
+    assert call(dv=0) == _lib.SP_EINVAL
+    assert call(out_dtype=7) == _lib.SP_EINVAL
+    assert call(d=128, dv=64, dtype=_lib.SP_BF16) == _lib.SP_EUNSUPPORTED  # 16-bit: Dv == D
+    for d in (40, 64, 80, 128, 160, 256):             # f32 head dims with kernels: no error
+        assert sp_lib.sp_flash_attention_ex(0, 0, 0, 0, None, 0, 0, 0, 0, 2, 8, 8, d, d, 0.1, 0,
+                                            _lib.SP_F32, _lib.SP_F32, None) == _lib.SP_OK
 
 
 def test_paged_prefill_workspace_size(sp_lib):

@@ -174,6 +174,28 @@ def test_attention_closed_forms():
     assert (o == 0).all()
 
 
+@pytest.mark.parametrize("d,dv", [(40, 160), (64, 24), (16, 16 * 3)])
+def test_attention_value_head_dim(d, dv):
+    """V with a head dim of its own (flash_attention's val_dim, sketchpad-cubecl
+    attention.rs:135-143): the output is linear in V column by column, so it equals the
+    equal-dim oracle applied to V's columns in D-wide slices (the last slice zero-padded), and
+    float64 SDPA (which takes any value dim) on the whole."""
+    rng = np.random.default_rng(d * 10 + dv)
+    q, k = _rand(rng, 7, 4, d), _rand(rng, 19, 2, d)
+    v = _rand(rng, 19, 2, dv)
+    got = O.attention_f64(q, k, v, scale=d ** -0.5, causal=True, q_pos0=12)
+    assert got.shape == (7, 4, dv)
+    for c0 in range(0, dv, d):
+        w = min(d, dv - c0)
+        vs = np.zeros((19, 2, d), np.float32)
+        vs[:, :, :w] = v[:, :, c0:c0 + w]
+        part = O.attention_f64(q, k, vs, scale=d ** -0.5, causal=True, q_pos0=12)
+        np.testing.assert_array_equal(got[:, :, c0:c0 + w], part[:, :, :w])
+    ref = _torch_sdpa_f64(q, np.repeat(k, 2, axis=1), np.repeat(v, 2, axis=1), d ** -0.5,
+                          O.prefill_causal_mask(7, 19))
+    np.testing.assert_allclose(got, ref, rtol=0, atol=1e-12)
+
+
 def test_attention_gqa_equals_repeated_mha():
     """repeat_kv (transformer.rs:257-271): query head h reads KV head h // (Hq/Hkv)."""
     rng = np.random.default_rng(5)
