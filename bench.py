@@ -22,6 +22,11 @@ before the timed region starts. Prints one JSON line:
   polar_decode  the same decode step on PolarQuant-compressed pools (sp_polar_kv_append +
              sp_polar_paged_decode): launch time, algorithmic bytes (2 + D/2 per cached
              vector), GB/s, fraction of HBM peak, and the speed-up over the dense decode
+  configs    C4 (one mixed iteration through sp_ragged_paged_attention: the prefill half's
+             fraction of the bf16 MFMA peak, the decode half's fraction of HBM, the call against
+             the serial bound) and the C5 / C1 decode calls' fractions of HBM
+The CPU legs run on the threads OMP_NUM_THREADS allots (every CPU this process may use when it
+is unset) and on one thread, and report the host's CPU model and counts.
 """
 from __future__ import annotations
 
@@ -66,8 +71,10 @@ def parse_args():
     ap.add_argument("--layer", action="store_true",
                     help="also time a whole attention layer (projections + RoPE append + "
                          "attention) on the C2 decode step and the C3 prefill")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="skip the C4 mixed step and the C5 / C1 decode legs")
     ap.add_argument("--secondary", action="store_true",
-                    help="also time the other decode configs (C4, C5) and report them")
+                    help="also time C4's halves on their own, f32 flash attention and a layer")
     return ap.parse_args()
 
 
@@ -185,12 +192,46 @@ def time_polar_decode(w, t, steps: int, warmup: int):
     }
 
 
+def host_cpu():
+    """This host's CPU: model name, logical CPUs, the CPUs this process may run on, and the
+    threads the CPU legs use: OMP_NUM_THREADS when set (the GPU box allots each GPU's job a
+    share of its cores through it), else every CPU this process may run on."""
+    model = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    try:
+        allowed = len(os.sched_getaffinity(0))
+    except AttributeError:
+        allowed = os.cpu_count() or 1
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    threads = int(env) if env.isdigit() and int(env) > 0 else allowed
+    return {"model": model, "nproc": os.cpu_count(), "affinity": allowed, "threads": threads,
+            "threads_from": "OMP_NUM_THREADS" if env.isdigit() and int(env) > 0 else "affinity"}
+
+
+def _timed_reps(fn, budget_s: float, max_reps: int, min_reps: int = 1):
+    reps, spent = 0, 0.0
+    while (spent < budget_s or reps < min_reps) and reps < max_reps:
+        t0 = time.perf_counter()
+        fn()
+        spent += time.perf_counter() - t0
+        reps += 1
+    return spent / reps, reps
+
+
 def cpu_baseline(w, t, budget_s: float):
-    """Time the oracle's C port of the reference's decode op sequence on this host."""
+    """Time the oracle's C port of the reference's decode op sequence on this host: full decode
+    steps of the workload, on the host's allotted threads and on one thread."""
     import torch
     from oracle import oracle as O
 
-    threads = min(16, os.cpu_count() or 1)
+    cpu = host_cpu()
+    threads = cpu["threads"]
     kp = t["k_pool"].float().cpu().numpy()
     vp = t["v_pool"].float().cpu().numpy()
     q = t["q"].float().cpu().numpy()
@@ -198,15 +239,13 @@ def cpu_baseline(w, t, budget_s: float):
     vn = t["v_new"].float().cpu().numpy()
     out = np.empty_like(q)
     olay = O.make_layout(w.num_blocks, w.num_layers, w.layer, w.hkv, w.block_size, w.head_dim)
-    reps, spent = 0, 0.0
-    while spent < budget_s and reps < 100:
-        t0 = time.perf_counter()
-        O.cpu_decode_baseline(out, q, kn, vn, kp, vp, olay, w.block_tables, w.context_lens,
-                              scale=w.head_dim ** -0.5, window_left=w.window_left,
-                              threads=threads)
-        spent += time.perf_counter() - t0
-        reps += 1
-    per_step = spent / reps
+    def step(nt):
+        return lambda: O.cpu_decode_baseline(out, q, kn, vn, kp, vp, olay, w.block_tables,
+                                             w.context_lens, scale=w.head_dim ** -0.5,
+                                             window_left=w.window_left, threads=nt)
+
+    per_step, reps = _timed_reps(step(threads), budget_s * 2 / 3, 100)
+    per_1, reps_1 = _timed_reps(step(1), budget_s / 3, 20)
     bytes_step = w.decode_bytes() + w.append_bytes()
     return {
         "value": round(bytes_step / per_step / 1e9, 3),
@@ -214,7 +253,10 @@ def cpu_baseline(w, t, budget_s: float):
         "cores": threads,
         "kind": "port",
         "sample": (f"{w.name}: {reps} full decode steps ({w.num_seqs} seqs, append + gather + "
-                   f"repeat_kv + matmul/softmax/matmul, f32), {per_step * 1e3:.1f} ms/step"),
+                   f"repeat_kv + matmul/softmax/matmul, f32), {per_step * 1e3:.1f} ms/step on "
+                   f"{threads} threads; {reps_1} on 1 thread, {per_1 * 1e3:.1f} ms/step"),
+        "value_1_thread": round(bytes_step / per_1 / 1e9, 3),
+        "host": cpu,
     }
 
 
@@ -487,31 +529,124 @@ def time_flash_f32(steps: int, warmup: int, b: int = 2, h: int = 8, s: int = 409
 
 def cpu_prefill_baseline(w, budget_s: float):
     """The oracle's C port of the reference's prefill op sequence ([Hq, L, L] f32 scores per
-    sequence) on a bounded sample: the two shortest C3 sequences."""
+    sequence) on the whole C3 workload (all eight sequences), on the host's allotted threads and
+    on one thread."""
     import torch
     from oracle import oracle as O
     from sketchpad_amd import workloads as W
 
-    threads = min(16, os.cpu_count() or 1)
-    idx = np.argsort(w.lens)[:2]
-    lens = w.lens[idx]
-    sub = W.PrefillWorkload(w.name + "-sample", w.seed, lens, w.hq, w.hkv, w.head_dim, w.dtype)
-    t = W.make_prefill_tensors(sub, device="cpu", with_pool=False)
+    cpu = host_cpu()
+    threads = cpu["threads"]
+    t = W.make_prefill_tensors(w, device="cpu", with_pool=False)
     q, k, v = (t[n].float().numpy() for n in ("q", "k", "v"))
     out = np.empty_like(q)
-    reps, spent = 0, 0.0
-    while spent < budget_s and reps < 50:
-        t0 = time.perf_counter()
-        O.cpu_prefill_baseline(out, q, k, v, sub.cu_seqlens, hq=w.hq, hkv=w.hkv, d=w.head_dim,
-                               scale=w.head_dim ** -0.5, threads=threads)
-        spent += time.perf_counter() - t0
-        reps += 1
-    per = spent / reps
-    return {"value": round(sub.flops() / per / 1e12, 5), "unit": "TFLOP/s", "cores": threads,
+
+    def run(nt):
+        return lambda: O.cpu_prefill_baseline(out, q, k, v, w.cu_seqlens, hq=w.hq, hkv=w.hkv,
+                                              d=w.head_dim, scale=w.head_dim ** -0.5,
+                                              threads=nt)
+
+    per, reps = _timed_reps(run(threads), budget_s * 2 / 3, 50)
+    per_1, reps_1 = _timed_reps(run(1), budget_s / 3, 5)
+    return {"value": round(w.flops() / per / 1e12, 5), "unit": "TFLOP/s", "cores": threads,
             "kind": "port",
-            "sample": f"C3 sequences of length {[int(x) for x in lens]}: {reps} causal prefills "
-                      f"(repeat_kv + [Hq,L,L] f32 scores + mask + softmax + matmul), "
-                      f"{per * 1e3:.1f} ms each"}
+            "sample": f"the whole C3 batch ({w.num_seqs} sequences, {w.total_tokens} tokens): "
+                      f"{reps} causal prefills (repeat_kv + [Hq,L,L] f32 scores + mask + softmax "
+                      f"+ matmul per sequence), {per * 1e3:.1f} ms each on {threads} threads; "
+                      f"{reps_1} on 1 thread, {per_1 * 1e3:.1f} ms",
+            "value_1_thread": round(w.flops() / per_1 / 1e12, 5),
+            "host": cpu}
+
+
+def time_mixed_c4(steps: int, warmup: int):
+    """C4, one scheduler iteration as one ragged batch over one pool:
+    append the 2,176 new tokens, then sp_ragged_paged_attention (chunked prefill over the 4
+    chunks, decode over the 128 one-token sequences, on one stream). Reports the attention call,
+    its two halves timed on their own, the prefill's fraction of the bf16 MFMA peak, the
+    decode's fraction of HBM, and the whole call against the serial bound
+    F / 2.5 PFLOP/s + B / 8 TB/s."""
+    import torch
+    import sketchpad_amd as sp
+    from sketchpad_amd import workloads as W
+
+    w = W.mixed_c4()
+    t = W.make_mixed_tensors(w)
+    lay = sp.layout(t["num_blocks"], 1, 0, w.hkv, w.block_size, w.head_dim)
+    stream = torch.cuda.current_stream()
+    s = stream.cuda_stream
+    P, T0 = w.num_prefill_seqs, w.num_prefill_tokens
+    pmax, dmax = int(w.chunk_lens.max()), int(w.decode_lens.max())
+    mb = t["block_tables"].shape[1]
+    ws = sp.alloc_ragged_workspace(w.num_seqs, P, pmax, dmax, w.hq, lay, mb)
+    scale = w.head_dim ** -0.5
+
+    def append():
+        sp.kv_append(t["k_pool"], t["v_pool"], lay, t["k_new"], t["v_new"], t["slot_mapping"],
+                     stream=s)
+
+    def attention():
+        sp.ragged_paged_attention(t["out"], t["q"], t["k_pool"], t["v_pool"], lay,
+                                  t["block_tables"], t["cu_seqlens_q"], t["context_lens"],
+                                  num_prefill_seqs=P, num_prefill_tokens=T0,
+                                  prefill_max_seqlen_q=pmax, decode_max_context_len=dmax,
+                                  scale=scale, workspace=ws, stream=s)
+
+    def prefill_half():
+        sp.paged_prefill(t["out"][:T0], t["q"][:T0], t["k_pool"], t["v_pool"], lay,
+                         t["block_tables"][:P], t["cu_seqlens_q"], t["context_lens"][:P], pmax,
+                         scale, workspace=ws, stream=s)
+
+    def decode_half():
+        sp.paged_decode(t["out"][T0:], t["q"][T0:], t["k_pool"], t["v_pool"], lay,
+                        t["block_tables"][P:], t["context_lens"][P:], dmax, scale, workspace=ws,
+                        stream=s)
+
+    for _ in range(warmup):
+        append()
+        attention()
+    torch.cuda.synchronize()
+    at_ms, _ = _event_times(stream, attention, steps)
+    ap_ms, _ = _event_times(stream, append, steps)
+    pf_ms, _ = _event_times(stream, prefill_half, steps)
+    dc_ms, _ = _event_times(stream, decode_half, steps)
+    F, B = w.prefill_flops(), w.decode_bytes()
+    bound_ms = (F / (MFMA_BF16_PEAK_TFLOPS * 1e12) + B / (HBM_PEAK_GBS * 1e9)) * 1e3
+    pf_tf = F / (pf_ms * 1e-3) / 1e12
+    dc_gbs = B / (dc_ms * 1e-3) / 1e9
+    return {
+        "workload": f"{w.name}: {P} chunks of {list(map(int, w.chunk_lens))} new tokens on "
+                    f"contexts {list(map(int, w.ctx_before))} + {w.num_decode_seqs} decode seqs "
+                    f"L~U[{int(w.decode_lens.min())},{int(w.decode_lens.max())}], Hq={w.hq}, "
+                    f"Hkv={w.hkv}, D={w.head_dim}, one pool, seed {w.seed:#x}",
+        "attention_ms": round(at_ms, 5),
+        "append_ms": round(ap_ms, 5),
+        "prefill_ms": round(pf_ms, 5),
+        "prefill_tflops": round(pf_tf, 2),
+        "prefill_frac_mfma": round(pf_tf / MFMA_BF16_PEAK_TFLOPS, 4),
+        "prefill_flops": F,
+        "decode_ms": round(dc_ms, 5),
+        "decode_GBs": round(dc_gbs, 2),
+        "decode_frac_hbm": round(dc_gbs / HBM_PEAK_GBS, 4),
+        "decode_bytes": B,
+        "serial_bound_ms": round(bound_ms, 5),
+        "frac_of_serial_bound": round(bound_ms / at_ms, 4),
+        "kernels": "sp_ragged_paged_attention: prefill_kernel<bf16,128,true> (+ "
+                   "prefill_combine_kernel) then paged_decode_kernel + decode_combine_kernel",
+    }
+
+
+def time_decode_leg(name: str, steps: int):
+    """A decode config's sp_paged_decode call: ms, GB/s over its algorithmic bytes, fraction of
+    HBM."""
+    from sketchpad_amd import workloads as W
+    wx = W.DECODE_CONFIGS[name]()
+    rx = time_decode_config(wx, steps, 2)
+    gbs = rx["decode_bytes"] / (rx["decode_ms_avg"] * 1e-3) / 1e9
+    return {"workload": f"{wx.name}: B={wx.num_seqs}, Hq={wx.hq}, Hkv={wx.hkv}, D={wx.head_dim}, "
+                        f"{wx.dtype}, window {wx.window_left}, "
+                        f"L~U[{int(wx.context_lens.min())},{int(wx.context_lens.max())}]",
+            "decode_ms": round(rx["decode_ms_avg"], 5), "decode_bytes": rx["decode_bytes"],
+            "decode_GBs": round(gbs, 2), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
 
 
 def main():
@@ -590,25 +725,22 @@ def main():
     if not args.no_prefill:
         wp, pf = time_prefill_c3(max(10, args.steps // 2), 3)
         if not args.no_cpu_baseline:
-            pf["cpu_baseline"] = cpu_prefill_baseline(wp, args.cpu_seconds / 2)
+            pf["cpu_baseline"] = cpu_prefill_baseline(wp, args.cpu_seconds)
         line["prefill"] = pf
+    if not args.no_configs:
+        # the other benchmark configurations: C4 (one mixed iteration), C5, C1
+        cfg = {"C4": time_mixed_c4(max(10, args.steps // 2), 2)}
+        for name in ("C5", "C1"):
+            if name != args.config:
+                cfg[name] = time_decode_leg(name, max(10, args.steps // 2))
+        line["configs"] = cfg
     if args.secondary:
-        line.setdefault("secondary", {})["C4-chunked-prefill"] = time_chunked_c4(10, 2)
-        line["secondary"]["flash-attention-f32"] = time_flash_f32(5, 2)
+        sec = line.setdefault("secondary", {})
+        sec["C4-chunked-prefill"] = time_chunked_c4(10, 2)
+        sec["C4-decode"] = time_decode_leg("C4", max(5, args.steps // 2))
+        sec["flash-attention-f32"] = time_flash_f32(5, 2)
     if args.layer or args.secondary:
         line["layer"] = time_layer(args.steps, 3)
-    if args.secondary:
-        sec = {}
-        for name in ("C4", "C5", "C1"):
-            if name == args.config:
-                continue
-            wx = W.DECODE_CONFIGS[name]()
-            rx = time_decode_config(wx, max(5, args.steps // 2), 2)
-            gbs = rx["decode_bytes"] / (rx["decode_ms_avg"] * 1e-3) / 1e9
-            sec[name] = {"decode_ms": round(rx["decode_ms_avg"], 5), "decode_GBs": round(gbs, 2),
-                         "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
-            del rx
-        line.setdefault("secondary", {}).update(sec)
     print(json.dumps(line), flush=True)
 
 

@@ -252,6 +252,40 @@ int sp_paged_prefill(void* out, const void* q,
                      void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * One mixed ragged batch over a paged cache: every sequence's new tokens attend to its whole
+ * paged context (append them first with sp_kv_append / sp_rope_kv_append). Sequences
+ * [0, num_prefill_seqs) are prompt chunks: chunked prefill (sp_paged_prefill, the bottom-right
+ * causal rule of prefill_causal_mask, llama.rs:374-388); sequences [num_prefill_seqs, num_seqs)
+ * add one token each: decode (sp_paged_decode, no mask, llama.rs:255-260). Replaces the
+ * per-sequence forward_cached calls of one scheduler iteration (transformer.rs:184-254 with
+ * start_pos and the mask chosen per sequence as Llama::forward does, llama.rs:247-260) with two
+ * launches on `stream`, chunks first.
+ *   q, out          : [total_q, Hq, D], the chunks' tokens first (num_prefill_tokens of them),
+ *                     then one token per decode sequence
+ *   cu_seqlens_q    : [num_prefill_seqs + 1] token offsets of the chunks (device); may be NULL
+ *                     when num_prefill_seqs == 0
+ *   context_lens    : [num_seqs] (device), block_tables [num_seqs, max_blocks_per_seq] (device)
+ *   prefill_max_seqlen_q, decode_max_context_len : bounds over the respective groups
+ *   workspace       : sp_ragged_attention_workspace_size() bytes (the larger of the two calls'
+ *                     needs; they share it, in stream order). Calls sharing it must not overlap.
+ */
+size_t sp_ragged_attention_workspace_size(int32_t num_seqs, int32_t num_prefill_seqs,
+                                          int32_t prefill_max_seqlen_q,
+                                          int32_t decode_max_context_len, int32_t num_q_heads,
+                                          int32_t window_left, const sp_cache_layout* layout,
+                                          int32_t max_blocks_per_seq);
+int sp_ragged_paged_attention(void* out, const void* q,
+                              const void* k_pool, const void* v_pool,
+                              const sp_cache_layout* layout,
+                              const int32_t* block_tables, int32_t max_blocks_per_seq,
+                              const int32_t* cu_seqlens_q, const int32_t* context_lens,
+                              int32_t num_seqs, int32_t num_prefill_seqs,
+                              int32_t num_prefill_tokens, int32_t prefill_max_seqlen_q,
+                              int32_t decode_max_context_len, int32_t num_q_heads, float scale,
+                              int32_t window_left, sp_dtype dtype, void* workspace,
+                              size_t workspace_bytes, void* stream);
+
+/*
  * Dense attention on [batch, heads, seq, dim] tensors with every option of the reference's
  * flash_attention_impl (sketchpad-cubecl attention.rs:130-178; FlashAttentionOptions
  * :39-69): q, k [batch, heads, seq_q / seq_k, head_dim], v [batch, heads, seq_k, v_head_dim],

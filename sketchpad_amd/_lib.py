@@ -76,6 +76,14 @@ _SIGNATURES = {
                                           POINTER(CacheLayout), c_void_p, c_int32, c_void_p,
                                           c_int32, c_int32, c_int32, c_float, c_int32, c_int32,
                                           c_void_p]),
+    "sp_ragged_attention_workspace_size": (c_size_t, [c_int32, c_int32, c_int32, c_int32,
+                                                      c_int32, c_int32, POINTER(CacheLayout),
+                                                      c_int32]),
+    "sp_ragged_paged_attention": (c_int32, [c_void_p, c_void_p, c_void_p, c_void_p,
+                                            POINTER(CacheLayout), c_void_p, c_int32, c_void_p,
+                                            c_void_p, c_int32, c_int32, c_int32, c_int32,
+                                            c_int32, c_int32, c_float, c_int32, c_int32,
+                                            c_void_p, c_size_t, c_void_p]),
     "sp_varlen_prefill": (c_int32, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                                     c_int32, c_int32, c_int32, c_int32, c_int32, c_float,
                                     c_int32, c_int32, c_int32, c_void_p]),
@@ -267,6 +275,34 @@ def paged_decode_noalloc(out, q, k_pool, v_pool, lay: CacheLayout, block_tables,
                                          block_tables.shape[1], _ptr(context_lens),
                                          max_context_len, num_seqs, hq, scale, window_left,
                                          sp_dtype(q), _stream(stream)))
+
+
+def ragged_paged_attention(out, q, k_pool, v_pool, lay: CacheLayout, block_tables, cu_seqlens_q,
+                           context_lens, *, num_prefill_seqs: int, num_prefill_tokens: int,
+                           prefill_max_seqlen_q: int, decode_max_context_len: int, scale: float,
+                           window_left: int = -1, workspace=None, stream=None) -> None:
+    """sp_ragged_paged_attention: one mixed batch, chunks [0, num_prefill_seqs) first, then one
+    token per decode sequence; q/out [total_q, Hq, D]."""
+    hq = q.shape[1]
+    ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    check(load().sp_ragged_paged_attention(
+        _ptr(out), _ptr(q), _ptr(k_pool), _ptr(v_pool), ctypes.byref(lay), _ptr(block_tables),
+        block_tables.shape[1], _ptr(cu_seqlens_q), _ptr(context_lens), context_lens.numel(),
+        num_prefill_seqs, num_prefill_tokens, prefill_max_seqlen_q, decode_max_context_len, hq,
+        scale, window_left, sp_dtype(q), _ptr(workspace), ws_bytes, _stream(stream)))
+
+
+def alloc_ragged_workspace(num_seqs: int, num_prefill_seqs: int, prefill_max_seqlen_q: int,
+                           decode_max_context_len: int, num_q_heads: int, lay: CacheLayout,
+                           max_blocks_per_seq: int, window_left: int = -1, device="cuda"):
+    """A workspace of sp_ragged_attention_workspace_size() bytes (None when none is needed)."""
+    torch = _torch()
+    n = int(load().sp_ragged_attention_workspace_size(num_seqs, num_prefill_seqs,
+                                                      prefill_max_seqlen_q,
+                                                      decode_max_context_len, num_q_heads,
+                                                      window_left, ctypes.byref(lay),
+                                                      max_blocks_per_seq))
+    return torch.empty(n, dtype=torch.uint8, device=device) if n else None
 
 
 def alloc_decode_workspace(num_seqs: int, num_q_heads: int, max_context_len: int,

@@ -477,6 +477,70 @@ int sp_paged_prefill(void* out, const void* q, const void* k_pool, const void* v
   return launch_prefill(a, dtype, D, true, (hipStream_t)stream);
 }
 
+size_t sp_ragged_attention_workspace_size(int32_t num_seqs, int32_t num_prefill_seqs,
+                                          int32_t prefill_max_seqlen_q,
+                                          int32_t decode_max_context_len, int32_t num_q_heads,
+                                          int32_t window_left, const sp_cache_layout* layout,
+                                          int32_t max_blocks_per_seq) {
+  if (num_seqs <= 0 || num_prefill_seqs < 0 || num_prefill_seqs > num_seqs) return 0;
+  size_t need = 0;
+  if (num_prefill_seqs > 0) {
+    const size_t p = sp_paged_prefill_workspace_size(num_prefill_seqs, prefill_max_seqlen_q,
+                                                     num_q_heads, layout, max_blocks_per_seq);
+    need = p > need ? p : need;
+  }
+  if (num_seqs > num_prefill_seqs) {
+    const size_t d = sp_paged_decode_workspace_size(num_seqs - num_prefill_seqs, num_q_heads,
+                                                    decode_max_context_len, window_left, layout);
+    need = d > need ? d : need;
+  }
+  return need;
+}
+
+int sp_ragged_paged_attention(void* out, const void* q, const void* k_pool, const void* v_pool,
+                              const sp_cache_layout* layout, const int32_t* block_tables,
+                              int32_t max_blocks_per_seq, const int32_t* cu_seqlens_q,
+                              const int32_t* context_lens, int32_t num_seqs,
+                              int32_t num_prefill_seqs, int32_t num_prefill_tokens,
+                              int32_t prefill_max_seqlen_q, int32_t decode_max_context_len,
+                              int32_t num_q_heads, float scale, int32_t window_left,
+                              sp_dtype dtype, void* workspace, size_t workspace_bytes,
+                              void* stream) {
+  const char* fn = "sp_ragged_paged_attention";
+  if (int rc = check_layout(layout, fn)) return rc;
+  if (int rc = check_dtype(dtype, fn)) return rc;
+  if (num_seqs < 0 || num_prefill_seqs < 0 || num_prefill_seqs > num_seqs ||
+      num_prefill_tokens < 0 || num_q_heads <= 0 || max_blocks_per_seq < 0)
+    return fail(SP_EINVAL,
+                "%s: invalid sizes (num_seqs=%d num_prefill_seqs=%d num_prefill_tokens=%d "
+                "num_q_heads=%d max_blocks_per_seq=%d)",
+                fn, num_seqs, num_prefill_seqs, num_prefill_tokens, num_q_heads,
+                max_blocks_per_seq);
+  if (num_seqs == 0) return SP_OK;
+  if (!out || !q || !block_tables || !context_lens || (num_prefill_seqs > 0 && !cu_seqlens_q))
+    return fail(SP_EINVAL, "%s: NULL pointer argument", fn);
+  const int nd = num_seqs - num_prefill_seqs;
+  // both launches go on the caller's stream in this order: the prefill's split partials are
+  // merged before the decode writes its own into the same workspace
+  if (num_prefill_seqs > 0) {
+    if (int rc = sp_paged_prefill(out, q, k_pool, v_pool, layout, block_tables,
+                                  max_blocks_per_seq, cu_seqlens_q, context_lens,
+                                  num_prefill_seqs, prefill_max_seqlen_q, num_q_heads, scale,
+                                  window_left, dtype, workspace, workspace_bytes, stream))
+      return rc;
+  }
+  if (nd > 0) {
+    const int64_t row = (int64_t)num_q_heads * layout->head_dim * dtype_size(dtype);
+    return sp_paged_decode((char*)out + num_prefill_tokens * row,
+                           (const char*)q + num_prefill_tokens * row, k_pool, v_pool, layout,
+                           block_tables + (int64_t)num_prefill_seqs * max_blocks_per_seq,
+                           max_blocks_per_seq, context_lens + num_prefill_seqs,
+                           decode_max_context_len, nd, num_q_heads, scale, window_left, dtype,
+                           workspace, workspace_bytes, stream);
+  }
+  return SP_OK;
+}
+
 static int flash_attention_impl(const char* fn, void* out, const void* q, const void* k,
                                 const void* v, const float* mask, int64_t mask_stride_b,
                                 int64_t mask_stride_h, int64_t mask_stride_q, int32_t batch,

@@ -149,34 +149,20 @@ void BatchedPagedAttention::forward(size_t layer_idx, const DeviceRaggedBatch& b
              "sp_kv_append");
   }
   // 2. attention: chunked prefill over the chunks [0, P), decode over the one-token entries
-  //    [P, B), enqueued in that order on one stream (they share the workspace: stream order
-  //    keeps the prefill's partials merged before the decode writes its own)
-  const int32_t P = hb.num_prefill_seqs, B = (int32_t)hb.num_seqs(), nd = B - P;
-  size_t need = 0;
-  if (P > 0)
-    need = std::max(need, sp_paged_prefill_workspace_size(P, hb.prefill_max_seqlen_q, hq, &lay,
-                                                          hb.max_blocks));
-  if (nd > 0)
-    need = std::max(need, sp_paged_decode_workspace_size(nd, hq, hb.decode_max_context_len, -1,
-                                                         &lay));
+  //    [P, B): one sp_ragged_paged_attention call, two launches on the cache's stream
+  const int32_t P = hb.num_prefill_seqs, B = (int32_t)hb.num_seqs();
+  const size_t need = sp_ragged_attention_workspace_size(B, P, hb.prefill_max_seqlen_q,
+                                                         hb.decode_max_context_len, hq, -1,
+                                                         &lay, hb.max_blocks);
   if (need > workspace_.nbytes())
     workspace_ = DeviceTensor({(int64_t)((need + 3) / 4)}, SP_F32);  // zero-filled
-  void* ws = workspace_.nbytes() ? workspace_.data() : nullptr;
-  if (P > 0)
-    check_sp(sp_paged_prefill(out.data(), q.data(), kp, vp, &lay, batch.block_tables(),
-                              hb.max_blocks, batch.cu_seqlens_q(), batch.context_lens(), P,
-                              hb.prefill_max_seqlen_q, hq, scale, -1, cache_.dtype(), ws,
-                              workspace_.nbytes(), stream),
-             "sp_paged_prefill");
-  if (nd > 0) {
-    const int64_t row = (int64_t)hq * d * (int64_t)dtype_bytes(cache_.dtype());
-    const int64_t tok0 = hb.num_prefill_tokens;
-    check_sp(sp_paged_decode((char*)out.data() + tok0 * row, (const char*)q.data() + tok0 * row,
-                             kp, vp, &lay, batch.block_tables() + (int64_t)P * hb.max_blocks,
-                             hb.max_blocks, batch.context_lens() + P, hb.decode_max_context_len,
-                             nd, hq, scale, -1, cache_.dtype(), ws, workspace_.nbytes(), stream),
-             "sp_paged_decode");
-  }
+  check_sp(sp_ragged_paged_attention(out.data(), q.data(), kp, vp, &lay, batch.block_tables(),
+                                     hb.max_blocks, batch.cu_seqlens_q(), batch.context_lens(),
+                                     B, P, hb.num_prefill_tokens, hb.prefill_max_seqlen_q,
+                                     hb.decode_max_context_len, hq, scale, -1, cache_.dtype(),
+                                     workspace_.nbytes() ? workspace_.data() : nullptr,
+                                     workspace_.nbytes(), stream),
+           "sp_ragged_paged_attention");
 }
 
 }  // namespace sketchpad

@@ -385,3 +385,125 @@ def make_chunked_tensors(w: ChunkedPrefillWorkload, device="cuda") -> dict:
     }
     t["out"] = torch.empty_like(t["q"])
     return t
+
+
+# ---------------------------------------------------------------------------------------------
+# mixed chunked-prefill + decode batch (C4)
+# ---------------------------------------------------------------------------------------------
+
+@dataclass
+class MixedWorkload:
+    """One scheduler iteration as a single ragged batch over one paged pool: prompt chunks first
+    (each attending to its cached context plus itself, bottom-right causal), then one new token
+    per decoding sequence (no mask) — the order build_ragged_batch produces."""
+
+    name: str
+    seed: int
+    chunk_lens: np.ndarray     # int32 [P] new tokens per chunk
+    ctx_before: np.ndarray     # int32 [P] cached tokens before each chunk
+    decode_lens: np.ndarray    # int32 [Bd] context of each decode sequence, its new token included
+    hq: int
+    hkv: int
+    head_dim: int
+    dtype: str
+    block_size: int = 16
+
+    @property
+    def num_prefill_seqs(self) -> int:
+        return len(self.chunk_lens)
+
+    @property
+    def num_decode_seqs(self) -> int:
+        return len(self.decode_lens)
+
+    @property
+    def num_seqs(self) -> int:
+        return self.num_prefill_seqs + self.num_decode_seqs
+
+    @property
+    def new_tokens(self) -> np.ndarray:
+        return np.concatenate([self.chunk_lens, np.ones(self.num_decode_seqs, np.int32)]
+                              ).astype(np.int32)
+
+    @property
+    def context_lens(self) -> np.ndarray:
+        return np.concatenate([self.ctx_before + self.chunk_lens, self.decode_lens]
+                              ).astype(np.int32)
+
+    @property
+    def num_prefill_tokens(self) -> int:
+        return int(self.chunk_lens.sum())
+
+    @property
+    def cu_seqlens_q(self) -> np.ndarray:
+        """Token offsets of the chunks (the decode tokens follow them, one each)."""
+        return np.concatenate([[0], np.cumsum(self.chunk_lens)]).astype(np.int32)
+
+    def prefill_flops(self) -> int:
+        c = self.chunk_lens.astype(np.int64)
+        b = self.ctx_before.astype(np.int64)
+        return int(4 * self.hq * self.head_dim * (c * b + c * (c + 1) // 2).sum())
+
+    def decode_bytes(self) -> int:
+        e = 4 if self.dtype == "f32" else 2
+        L = self.decode_lens.astype(np.int64)
+        return int((L * 2 * self.hkv * self.head_dim * e).sum()
+                   + self.num_decode_seqs * self.hq * self.head_dim * e * 2
+                   + ((L + self.block_size - 1) // self.block_size * 4).sum()
+                   + self.num_decode_seqs * 4)
+
+    def tables(self):
+        rng = np.random.default_rng(self.seed + 1)
+        lens = self.context_lens
+        nblk = int(((lens + self.block_size - 1) // self.block_size).sum())
+        return _tables_from_pool(rng, lens, self.block_size, nblk), nblk
+
+    def positions(self) -> np.ndarray:
+        lens, new = self.context_lens, self.new_tokens
+        return np.concatenate([np.arange(L - n, L) for L, n in zip(lens, new)]).astype(np.int32)
+
+    def slot_mapping(self) -> np.ndarray:
+        tables, _ = self.tables()
+        out = []
+        for s, (L, n) in enumerate(zip(self.context_lens, self.new_tokens)):
+            pos = np.arange(L - n, L)
+            out.append(tables[s, pos // self.block_size] * self.block_size + pos % self.block_size)
+        return np.concatenate(out).astype(np.int32)
+
+
+def mixed_c4() -> MixedWorkload:
+    """C4: Qwen2.5-7B heads (28 q / 4 kv, D 128, bf16, BS 16); 4 chunks of
+    512 new tokens on contexts U[1024, 8192] plus 128 decode sequences with contexts
+    U[256, 4096], one seeded shuffle of one pool."""
+    pre, dec = chunked_prefill_c4(), decode_c4()
+    return MixedWorkload("C4-qwen25-7b-mixed", seed_for(4) + 200, pre.chunk_lens, pre.ctx_before,
+                         dec.context_lens, 28, 4, 128, "bf16")
+
+
+def make_mixed_tensors(w: MixedWorkload, device="cuda") -> dict:
+    """One pool with random cached context, the batch's q / k_new / v_new (chunk tokens first)
+    and the int32 metadata."""
+    import torch
+    g = torch.Generator(device=device)
+    g.manual_seed(w.seed)
+    dt = torch_dtype(w.dtype)
+    tables, nblk = w.tables()
+
+    def randn(*shape):
+        return torch.randn(*shape, generator=g, device=device, dtype=torch.float32).to(dt)
+
+    T = int(w.new_tokens.sum())
+    t = {
+        "k_pool": randn(nblk, 1, w.hkv, w.block_size, w.head_dim),
+        "v_pool": randn(nblk, 1, w.hkv, w.block_size, w.head_dim),
+        "q": randn(T, w.hq, w.head_dim),
+        "k_new": randn(T, w.hkv, w.head_dim),
+        "v_new": randn(T, w.hkv, w.head_dim),
+        "block_tables": torch.from_numpy(tables).to(device),
+        "context_lens": torch.from_numpy(w.context_lens).to(device),
+        "cu_seqlens_q": torch.from_numpy(w.cu_seqlens_q).to(device),
+        "slot_mapping": torch.from_numpy(w.slot_mapping()).to(device),
+        "num_blocks": nblk,
+    }
+    t["out"] = torch.empty_like(t["q"])
+    return t

@@ -220,3 +220,27 @@ def test_missing_library_fails_loudly(monkeypatch, tmp_path):
     monkeypatch.setattr(_lib, "LIB_PATH", tmp_path / "nope.so")
     with pytest.raises(RuntimeError, match="no fallback"):
         _lib.load()
+
+
+def test_ragged_paged_attention_validation(sp_lib):
+    """sp_ragged_paged_attention: the group split and pointers are checked before any launch;
+    the workspace is the larger of the two calls' needs."""
+    lay = _lib.layout(10_000, 1, 0, 4, 16, 128)
+
+    def call(num_seqs=4, num_prefill=2, cu=1 << 20, tok=100):
+        return sp_lib.sp_ragged_paged_attention(16, 16, 16, 16, ctypes.byref(lay), 16, 8, cu, 16,
+                                                num_seqs, num_prefill, tok, 64, 100, 28, 0.1, -1,
+                                                _lib.SP_BF16, None, 0, None)
+    assert call(num_prefill=5) == _lib.SP_EINVAL
+    assert call(num_prefill=-1) == _lib.SP_EINVAL
+    assert call(tok=-1) == _lib.SP_EINVAL
+    assert call(cu=None) == _lib.SP_EINVAL
+    assert call(num_seqs=0, num_prefill=0) == _lib.SP_OK
+    # C4's shape: the chunks' split partials are larger than the decode partials
+    pre = sp_lib.sp_paged_prefill_workspace_size(4, 512, 28, ctypes.byref(lay), 547)
+    dec = sp_lib.sp_paged_decode_workspace_size(128, 28, 4096, -1, ctypes.byref(lay))
+    both = sp_lib.sp_ragged_attention_workspace_size(132, 4, 512, 4096, 28, -1, ctypes.byref(lay),
+                                                     547)
+    assert both == max(pre, dec) > 0
+    assert sp_lib.sp_ragged_attention_workspace_size(128, 0, 0, 4096, 28, -1, ctypes.byref(lay),
+                                                     547) == dec
