@@ -15,6 +15,8 @@
 #include <omp.h>
 #endif
 
+#include <immintrin.h>
+
 /* ------------------------------------------------------------------------------------------ */
 /* element conversion                                                                          */
 /* ------------------------------------------------------------------------------------------ */
@@ -386,6 +388,92 @@ void spo_cpu_decode_baseline(float* out, const float* q, const float* k_new, con
   }
 }
 
+/* Blocked single-precision GEMM for the prefill baseline: the reference's two matmuls go through
+ * burn-ndarray, i.e. the matrixmultiply crate's packed sgemm with AVX2/FMA micro-kernels, so the
+ * port uses the same kind of kernel rather than a dot product per output. B is packed into
+ * panels of 16 columns (panel p, row kk at bp[(p * k + kk) * 16], zero padded); a 6 x 16 block of
+ * C is held in 12 AVX registers while kk runs over the shared dimension. */
+#define GEMM_MR 6
+#define GEMM_NR 16
+
+/* C[i, j] = alpha * sum_kk A[i, kk] * B[kk, j] over rows [0, m), columns [0, n) */
+static void gemm_packed(float* c, int64_t ldc, const float* a, int64_t lda, const float* bp,
+                        int64_t m, int64_t n, int64_t k, float alpha) {
+  for (int64_t p = 0; p * GEMM_NR < n; ++p) {
+    const float* panel = bp + p * k * GEMM_NR;
+    const int64_t j0 = p * GEMM_NR, nc = n - j0 < GEMM_NR ? n - j0 : GEMM_NR;
+    for (int64_t i0 = 0; i0 < m; i0 += GEMM_MR) {
+      const int mr = m - i0 < GEMM_MR ? (int)(m - i0) : GEMM_MR;
+      const float* a0 = a + i0 * lda;
+      const float* a1 = a + (i0 + (mr > 1 ? 1 : 0)) * lda;
+      const float* a2 = a + (i0 + (mr > 2 ? 2 : 0)) * lda;
+      const float* a3 = a + (i0 + (mr > 3 ? 3 : 0)) * lda;
+      const float* a4 = a + (i0 + (mr > 4 ? 4 : 0)) * lda;
+      const float* a5 = a + (i0 + (mr > 5 ? 5 : 0)) * lda;
+      __m256 c00 = _mm256_setzero_ps(), c01 = c00, c10 = c00, c11 = c00, c20 = c00, c21 = c00;
+      __m256 c30 = c00, c31 = c00, c40 = c00, c41 = c00, c50 = c00, c51 = c00;
+      for (int64_t kk = 0; kk < k; ++kk) {
+        const __m256 b0 = _mm256_loadu_ps(panel + kk * GEMM_NR);
+        const __m256 b1 = _mm256_loadu_ps(panel + kk * GEMM_NR + 8);
+        __m256 av = _mm256_broadcast_ss(a0 + kk);
+        c00 = _mm256_fmadd_ps(av, b0, c00);
+        c01 = _mm256_fmadd_ps(av, b1, c01);
+        av = _mm256_broadcast_ss(a1 + kk);
+        c10 = _mm256_fmadd_ps(av, b0, c10);
+        c11 = _mm256_fmadd_ps(av, b1, c11);
+        av = _mm256_broadcast_ss(a2 + kk);
+        c20 = _mm256_fmadd_ps(av, b0, c20);
+        c21 = _mm256_fmadd_ps(av, b1, c21);
+        av = _mm256_broadcast_ss(a3 + kk);
+        c30 = _mm256_fmadd_ps(av, b0, c30);
+        c31 = _mm256_fmadd_ps(av, b1, c31);
+        av = _mm256_broadcast_ss(a4 + kk);
+        c40 = _mm256_fmadd_ps(av, b0, c40);
+        c41 = _mm256_fmadd_ps(av, b1, c41);
+        av = _mm256_broadcast_ss(a5 + kk);
+        c50 = _mm256_fmadd_ps(av, b0, c50);
+        c51 = _mm256_fmadd_ps(av, b1, c51);
+      }
+      const __m256 al = _mm256_set1_ps(alpha);
+      float tmp[GEMM_MR][GEMM_NR];
+      _mm256_storeu_ps(tmp[0], _mm256_mul_ps(c00, al));
+      _mm256_storeu_ps(tmp[0] + 8, _mm256_mul_ps(c01, al));
+      _mm256_storeu_ps(tmp[1], _mm256_mul_ps(c10, al));
+      _mm256_storeu_ps(tmp[1] + 8, _mm256_mul_ps(c11, al));
+      _mm256_storeu_ps(tmp[2], _mm256_mul_ps(c20, al));
+      _mm256_storeu_ps(tmp[2] + 8, _mm256_mul_ps(c21, al));
+      _mm256_storeu_ps(tmp[3], _mm256_mul_ps(c30, al));
+      _mm256_storeu_ps(tmp[3] + 8, _mm256_mul_ps(c31, al));
+      _mm256_storeu_ps(tmp[4], _mm256_mul_ps(c40, al));
+      _mm256_storeu_ps(tmp[4] + 8, _mm256_mul_ps(c41, al));
+      _mm256_storeu_ps(tmp[5], _mm256_mul_ps(c50, al));
+      _mm256_storeu_ps(tmp[5] + 8, _mm256_mul_ps(c51, al));
+      for (int r = 0; r < mr; ++r)
+        memcpy(c + (i0 + r) * ldc + j0, tmp[r], sizeof(float) * (size_t)nc);
+    }
+  }
+}
+
+/* pack B = X^T for X [n rows, k cols] (row stride ldx): panel rows are X's columns */
+static void pack_transposed(float* bp, const float* x, int64_t ldx, int64_t n, int64_t k) {
+  for (int64_t p = 0; p * GEMM_NR < n; ++p)
+    for (int64_t kk = 0; kk < k; ++kk)
+      for (int c = 0; c < GEMM_NR; ++c) {
+        const int64_t j = p * GEMM_NR + c;
+        bp[(p * k + kk) * GEMM_NR + c] = j < n ? x[j * ldx + kk] : 0.f;
+      }
+}
+
+/* pack B = X for X [k rows, n cols] (row stride ldx) */
+static void pack_rows(float* bp, const float* x, int64_t ldx, int64_t k, int64_t n) {
+  for (int64_t p = 0; p * GEMM_NR < n; ++p)
+    for (int64_t kk = 0; kk < k; ++kk)
+      for (int c = 0; c < GEMM_NR; ++c) {
+        const int64_t j = p * GEMM_NR + c;
+        bp[(p * k + kk) * GEMM_NR + c] = j < n ? x[kk * ldx + j] : 0.f;
+      }
+}
+
 void spo_cpu_prefill_baseline(float* out, const float* q, const float* k, const float* v,
                               const int32_t* cu_seqlens, int64_t num_seqs, int hq, int hkv,
                               int d, float scale, int threads) {
@@ -399,37 +487,29 @@ void spo_cpu_prefill_baseline(float* out, const float* q, const float* k, const 
       const int64_t t0 = cu_seqlens[s], len = cu_seqlens[s + 1] - cu_seqlens[s];
       if (len <= 0) continue;
       const int g = h / rep;
-      /* repeat_kv copy of this head's K/V, contiguous [len, D] */
-      float* kh = (float*)malloc(sizeof(float) * (size_t)(len * d));
-      float* vh = (float*)malloc(sizeof(float) * (size_t)(len * d));
-      for (int64_t j = 0; j < len; ++j) {
-        memcpy(kh + j * d, k + ((t0 + j) * hkv + g) * d, sizeof(float) * (size_t)d);
-        memcpy(vh + j * d, v + ((t0 + j) * hkv + g) * d, sizeof(float) * (size_t)d);
-      }
-      /* [len, len] scores, * scale, + causal mask, softmax, matmul */
+      const int64_t lp = (len + GEMM_NR - 1) / GEMM_NR * GEMM_NR;
+      const int64_t dp = ((int64_t)d + GEMM_NR - 1) / GEMM_NR * GEMM_NR;
+      /* repeat_kv of this head's K/V, packed for the two products: K^T [D, L] and V [L, D] */
+      float* kt = (float*)malloc(sizeof(float) * (size_t)(lp * d));
+      float* vp = (float*)malloc(sizeof(float) * (size_t)(dp * len));
+      pack_transposed(kt, k + (t0 * hkv + g) * d, (int64_t)hkv * d, len, d);
+      pack_rows(vp, v + (t0 * hkv + g) * d, (int64_t)hkv * d, len, d);
+      /* [L, L] scores = (q k^T) * scale, + causal mask, softmax, then p v: both full products,
+       * as the reference computes them */
       float* sc = (float*)malloc(sizeof(float) * (size_t)(len * len));
+      gemm_packed(sc, len, q + (t0 * hq + h) * d, (int64_t)hq * d, kt, len, len, d, scale);
       for (int64_t i = 0; i < len; ++i) {
-        const float* qi = q + ((t0 + i) * hq + h) * d;
         float* row = sc + i * len;
-        for (int64_t j = 0; j < len; ++j) row[j] = dot_f32(qi, kh + j * d, d) * scale;
         for (int64_t j = i + 1; j < len; ++j) row[j] += -INFINITY;
         softmax_row(row, len);
-        float* oi = out + ((t0 + i) * hq + h) * d;
-        for (int c = 0; c < d; ++c) oi[c] = 0.f;
-        for (int64_t j = 0; j < len; ++j) {
-          const float pj = row[j];
-          const float* vj = vh + j * d;
-#pragma omp simd
-          for (int c = 0; c < d; ++c) oi[c] += pj * vj[c];
-        }
       }
+      gemm_packed(out + (t0 * hq + h) * d, (int64_t)hq * d, sc, len, vp, len, d, len, 1.f);
       free(sc);
-      free(kh);
-      free(vh);
+      free(kt);
+      free(vp);
     }
   }
 }
-
 
 /* ---------------------------------------------------------------------------------------------
  * Rotary position embedding (crates/sketchpad-core/src/rope.rs). Compiled without floating-point

@@ -55,7 +55,9 @@
  *               pins the same formula's shape), NaN / infinity / zero rows
  *   spo_cpu_decode_baseline / spo_cpu_prefill_baseline    the reference's whole decode / prefill
  *       op sequence (store, gather+concat, repeat_kv, matmul, scale, mask, softmax, matmul), f32,
- *       OpenMP over sequences; pinned against spo_attention_f64.
+ *       OpenMP over sequences; the prefill's two products run on a packed 6x16 AVX2/FMA GEMM
+ *       (burn-ndarray's matmul is the matrixmultiply crate's packed sgemm), the decode's are
+ *       matrix-vector products (bandwidth-bound); pinned against spo_attention_f64.
  */
 #ifndef SP_ORACLE_H
 #define SP_ORACLE_H
@@ -136,7 +138,8 @@ void spo_cpu_decode_baseline(float* out, const float* q, const float* k_new, con
 
 /*
  * Timed CPU baseline of causal prefill over packed sequences in the reference's op order:
- * per sequence, repeat_kv, [Hq, L, L] f32 scores, scale, + causal mask, softmax, matmul.
+ * per sequence, repeat_kv, [Hq, L, L] f32 scores, scale, + causal mask, softmax, matmul; both
+ * products in full (as the reference computes them) on a packed AVX2/FMA GEMM.
  * q [T, Hq, D], k/v [T, Hkv, D] f32, cu_seqlens [num_seqs+1]; out [T, Hq, D].
  */
 void spo_cpu_prefill_baseline(float* out, const float* q, const float* k, const float* v,
