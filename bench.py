@@ -62,6 +62,10 @@ def parse_args():
                     help="only run 10 plain 512 MiB device-to-device copies and exit")
     ap.add_argument("--prefill-only", action="store_true",
                     help="only the C3 prefill leg (profiling); prints its JSON object")
+    ap.add_argument("--mixed-only", action="store_true",
+                    help="only the C4 mixed ragged step (profiling); prints its JSON object")
+    ap.add_argument("--flash-only", action="store_true",
+                    help="only the f32 flash-attention leg (profiling); prints its JSON object")
     ap.add_argument("--no-prefill", action="store_true",
                     help="skip the C3 ragged-prefill leg")
     ap.add_argument("--no-polar", action="store_true",
@@ -662,12 +666,34 @@ def main():
         print("bench.py: no GPU visible", file=sys.stderr)
         sys.exit(1)
     if args.calibrate_copy:
+        # counter calibration: 10 runtime device copies (512 MiB read + 512 MiB written each),
+        # then 10 sp_kv_gather calls of one 131,072-token sequence (bf16, 8 KV heads, D 128):
+        # 256 MiB of K and 256 MiB of V read from the pools with the 16-byte loads the decode
+        # kernel uses, the same bytes written out
+        import sketchpad_amd as sp
         src = torch.ones(512 << 20, dtype=torch.uint8, device="cuda")
         dst = torch.empty_like(src)
         for _ in range(10):
             dst.copy_(src)
+        del dst
+        tokens, hkv, d, bs = 131072, 8, 128, 16
+        lay = sp.layout(tokens // bs, 1, 0, hkv, bs, d)
+        kp = torch.randn(tokens // bs, 1, hkv, bs, d, device="cuda").bfloat16()
+        vp = torch.randn_like(kp)
+        table = torch.randperm(tokens // bs, device="cuda").int()
+        ko = torch.empty(hkv, tokens, d, dtype=torch.bfloat16, device="cuda")
+        vo = torch.empty_like(ko)
+        for _ in range(10):
+            sp.kv_gather(ko, vo, kp, vp, lay, table, tokens)
         torch.cuda.synchronize()
-        print(json.dumps({"calibrate_copy_bytes": src.numel(), "copies": 10}), flush=True)
+        print(json.dumps({"calibrate_copy_bytes": src.numel(), "copies": 10,
+                          "gather_read_bytes": 2 * kp.numel() * 2, "gathers": 10}), flush=True)
+        return
+    if args.mixed_only:
+        print(json.dumps({"C4_mixed": time_mixed_c4(args.steps, args.warmup)}), flush=True)
+        return
+    if args.flash_only:
+        print(json.dumps({"flash_f32": time_flash_f32(args.steps, args.warmup)}), flush=True)
         return
     if args.prefill_only:
         _, pf = time_prefill_c3(args.steps, args.warmup)

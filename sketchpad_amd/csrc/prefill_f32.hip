@@ -29,6 +29,9 @@ namespace sp {
 namespace {
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+// Tile chunks in the native vector type: arrays of HIP's float4 struct are copied with memcpy,
+// which keeps them in scratch memory and makes every load wait as soon as it is issued.
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kF32BN = 32;  // keys per tile
 
@@ -44,8 +47,10 @@ struct F32Cfg {
   static constexpr int TILE_K = kF32BN * PITCH_K;
   static constexpr int BUF = TILE_K + kF32BN * PITCH_V;  // K tile then V tile
   static constexpr int CPR = D / 4;                 // float4 chunks per K row
-  static constexpr int LOADS_K = (kF32BN * CPR + 255) / 256;       // per thread per K tile
-  static constexpr int LOADS_V = (kF32BN * DB * 8 + 255) / 256;    // at most, per V tile
+  static constexpr int CPRV = DB * 8;               // float4 chunks per (padded) V row
+  static constexpr int LOADS_K = (kF32BN * CPR + 255) / 256;  // per thread per K tile
+  static constexpr int LOADS_V = kF32BN * CPRV / 256;         // per thread per V tile
+  static_assert(LOADS_V * 256 == kF32BN * CPRV, "V tile load split");
 };
 
 __device__ __forceinline__ f32x16 mfma_f32(float a, float b, f32x16 c) {
@@ -60,7 +65,7 @@ __device__ __forceinline__ void swap_halves_f32(float x, float& a, float& b) {
 }
 
 template <int D, int DB, bool PAGED>
-__global__ void __launch_bounds__(256, (DB >= 8 || D >= 256) ? 1 : 2) prefill_f32_kernel(PrefillArgs a) {
+__global__ void __launch_bounds__(256, (DB >= 8 || D >= 256 || (D >= 160 && DB >= 4)) ? 1 : 2) prefill_f32_kernel(PrefillArgs a) {
   using C = F32Cfg<D, DB>;
   constexpr int BN = kF32BN, CPR = C::CPR;
   constexpr int PITCH_K = C::PITCH_K, PITCH_V = C::PITCH_V;
@@ -68,7 +73,7 @@ __global__ void __launch_bounds__(256, (DB >= 8 || D >= 256) ? 1 : 2) prefill_f3
   static_assert(D % 8 == 0, "the QK steps split a row into two halves of float4 chunks");
   __shared__ __attribute__((aligned(16))) float lds[2][C::BUF];
   const int dv = a.dv;           // value head dim (<= 32 DB, a multiple of 4)
-  const int cprv = dv / 4;       // float4 chunks per V row
+  const int last_v = dv / 4 - 1; // last float4 chunk of a V row in memory
 
   // ---- workgroup -> (kv head, group member, sequence, query block), heavy query blocks first
   int id = blockIdx.x;
@@ -144,7 +149,11 @@ __global__ void __launch_bounds__(256, (DB >= 8 || D >= 256) ? 1 : 2) prefill_f3
   }
 
   // ---- tile loads: thread tid moves float4 chunk (tid + 256 u) of the K tile and of the V tile;
-  // rows outside [kv_lo, kv_hi) are clamped to a valid row (their scores are masked).
+  // rows outside [kv_lo, kv_hi) are clamped to a valid row (their scores are masked). Every load
+  // is unconditional (a load under a condition makes the compiler wait for all outstanding loads
+  // before each tile): chunks past the K tile (head dims 40, 80) repeat its last row, and V
+  // chunks past the value head dim repeat the row's last chunk into LDS columns that only feed
+  // output columns which are never stored.
   auto row_src = [&](int j, bool is_v) __attribute__((always_inline)) {
     j = min(max(j, kv_lo), kv_hi - 1);
     if constexpr (PAGED) {
@@ -156,29 +165,42 @@ __global__ void __launch_bounds__(256, (DB >= 8 || D >= 256) ? 1 : 2) prefill_f3
       return is_v ? vbase + (int64_t)j * a.v_tok * 4 : kbase + (int64_t)j * a.kv_tok * 4;
     }
   };
-  float4 kreg[C::LOADS_K], vreg[C::LOADS_V];
+  f32x4 kreg[C::LOADS_K], vreg[C::LOADS_V];
+  auto k_chunk = [&](int u, int& r, int& c) __attribute__((always_inline)) {
+    const int ch = tid + 256 * u;
+    r = ch / CPR;
+    c = ch % CPR;
+    if constexpr (C::LOADS_K * 256 != BN * CPR) {
+      if (r >= BN) {
+        r = BN - 1;
+        c = ch % CPR;  // the same (row, chunk) as another thread: an identical LDS store
+      }
+    }
+  };
   auto load_tile = [&](int t0) __attribute__((always_inline)) {
 #pragma unroll
     for (int u = 0; u < C::LOADS_K; ++u) {
-      const int ch = tid + 256 * u, r = ch / CPR, c = ch % CPR;
-      if (ch < BN * CPR) kreg[u] = *(const float4*)(row_src(t0 + r, false) + c * 16);
+      int r, c;
+      k_chunk(u, r, c);
+      kreg[u] = *(const f32x4*)(row_src(t0 + r, false) + c * 16);
     }
 #pragma unroll
     for (int u = 0; u < C::LOADS_V; ++u) {
-      const int ch = tid + 256 * u, r = ch / cprv, c = ch % cprv;
-      if (ch < BN * cprv) vreg[u] = *(const float4*)(row_src(t0 + r, true) + c * 16);
+      const int ch = tid + 256 * u, r = ch / C::CPRV, c = min(ch % C::CPRV, last_v);
+      vreg[u] = *(const f32x4*)(row_src(t0 + r, true) + c * 16);
     }
   };
   auto store_tile = [&](float* buf) __attribute__((always_inline)) {
 #pragma unroll
     for (int u = 0; u < C::LOADS_K; ++u) {
-      const int ch = tid + 256 * u, r = ch / CPR, c = ch % CPR;
-      if (ch < BN * CPR) *(float4*)(buf + r * PITCH_K + 4 * c) = kreg[u];
+      int r, c;
+      k_chunk(u, r, c);
+      *(f32x4*)(buf + r * PITCH_K + 4 * c) = kreg[u];
     }
 #pragma unroll
     for (int u = 0; u < C::LOADS_V; ++u) {
-      const int ch = tid + 256 * u, r = ch / cprv, c = ch % cprv;
-      if (ch < BN * cprv) *(float4*)(buf + C::TILE_K + r * PITCH_V + 4 * c) = vreg[u];
+      const int ch = tid + 256 * u, r = ch / C::CPRV, c = ch % C::CPRV;
+      *(f32x4*)(buf + C::TILE_K + r * PITCH_V + 4 * c) = vreg[u];
     }
   };
 
@@ -291,10 +313,11 @@ __global__ void __launch_bounds__(256, (DB >= 8 || D >= 256) ? 1 : 2) prefill_f3
   __syncthreads();
   int cur = 0;
   for (int t0 = t_first; t0 < kv_hi; t0 += BN) {
-    const bool more = t0 + BN < kv_hi;
-    if (more) load_tile(t0 + BN);
+    // unconditional: past the last tile the rows clamp to the last key and the copy lands in
+    // the buffer nobody reads again
+    load_tile(t0 + BN);
     if (visits(t0)) compute_tile(t0, lds[cur]);
-    if (more) store_tile(lds[cur ^ 1]);
+    store_tile(lds[cur ^ 1]);
     __syncthreads();
     cur ^= 1;
   }
