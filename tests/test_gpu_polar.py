@@ -7,7 +7,10 @@ against the oracle's restatement of polar_quant_compress / polar_quant_decompres
     rounded once for bf16 / f16;
   - the pool layout documented in the header is read back on the host and equals the export;
   - decode attention on the codes matches float64 attention over the oracle-decompressed keys and
-    values (the reference's CompressedKvCache + forward_cached), within the 16-bit tolerance."""
+    values (the reference's CompressedKvCache + forward_cached): within 2e-2 absolute on
+    unit-scale data, and on data with row norms spread over e^(0.5 N(0,1)) within a per-output
+    bound derived from the kernel's rounding points (polar_error_bound), with the worst measured
+    error and its ratio to the bound printed."""
 import numpy as np
 import pytest
 import torch
@@ -181,7 +184,7 @@ def test_gather_out_of_pool_block_gives_zeros():
 # --- decode on the codes ----------------------------------------------------------------------
 
 def _polar_decode_case(seed, *, lens, hq, hkv, d, bs, dtype, window=-1, num_layers=1, layer=0,
-                       spare_blocks=3, q_scale=1.0):
+                       spare_blocks=3, q_scale=1.0, row_spread=0.5):
     announce(f"polar decode seed={seed} B={len(lens)} Hq={hq} Hkv={hkv} D={d} BS={bs} {dtype} "
              f"window={window} maxL={max(lens)} layer={layer}/{num_layers}")
     rng = np.random.default_rng(seed)
@@ -195,9 +198,9 @@ def _polar_decode_case(seed, *, lens, hq, hkv, d, bs, dtype, window=-1, num_laye
     g = torch.Generator(device="cuda").manual_seed(seed)
     dt = DT[dtype]
     k = (torch.randn(T, hkv, d, generator=g, device="cuda") *
-         torch.exp(torch.randn(T, hkv, 1, generator=g, device="cuda") * 0.5)).to(dt)
+         torch.exp(torch.randn(T, hkv, 1, generator=g, device="cuda") * row_spread)).to(dt)
     v = (torch.randn(T, hkv, d, generator=g, device="cuda") *
-         torch.exp(torch.randn(T, hkv, 1, generator=g, device="cuda") * 0.5)).to(dt)
+         torch.exp(torch.randn(T, hkv, 1, generator=g, device="cuda") * row_spread)).to(dt)
     q = (torch.randn(len(lens), hq, d, generator=g, device="cuda") * q_scale).to(dt)
     kp, vp = sp.alloc_polar_pools(lay)
     slot_d = torch.from_numpy(slots).cuda()
@@ -219,22 +222,72 @@ def _polar_decode_case(seed, *, lens, hq, hkv, d, bs, dtype, window=-1, num_laye
     olay = O.make_layout(nblk, num_layers, layer, hkv, bs, d)
     ref = O.paged_decode_f64(q.float().cpu().numpy(), kpool, vpool, olay, tables, lens,
                              scale=d ** -0.5, window_left=window, dtype=O.F32)
-    # the largest decompressed value each sequence attends (its output's natural magnitude)
-    offs = np.concatenate([[0], np.cumsum(lens)])  # tokens are appended sequence by sequence
-    vmax = np.array([np.abs(vd[offs[s]:offs[s + 1]]).max() if lens[s] > 0 else 0.0
-                     for s in range(len(lens))])
-    return as_f64(out), ref, vmax
+    bound = polar_error_bound(q.float().cpu().numpy(), k.float().cpu().numpy(),
+                              v.float().cpu().numpy(), kd, vd, lens, hq, window, dtype)
+    return as_f64(out), ref, bound
 
 
-def assert_scaled_close(got, ref, vmax, what):
-    """16-bit bar scaled to the data: |err| <= 2e-2 * max(1, max |V|) per sequence. The kernel
-    rounds P' = p |v|/7 to bf16 and the output to the storage type, each a relative 2^-9, so its
-    error grows with the magnitude of the values it averages; 2e-2 absolute is the bar for
-    unit-scale values."""
+def polar_error_bound(q, k, v, kd, vd, lens, hq, window, dtype):
+    """Per-output bound [B, Hq, D] on |kernel - float64 attention over the decompressed K/V|,
+    from the rounding points of polar_decode_kernel (tokens appended sequence by sequence):
+
+      1. P'_j = p_j |v_j| is rounded to bf16 (unit roundoff 2^-8) before the PV MFMA; the bias
+         row sums the same rounded P', so the error left is sum_j (P'_j~ - P'_j) n_jd / 7, at
+         most 2^-8 * A_d with A_d = sum_j w_j |v_jd| (w the exact softmax weights).
+      2. The raw score q . n_j is accumulated in fp32 from -136 sum(q) over D/32 MFMA steps, each
+         partial sum below 143 sum|q|: |error| <= (D/32 + 2) * 2 * 2^-24 * 143 * sum|q|, then
+         times |k_j|/7 * scale; the fp32 scale product, the exp2 and the offset add a few ulp.
+         A score error eps moves each normalised weight by a factor within e^(+-2 eps).
+      3. The PV accumulation in fp32 over L/64 + 16 MFMA steps of terms below P'_j * 143, the
+         four-wave and split merges, and the f32 rounding of the oracle's decompressed values:
+         (L/64 + 40) * 2^-24 * (143/7) * sum_j w_j |v_j|.
+      4. The output is rounded once to the storage type (2^-8 bf16, 2^-11 f16).
+    Norms are the vectors' binary16 norms (|x| rounded to binary16, times 1 + 2^-10)."""
+    B, D = len(lens), q.shape[-1]
+    hkv = k.shape[1]
+    G = hq // hkv
+    scale = D ** -0.5
+    u32, u_p = 2.0 ** -24, 2.0 ** -8
+    u_out = {"bf16": 2.0 ** -8, "f16": 2.0 ** -11}[dtype]
+    knorm = np.float16(np.sqrt((k.astype(np.float64) ** 2).sum(-1))).astype(np.float64)
+    vnorm = np.float16(np.sqrt((v.astype(np.float64) ** 2).sum(-1))).astype(np.float64)
+    knorm *= 1 + 2.0 ** -10
+    vnorm *= 1 + 2.0 ** -10
+    offs = np.concatenate([[0], np.cumsum(lens)])
+    bound = np.zeros((B, hq, D))
+    for s in range(B):
+        L = int(lens[s])
+        if L == 0:
+            continue
+        lo = offs[s] + (0 if window < 0 else max(0, L - 1 - window))
+        hi = offs[s] + L
+        for h in range(hq):
+            kh = h // G
+            qh = q[s, h].astype(np.float64)
+            sc = (kd[lo:hi, kh].astype(np.float64) @ qh) * scale
+            w = np.exp(sc - sc.max())
+            w /= w.sum()
+            A = w @ np.abs(vd[lo:hi, kh].astype(np.float64))
+            raw = (D / 32 + 2) * 2 * u32 * 143 * np.abs(qh).sum()
+            eps = (raw * knorm[lo:hi, kh] / 7 * scale).max()
+            eps += 8 * u32 * (np.abs(sc).max() + 1) + 4 * u32
+            eps += 4 * u32 * scale * (np.abs(kd[lo:hi, kh]) @ np.abs(qh)).max()
+            acc = (L / 64 + 40) * u32 * (143 / 7) * (w @ vnorm[lo:hi, kh])
+            pre = u_p * A + np.expm1(2 * eps) * A + acc
+            bound[s, h] = pre + u_out * (np.abs(w @ vd[lo:hi, kh].astype(np.float64)) + pre)
+    return bound
+
+
+def assert_within_bound(got, ref, bound, what):
+    """|got - ref| <= bound for every output; prints the worst error and its ratio to the bound."""
     assert np.isfinite(got).all(), f"{what}: non-finite output"
-    err = np.abs(got - ref).reshape(len(vmax), -1).max(1)
-    lim = LOWP_ABS_TOL * np.maximum(1.0, vmax)
-    assert (err <= lim).all(), f"{what}: errors {err} > limits {lim}"
+    err = np.abs(got - ref)
+    ratio = (err / np.maximum(bound, 1e-300)).max()
+    print(f"[polar-bound] {what}: worst |err| {err.max():.3e}, worst err/bound {ratio:.3f}, "
+          f"largest bound {bound.max():.3e}", flush=True)
+    bad = err > bound
+    assert not bad.any(), (f"{what}: {int(bad.sum())} outputs beyond the derived bound, e.g. "
+                           f"err {err[bad][:4]} > bound {bound[bad][:4]}")
 
 
 @pytest.mark.parametrize("dtype", ["bf16", "f16"])
@@ -243,37 +296,54 @@ def assert_scaled_close(got, ref, vmax, what):
 def test_polar_decode_shapes(dtype, hq, hkv, d):
     rng = np.random.default_rng(hq * 31 + hkv + d)
     lens = rng.integers(1, 300, 5)
-    got, ref, vmax = _polar_decode_case(hq * 31 + hkv + d, lens=lens, hq=hq, hkv=hkv, d=d,
+    got, ref, bound = _polar_decode_case(hq * 31 + hkv + d, lens=lens, hq=hq, hkv=hkv, d=d,
                                         bs=16, dtype=dtype)
-    assert_scaled_close(got, ref, vmax, f"polar decode {dtype} {hq}/{hkv} D={d}")
+    assert_within_bound(got, ref, bound, f"polar decode {dtype} {hq}/{hkv} D={d}")
 
 
 def test_polar_decode_edge_lengths_and_windows():
     lens = [1, 2, 15, 16, 17, 31, 32, 33, 255, 256, 257, 1023, 1024, 1025]
-    got, ref, vmax = _polar_decode_case(5, lens=lens, hq=32, hkv=8, d=128, bs=16, dtype="bf16")
-    assert_scaled_close(got, ref, vmax, "edge lengths")
+    got, ref, bound = _polar_decode_case(5, lens=lens, hq=32, hkv=8, d=128, bs=16, dtype="bf16")
+    assert_within_bound(got, ref, bound, "edge lengths")
     for window in (0, 15, 16, 100):
-        got, ref, vmax = _polar_decode_case(6 + window, lens=lens[::2], hq=16, hkv=4, d=128,
+        got, ref, bound = _polar_decode_case(6 + window, lens=lens[::2], hq=16, hkv=4, d=128,
                                             bs=16, dtype="bf16", window=window)
-        assert_scaled_close(got, ref, vmax, f"window {window}")
+        assert_within_bound(got, ref, bound, f"window {window}")
 
 
 def test_polar_decode_long_contexts_many_splits():
-    got, ref, vmax = _polar_decode_case(11, lens=[5000, 9000, 7123], hq=32, hkv=8, d=128, bs=16,
+    got, ref, bound = _polar_decode_case(11, lens=[5000, 9000, 7123], hq=32, hkv=8, d=128, bs=16,
                                         dtype="bf16")
-    assert_scaled_close(got, ref, vmax, "long contexts")
+    assert_within_bound(got, ref, bound, "long contexts")
 
 
 def test_polar_decode_multi_layer_block32_and_zero_length():
-    got, ref, vmax = _polar_decode_case(12, lens=[0, 40, 700, 0, 33], hq=16, hkv=4, d=64, bs=32,
+    got, ref, bound = _polar_decode_case(12, lens=[0, 40, 700, 0, 33], hq=16, hkv=4, d=64, bs=32,
                                         dtype="f16", num_layers=3, layer=2)
     assert (got[0] == 0).all() and (got[3] == 0).all()
-    assert_scaled_close(got, ref, vmax, "multi-layer / block 32 / empty")
+    assert_within_bound(got, ref, bound, "multi-layer / block 32 / empty")
 
 
 def test_polar_decode_large_query_scale():
     """Sharp softmax (large scores): the bias removal happens before the scale, so the scores
-    stay exact enough for a near-argmax distribution."""
-    got, ref, vmax = _polar_decode_case(13, lens=[100, 333], hq=8, hkv=2, d=128, bs=16,
+    stay exact enough for a near-argmax distribution (the score term of the bound grows with
+    sum|q|)."""
+    got, ref, bound = _polar_decode_case(13, lens=[100, 333], hq=8, hkv=2, d=128, bs=16,
                                         dtype="bf16", q_scale=8.0)
-    assert_scaled_close(got, ref, vmax, "sharp softmax")
+    assert_within_bound(got, ref, bound, "sharp softmax")
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f16"])
+@pytest.mark.parametrize("hq,hkv,d", [(32, 8, 128), (28, 4, 128), (16, 2, 64)])
+def test_polar_decode_unit_scale_holds_abs_bar(dtype, hq, hkv, d):
+    """Unit-scale K/V (N(0, 1) rows, no norm spread), C2's length range U[512, 4096] plus three
+    short contexts: the plain 16-bit bar, 2e-2 absolute, on every output, besides the derived
+    bound. (A one-token context is left to the bound: its output is one value row taken through
+    two 16-bit roundings, bf16 P' and the output, up to 2^-7 of |v| ~ 3.)"""
+    rng = np.random.default_rng(hq + d)
+    lens = np.concatenate([[16, 17, 100], rng.integers(512, 4097, 13)])
+    got, ref, bound = _polar_decode_case(40 + hq + d, lens=lens, hq=hq, hkv=hkv, d=d, bs=16,
+                                         dtype=dtype, row_spread=0.0)
+    assert_within_bound(got, ref, bound, f"unit scale {dtype} {hq}/{hkv} D={d}")
+    err = np.abs(got - ref).max()
+    assert err <= LOWP_ABS_TOL, f"unit scale: abs error {err:.3e} > {LOWP_ABS_TOL}"
