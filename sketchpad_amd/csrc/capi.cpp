@@ -209,9 +209,13 @@ size_t sp_paged_decode_workspace_size(int32_t num_seqs, int32_t num_q_heads,
   if (!layout || layout->num_kv_heads <= 0 || num_seqs <= 0 || num_q_heads <= 0 ||
       max_context_len <= 0)
     return 0;
+  // one size for both pool kinds: the larger of the dense and the PolarQuant plans
   const DecodePlan p = plan_decode(num_seqs, num_q_heads, layout->num_kv_heads, layout->head_dim,
-                                   max_context_len, window_left);
-  return p.ws_bytes;
+                                   max_context_len, window_left, DecodeKind::Dense);
+  const DecodePlan pq = plan_decode(num_seqs, num_q_heads, layout->num_kv_heads,
+                                    layout->head_dim, max_context_len, window_left,
+                                    DecodeKind::Polar);
+  return p.ws_bytes > pq.ws_bytes ? p.ws_bytes : pq.ws_bytes;
 }
 
 // Validation and arguments shared by the dense and the PolarQuant decode entry points. The pool
@@ -222,7 +226,7 @@ static int decode_setup(const char* fn, void* out, const void* q, const void* k_
                         const int32_t* context_lens, int32_t max_context_len, int32_t num_seqs,
                         int32_t num_q_heads, float scale, int32_t window_left, sp_dtype dtype,
                         void* workspace, size_t workspace_bytes, DecodeArgs* a,
-                        int max_tps = 32, int cap = 64) {
+                        DecodeKind kind = DecodeKind::Dense) {
   if (int rc = check_layout(layout, fn)) return rc;
   if (int rc = check_dtype(dtype, fn)) return rc;
   if (num_seqs < 0 || num_q_heads <= 0 || max_context_len < 0 || max_blocks_per_seq < 0)
@@ -251,7 +255,7 @@ static int decode_setup(const char* fn, void* out, const void* q, const void* k_
   if (!isfinite(scale)) return fail(SP_EINVAL, "%s: scale is not finite", fn);
   const DecodePlan p =
       plan_decode(num_seqs, num_q_heads, hkv, D, max_context_len < 1 ? 1 : max_context_len,
-                  window_left, max_tps, cap);
+                  window_left, kind);
   if (layout->block_size % p.tt != 0)
     return fail(SP_EUNSUPPORTED, "%s: block_size %d is not a multiple of the %d-token tile", fn,
                 layout->block_size, p.tt);
@@ -307,8 +311,12 @@ int sp_paged_decode_noalloc(void* out, const void* q, const void* k_pool, const 
   const char* fn = "sp_paged_decode_noalloc";
   // The split plan (and so the partials' size) is sp_paged_decode's for the same shape, so both
   // entry points run the same kernels on the same split boundaries.
-  const size_t need = sp_paged_decode_workspace_size(num_seqs, num_q_heads, max_context_len,
-                                                     window_left, layout);
+  size_t need = 0;
+  if (layout && layout->num_kv_heads > 0 && num_seqs > 0 && num_q_heads > 0 &&
+      max_context_len > 0)
+    need = plan_decode(num_seqs, num_q_heads, layout->num_kv_heads, layout->head_dim,
+                       max_context_len, window_left, DecodeKind::Dense)
+               .ws_bytes;
   if (need > kDecodeScratchBytes)
     return fail(SP_ENOSPACE,
                 "%s: this batch needs %zu bytes of split partials, past the library's %zu-byte "
@@ -780,11 +788,10 @@ int sp_polar_paged_decode(void* out, const void* q, const void* k_pool, const vo
     return fail(dtype == SP_F32 ? SP_EUNSUPPORTED : SP_EINVAL,
                 "%s: dtype %d has no kernel (bf16, f16)", fn, (int)dtype);
   DecodeArgs a{};
-  // a compressed tile is a quarter of a dense one: splits of up to 64 tiles (never more splits
-  // than the dense plan, so sp_paged_decode_workspace_size covers this call too)
+  // the PolarQuant split plan (sp_paged_decode_workspace_size covers both plans)
   if (int rc = decode_setup(fn, out, q, k_pool, v_pool, layout, block_tables, max_blocks_per_seq,
                             context_lens, max_context_len, num_seqs, num_q_heads, scale,
-                            window_left, dtype, workspace, workspace_bytes, &a, 64, 128))
+                            window_left, dtype, workspace, workspace_bytes, &a, DecodeKind::Polar))
     return rc;
   if (num_seqs == 0) return SP_OK;
   polar_strides(layout, &a.block_stride_b, &a.layer_off_b);

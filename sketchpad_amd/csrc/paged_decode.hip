@@ -204,11 +204,13 @@ __global__ void __launch_bounds__(64 * kDecodeWaves, decode_min_waves<T>())
   char* vst = smem + wave * C::WAVE_LDS;
 
   // Block ids of this split's tiles, fetched once up front: lane j holds the block of tile
-  // t_begin + j (tps <= 64), so no tile load waits on a dependent block-table read.
-  int my_blk = 0;
+  // t_begin + j in blk0 and of tile t_begin + 64 + j in blk1 (tps <= 128), so no tile load waits
+  // on a dependent block-table read.
+  int blk0 = 0, blk1 = 0;
   {
-    const int tj = t_begin + lane;
-    if (lane < t_end - t_begin) my_blk = table[(tj * kTile) / a.block_size];
+    const int n_tiles = t_end - t_begin;
+    if (lane < n_tiles) blk0 = table[((t_begin + lane) * kTile) / a.block_size];
+    if (lane + 64 < n_tiles) blk1 = table[((t_begin + 64 + lane) * kTile) / a.block_size];
   }
 
   // Tile loads. K in MFMA A-operand order (token n, 16 bytes at c*64 + g*16); V coalesced
@@ -222,7 +224,10 @@ __global__ void __launch_bounds__(64 * kDecodeWaves, decode_min_waves<T>())
   };
   auto load_tile = [&](int t, uint4* kr, uint4* vr, bool& ok) {
     const int pos0 = t * kTile;
-    const int blk = __builtin_amdgcn_readlane(my_blk, t - t_begin);
+    const int ti = t - t_begin;  // wave-uniform, < tps
+    const int b0 = __builtin_amdgcn_readlane(blk0, ti & 63);
+    const int b1 = __builtin_amdgcn_readlane(blk1, ti & 63);
+    const int blk = ti < 64 ? b0 : b1;
     ok = blk >= 0 && blk < a.num_blocks;
     const int64_t base = (int64_t)(ok ? blk : 0) * a.block_stride_b + head_off +
                          (int64_t)(pos0 % a.block_size) * RB;
@@ -455,7 +460,7 @@ __global__ void __launch_bounds__(64) decode_combine_kernel(DecodeArgs a) {
 }
 
 DecodePlan plan_decode(int num_seqs, int hq, int hkv, int head_dim, int max_context_len,
-                       int window_left, int max_tps, int cap) {
+                       int window_left, DecodeKind kind) {
   DecodePlan p{};
   p.group = hkv > 0 ? hq / hkv : 0;
   p.tt = kTile;
@@ -465,14 +470,39 @@ DecodePlan plan_decode(int num_seqs, int hq, int hkv, int head_dim, int max_cont
     if (wt < max_tiles) max_tiles = wt;
   }
   p.max_tiles = max_tiles < 1 ? 1 : max_tiles;
-  int tps = max_tps < kDecodeWaves ? kDecodeWaves : (max_tps > cap ? cap : max_tps);
-  {
-    // Halve the split while the batch launches fewer than 2048 workgroups, but not below
-    // 32 tiles (512 tokens) once there are 512 (two per CU): shorter splits then only add
-    // per-workgroup start-up and partials to merge (measured on the windowed C5 batch: 128
-    // (sequence, KV head) units, 16-tile splits 53.8 us, 32-tile 49.5 us).
-    const int64_t units = (int64_t)num_seqs * (hkv > 0 ? hkv : 1);
-    auto wgs = [&](int t) { return units * ((p.max_tiles + t - 1) / t); };
+  // Workgroups the batch launches with splits of t tiles if every sequence spanned max_tiles
+  // (the host does not read the context lengths).
+  const int64_t units = (int64_t)num_seqs * (hkv > 0 ? hkv : 1);
+  auto wgs = [&](int t) { return units * ((p.max_tiles + t - 1) / t); };
+  int tps;
+  if (kind == DecodeKind::Dense) {
+    // A rule fitted to measurements (24 batches: groups 1-16, 64-1024 units, contexts of
+    // 256-16k tokens, windowed and not; it is within 2 % of the best of 32 / 64 / 128 tiles on
+    // each, where one fixed length loses up to 20 %):
+    //  - 64 tiles (1024 tokens) by default;
+    //  - batches that would launch fewer than two workgroups per CU (256 CUs) with 64-tile
+    //    splits take 32, halved while they still launch fewer;
+    //  - 128 when that plan launches 384-512 workgroups: its longest splits then fill the GPU
+    //    about once and a half to twice, with the fewest partials to merge (the windowed
+    //    Mistral batch, 16-head groups, 256 units of 4k-token contexts);
+    //  - 32 for groups of at most 4 query heads over contexts of 129-256 tiles with 512 or
+    //    more units, where the short per-tile work leaves the merge cheap and finer splits
+    //    balance the ragged lengths better (Llama-3-8B at 64 sequences: 104 against 106 us).
+    tps = 64;
+    if (wgs(64) < 512) {
+      tps = 32;
+      while (tps > kDecodeWaves && wgs(tps) < 512) tps /= 2;
+    } else if (wgs(128) >= 384 && wgs(128) <= 512) {
+      tps = 128;
+    } else if (p.group <= 4 && units >= 512 && p.max_tiles > 128 && p.max_tiles <= 256) {
+      tps = 32;
+    }
+  } else {
+    // Compressed tiles are a quarter of a dense one's bytes: start from 64-tile splits and halve
+    // while the batch launches fewer than 2048 workgroups, but not below 32 tiles once it
+    // launches 512 (two per CU); shorter splits then only add per-workgroup start-up and
+    // partials to merge.
+    tps = 64;
     while (tps > kDecodeWaves && wgs(tps) < 2048 && !(tps <= 32 && wgs(tps) >= 512))
       tps = tps / 2 < kDecodeWaves ? kDecodeWaves : tps / 2;
   }

@@ -17,11 +17,13 @@ struct DecodePlan {
   size_t ws_bytes;      // fp32 partials [num_seqs][Hq][max_splits][D + 4]
 };
 
-// max_tps: the largest split (in 16-token tiles) the kernel should take; a split is halved
-// while the batch would launch fewer than 2048 workgroups, down to 32 tiles once it launches at
-// least 512. cap: the most tiles per split the kernel can hold.
+enum class DecodeKind { Dense, Polar };
+
+// The split plan of a decode call, a function of the batch shape only: tiles per split (at most
+// 128, the block ids one workgroup prefetches), the splits a sequence can span and the
+// partials' bytes. Dense and PolarQuant pools have rules of their own.
 DecodePlan plan_decode(int num_seqs, int hq, int hkv, int head_dim, int max_context_len,
-                       int window_left, int max_tps = 32, int cap = 64);
+                       int window_left, DecodeKind kind);
 
 struct DecodeArgs {
   void* out;

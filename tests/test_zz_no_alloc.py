@@ -57,7 +57,8 @@ def test_noalloc_decode_matches_workspace_decode_twice():
 
 
 def test_noalloc_decode_rejects_batches_past_the_scratch():
-    """256 sequences x 32 heads x 32k keys need ~276 MB of partials: SP_ENOSPACE, no launch."""
+    """256 sequences x 32 heads x 32k keys need 138 MB of partials (32 splits of 64 tiles):
+    SP_ENOSPACE, no launch."""
     lay = sp.layout(16, 1, 0, 8, 16, 128)
     need = sp.paged_decode_workspace_size(256, 32, 32768, -1, lay)
     assert need > 32 << 20
