@@ -217,41 +217,73 @@ void spo_attention_f64_v(const void* q, int64_t q_tok, int64_t q_head, const voi
                          double scale, const float* mask, int causal, int64_t q_pos0,
                          int64_t window_left, int dtype, double* out) {
   const int rep = hq / hkv; /* repeat_kv: head h reads KV head h / rep (transformer.rs:263-270) */
-  double* s = (double*)malloc(sizeof(double) * (size_t)(lk > 0 ? lk : 1));
-  for (int h = 0; h < hq; ++h) {
-    const int g = h / rep;
-    for (int64_t i = 0; i < sq; ++i) {
-      double m = -INFINITY;
-      for (int64_t j = 0; j < lk; ++j) {
-        double acc = 0.0;
-        for (int c = 0; c < d; ++c)
-          acc += (double)load_elem(q, i * q_tok + h * q_head + c, dtype) *
-                 (double)load_elem(k, j * k_tok + g * k_head + c, dtype);
-        acc *= scale; /* scale after the product (transformer.rs:234-235) */
-        if (mask)
-          acc += (double)mask[i * lk + j];
-        else if (!visible(causal, q_pos0, window_left, i, j))
-          acc = -INFINITY;
-        s[j] = acc;
-        if (acc > m) m = acc;
+  /* Work items are (head, block of 64 query rows), spread over OpenMP threads. Each output row
+   * is still one sequential sum over the keys in ascending order, so the thread count does not
+   * change any result. Without an additive mask, keys the causal / window predicate hides are
+   * skipped: they would enter as exp(-inf) = 0 and change neither the maximum nor the sums. */
+  const int64_t rb = 64, nrb = (sq + rb - 1) / rb;
+#pragma omp parallel
+  {
+    double* s = (double*)malloc(sizeof(double) * (size_t)(lk > 0 ? lk : 1));
+    double* kd = (double*)malloc(sizeof(double) * (size_t)(lk > 0 ? lk : 1) * (size_t)d);
+    double* vd = (double*)malloc(sizeof(double) * (size_t)(lk > 0 ? lk : 1) * (size_t)dv);
+    double* qd = (double*)malloc(sizeof(double) * (size_t)d);
+    int g_have = -1;
+#pragma omp for schedule(dynamic, 1)
+    for (int64_t item = 0; item < (int64_t)hq * nrb; ++item) {
+      const int h = (int)(item / nrb);
+      const int64_t i0 = (item % nrb) * rb, i1 = i0 + rb < sq ? i0 + rb : sq;
+      const int g = h / rep;
+      if (g != g_have) { /* this KV head's rows, converted once per thread */
+        for (int64_t j = 0; j < lk; ++j) {
+          for (int c = 0; c < d; ++c)
+            kd[j * d + c] = (double)load_elem(k, j * k_tok + g * k_head + c, dtype);
+          for (int c = 0; c < dv; ++c)
+            vd[j * dv + c] = (double)load_elem(v, j * v_tok + g * v_head + c, dtype);
+        }
+        g_have = g;
       }
-      double* o = out + (i * hq + h) * dv;
-      for (int c = 0; c < dv; ++c) o[c] = 0.0;
-      if (m == -INFINITY) continue; /* no visible key (or no keys): zeros */
-      double sum = 0.0;
-      for (int64_t j = 0; j < lk; ++j) {
-        s[j] = exp(s[j] - m); /* softmax(dim 3), max-subtracted (transformer.rs:242) */
-        sum += s[j];
-      }
-      for (int64_t j = 0; j < lk; ++j) {
-        if (s[j] == 0.0) continue;
-        const double pj = s[j] / sum;
-        for (int c = 0; c < dv; ++c)
-          o[c] += pj * (double)load_elem(v, j * v_tok + g * v_head + c, dtype);
+      for (int64_t i = i0; i < i1; ++i) {
+        for (int c = 0; c < d; ++c) qd[c] = (double)load_elem(q, i * q_tok + h * q_head + c, dtype);
+        int64_t jlo = 0, jhi = lk; /* keys [jlo, jhi) can be visible */
+        if (!mask) {
+          const int64_t p = q_pos0 + i;
+          if (causal && p + 1 < jhi) jhi = p + 1 > 0 ? p + 1 : 0;
+          if (window_left >= 0 && p - window_left > jlo) jlo = p - window_left;
+          if (jlo > jhi) jlo = jhi;
+        }
+        double m = -INFINITY;
+        for (int64_t j = jlo; j < jhi; ++j) {
+          double acc = 0.0;
+          for (int c = 0; c < d; ++c) acc += qd[c] * kd[j * d + c];
+          acc *= scale; /* scale after the product (transformer.rs:234-235) */
+          if (mask)
+            acc += (double)mask[i * lk + j];
+          else if (!visible(causal, q_pos0, window_left, i, j))
+            acc = -INFINITY;
+          s[j] = acc;
+          if (acc > m) m = acc;
+        }
+        double* o = out + (i * hq + h) * dv;
+        for (int c = 0; c < dv; ++c) o[c] = 0.0;
+        if (m == -INFINITY) continue; /* no visible key (or no keys): zeros */
+        double sum = 0.0;
+        for (int64_t j = jlo; j < jhi; ++j) {
+          s[j] = exp(s[j] - m); /* softmax(dim 3), max-subtracted (transformer.rs:242) */
+          sum += s[j];
+        }
+        for (int64_t j = jlo; j < jhi; ++j) {
+          if (s[j] == 0.0) continue;
+          const double pj = s[j] / sum;
+          for (int c = 0; c < dv; ++c) o[c] += pj * vd[j * dv + c];
+        }
       }
     }
+    free(s);
+    free(kd);
+    free(vd);
+    free(qd);
   }
-  free(s);
 }
 
 void spo_attention_f32_refops(const void* q, int64_t q_tok, int64_t q_head, const void* k,

@@ -1,10 +1,10 @@
 """A mixed ragged batch (prompt chunks + one-token decode sequences over one paged pool) through
 sp_ragged_paged_attention, the entry point BatchedPagedAttention calls for every layer of a
 scheduler iteration: at the full C4 size (Qwen2.5-7B heads) and on a small
-batch with a window. Decode rows are checked against the oracle's paged decode (gather_kv then
-softmax(q k^T d^-1/2) v with no mask, llama.rs:255-260), chunk rows against f64 attention over
-the gathered context with prefill_causal_mask (llama.rs:374-388), and both halves bit for bit
-against the separate sp_paged_prefill / sp_paged_decode calls on the same data."""
+batch with a window. Every decode row is checked against the oracle's paged decode (gather_kv
+then softmax(q k^T d^-1/2) v with no mask, llama.rs:255-260), every chunk row against f64
+attention over the gathered context with prefill_causal_mask (llama.rs:374-388), and both halves
+bit for bit against the separate sp_paged_prefill / sp_paged_decode calls on the same data."""
 import numpy as np
 import pytest
 import torch
@@ -17,7 +17,7 @@ from tests.helpers import announce, as_f64, assert_attention_close, host_array, 
 pytestmark = pytest.mark.gpu
 
 
-def _run(w: W.MixedWorkload, sample_rows: int | None, window_left: int = -1):
+def _run(w: W.MixedWorkload, window_left: int = -1):
     t = W.make_mixed_tensors(w)
     lay = sp.layout(t["num_blocks"], 1, 0, w.hkv, w.block_size, w.head_dim)
     P, T0 = w.num_prefill_seqs, w.num_prefill_tokens
@@ -64,29 +64,22 @@ def _run(w: W.MixedWorkload, sample_rows: int | None, window_left: int = -1):
         ref = O.paged_decode_f64(q[T0:], kp, vp, olay, tables[P:], lens[P:], scale=scale,
                                  window_left=window_left, dtype=odt)
         assert_attention_close(got[T0:], ref, w.dtype, f"{w.name} decode rows")
-    # chunk rows: all of them, or first / last plus a seeded sample
+    # chunk rows: every row of every chunk (queries at positions L - lq .. L - 1)
     cu = w.cu_seqlens_q
-    rng = np.random.default_rng(0)
     for s in range(P):
         L, lq = int(lens[s]), int(w.chunk_lens[s])
         kg, vg = O.gather_kv(kp, vp, olay, tables[s], L)
         kt = np.ascontiguousarray(kg.transpose(1, 0, 2))
         vt = np.ascontiguousarray(vg.transpose(1, 0, 2))
-        rows = np.arange(lq) if sample_rows is None else np.unique(
-            np.concatenate([[0, lq - 1], rng.choice(lq, size=min(lq, sample_rows), replace=False)]))
-        for i in rows:
-            pos = L - lq + i
-            r = O.attention_f64(q[cu[s] + i:cu[s] + i + 1], kt[:pos + 1], vt[:pos + 1],
-                                scale=scale, causal=True, q_pos0=pos, window_left=window_left,
-                                dtype=odt)
-            assert_attention_close(got[cu[s] + i:cu[s] + i + 1], r, w.dtype,
-                                   f"{w.name} chunk {s} row {i}")
+        r = O.attention_f64(q[cu[s]:cu[s] + lq], kt, vt, scale=scale, causal=True,
+                            q_pos0=L - lq, window_left=window_left, dtype=odt)
+        assert_attention_close(got[cu[s]:cu[s] + lq], r, w.dtype, f"{w.name} chunk {s}")
 
 
 def test_ragged_c4_mixed_full_size():
     """C4: 4 chunks x 512 new tokens on contexts U[1024, 8192] + 128 decode sequences with
-    contexts U[256, 4096], one pool; every decode row, 32 sampled rows per chunk."""
-    _run(W.mixed_c4(), sample_rows=32)
+    contexts U[256, 4096], one pool; every decode row and every chunk row."""
+    _run(W.mixed_c4())
 
 
 @pytest.mark.parametrize("window", [-1, 100])
@@ -94,7 +87,7 @@ def test_ragged_small_mixed(window):
     w = W.MixedWorkload("mixed-small", 77, np.array([33, 2, 130], np.int32),
                         np.array([0, 500, 40], np.int32),
                         np.array([1, 17, 300, 64, 129], np.int32), 8, 2, 128, "bf16")
-    _run(w, sample_rows=None, window_left=window)
+    _run(w, window_left=window)
 
 
 def test_ragged_decode_only_and_prefill_only():
@@ -102,8 +95,8 @@ def test_ragged_decode_only_and_prefill_only():
     only_dec = W.MixedWorkload("mixed-decode-only", 78, np.zeros(0, np.int32),
                                np.zeros(0, np.int32), np.array([5, 40, 200], np.int32),
                                8, 2, 64, "bf16")
-    _run(only_dec, sample_rows=None)
+    _run(only_dec)
     only_pre = W.MixedWorkload("mixed-prefill-only", 79, np.array([7, 64], np.int32),
                                np.array([10, 0], np.int32), np.zeros(0, np.int32),
                                8, 2, 64, "bf16")
-    _run(only_pre, sample_rows=None)
+    _run(only_pre)
