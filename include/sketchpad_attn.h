@@ -258,16 +258,21 @@ int sp_paged_prefill(void* out, const void* q,
  * causal rule of prefill_causal_mask, llama.rs:374-388); sequences [num_prefill_seqs, num_seqs)
  * add one token each: decode (sp_paged_decode, no mask, llama.rs:255-260). Replaces the
  * per-sequence forward_cached calls of one scheduler iteration (transformer.rs:184-254 with
- * start_pos and the mask chosen per sequence as Llama::forward does, llama.rs:247-260) with two
- * launches on `stream`, chunks first.
+ * start_pos and the mask chosen per sequence as Llama::forward does, llama.rs:247-260). With
+ * both groups present the decode runs on a library-owned side stream of the current device
+ * (created on first use, default priority), forked from `stream` and joined back into it with
+ * events, so it overlaps the chunks' prefill; the call is ordered on `stream` like one launch
+ * (work after it on `stream` sees both halves) and can be captured into a graph.
  *   q, out          : [total_q, Hq, D], the chunks' tokens first (num_prefill_tokens of them),
  *                     then one token per decode sequence
  *   cu_seqlens_q    : [num_prefill_seqs + 1] token offsets of the chunks (device); may be NULL
  *                     when num_prefill_seqs == 0
  *   context_lens    : [num_seqs] (device), block_tables [num_seqs, max_blocks_per_seq] (device)
  *   prefill_max_seqlen_q, decode_max_context_len : bounds over the respective groups
- *   workspace       : sp_ragged_attention_workspace_size() bytes (the larger of the two calls'
- *                     needs; they share it, in stream order). Calls sharing it must not overlap.
+ *   workspace       : sp_ragged_attention_workspace_size() bytes: the decode's partials first
+ *                     (its need rounded up to 256 bytes), then the prefill's split partials
+ *                     (none when the prefill plan does not split). Calls sharing it must not
+ *                     overlap.
  */
 size_t sp_ragged_attention_workspace_size(int32_t num_seqs, int32_t num_prefill_seqs,
                                           int32_t prefill_max_seqlen_q,

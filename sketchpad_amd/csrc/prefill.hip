@@ -679,8 +679,11 @@ __global__ void __launch_bounds__(256) prefill_combine_kernel(PrefillArgs a) {
 }
 
 int plan_prefill_splits(int64_t base_wgs, int64_t max_ctx_tiles) {
-  if (base_wgs <= 0 || base_wgs >= 1024) return 1;
-  int64_t s = (1024 + base_wgs / 2) / base_wgs;
+  // A split pays for its partial records and merge only while it turns idle resident slots into
+  // shorter walks: past one round of workgroups the extra ones queue behind the first.
+  constexpr int64_t kResidentWgs = 2 * 256;
+  if (base_wgs <= 0 || base_wgs * 2 > kResidentWgs) return 1;
+  int64_t s = kResidentWgs / base_wgs;
   s = s > 8 ? 8 : s;
   const int64_t by_len = max_ctx_tiles / 16;
   s = s > by_len ? by_len : s;

@@ -53,8 +53,8 @@ struct PrefillArgs {
 };
 
 // Split count for a chunked prefill of base_wgs workgroups whose sequences span up to
-// max_ctx_tiles 64-key tiles: about 1024 workgroups in all, at least 16 tiles per split, at
-// most 8 splits.
+// max_ctx_tiles 64-key tiles: as many splits as keep the whole grid within one round of
+// resident workgroups (2 per CU on 256 CUs), at least 16 tiles per split, at most 8 splits.
 int plan_prefill_splits(int64_t base_wgs, int64_t max_ctx_tiles);
 size_t prefill_partials_bytes(int num_seqs, int max_seqlen_q, int hq, int head_dim, int nsplit);
 

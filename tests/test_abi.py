@@ -201,13 +201,18 @@ def test_flash_attention_ex_validation(sp_lib):
 
 
 def test_paged_prefill_workspace_size(sp_lib):
-    """Key splits are planned only for few query blocks over long contexts: C4's shape (4 x 512
-    queries, 28 heads, contexts up to 428 blocks of 16) gets 2 splits of fp32 (m, l, acc) records;
-    a C3-sized batch (2,496 query blocks) and short contexts get none."""
+    """Key splits are planned only while the split grid stays within one round of resident
+    workgroups (512), with at least 16 key tiles per split and at most 8 splits, as fp32
+    (m, l, acc) records: one 512-query chunk of 28 heads (112 workgroups) on a 32k context gets 4,
+    two 128-query chunks (56 workgroups) on contexts of up to 428 blocks of 16 get 107 / 16 = 6;
+    C4's shape (4 x 512 queries, 448 workgroups), a C3-sized batch and short contexts get none."""
     lay = _lib.layout(10_000, 1, 0, 4, 16, 128)
     rec = 128 + 4
-    assert sp_lib.sp_paged_prefill_workspace_size(4, 512, 28, ctypes.byref(lay), 428) == \
-        4 * 512 * 28 * 2 * rec * 4
+    assert sp_lib.sp_paged_prefill_workspace_size(1, 512, 28, ctypes.byref(lay), 2016) == \
+        1 * 512 * 28 * 4 * rec * 4
+    assert sp_lib.sp_paged_prefill_workspace_size(2, 128, 28, ctypes.byref(lay), 428) == \
+        2 * 128 * 28 * 6 * rec * 4
+    assert sp_lib.sp_paged_prefill_workspace_size(4, 512, 28, ctypes.byref(lay), 428) == 0
     lay32 = _lib.layout(10_000, 1, 0, 8, 16, 128)
     assert sp_lib.sp_paged_prefill_workspace_size(8, 1672, 32, ctypes.byref(lay32), 105) == 0
     assert sp_lib.sp_paged_prefill_workspace_size(4, 512, 28, ctypes.byref(lay), 10) == 0
@@ -224,7 +229,8 @@ def test_missing_library_fails_loudly(monkeypatch, tmp_path):
 
 def test_ragged_paged_attention_validation(sp_lib):
     """sp_ragged_paged_attention: the group split and pointers are checked before any launch;
-    the workspace is the larger of the two calls' needs."""
+    the workspace holds the decode's partials (rounded up to 256 bytes) followed by the
+    prefill's."""
     lay = _lib.layout(10_000, 1, 0, 4, 16, 128)
 
     def call(num_seqs=4, num_prefill=2, cu=1 << 20, tok=100):
@@ -236,11 +242,19 @@ def test_ragged_paged_attention_validation(sp_lib):
     assert call(tok=-1) == _lib.SP_EINVAL
     assert call(cu=None) == _lib.SP_EINVAL
     assert call(num_seqs=0, num_prefill=0) == _lib.SP_OK
-    # C4's shape: the chunks' split partials are larger than the decode partials
-    pre = sp_lib.sp_paged_prefill_workspace_size(4, 512, 28, ctypes.byref(lay), 547)
+    # C4's shape: the chunks do not split, so the decode partials are all
     dec = sp_lib.sp_paged_decode_workspace_size(128, 28, 4096, -1, ctypes.byref(lay))
-    both = sp_lib.sp_ragged_attention_workspace_size(132, 4, 512, 4096, 28, -1, ctypes.byref(lay),
-                                                     547)
-    assert both == max(pre, dec) > 0
+    assert dec > 0
+    dec_al = (dec + 255) // 256 * 256
+    assert sp_lib.sp_paged_prefill_workspace_size(4, 512, 28, ctypes.byref(lay), 547) == 0
+    assert sp_lib.sp_ragged_attention_workspace_size(132, 4, 512, 4096, 28, -1,
+                                                     ctypes.byref(lay), 547) == dec_al
+    # one chunk on a 32k context splits: both regions
+    pre = sp_lib.sp_paged_prefill_workspace_size(1, 512, 28, ctypes.byref(lay), 2016)
+    assert pre > 0
+    assert sp_lib.sp_ragged_attention_workspace_size(129, 1, 512, 4096, 28, -1,
+                                                     ctypes.byref(lay), 2016) == dec_al + pre
     assert sp_lib.sp_ragged_attention_workspace_size(128, 0, 0, 4096, 28, -1, ctypes.byref(lay),
-                                                     547) == dec
+                                                     547) == dec_al
+    assert sp_lib.sp_ragged_attention_workspace_size(1, 1, 512, 0, 28, -1, ctypes.byref(lay),
+                                                     2016) == pre

@@ -17,7 +17,7 @@ from tests.helpers import announce, as_f64, assert_attention_close, host_array, 
 pytestmark = pytest.mark.gpu
 
 
-def _run(w: W.MixedWorkload, window_left: int = -1):
+def _run(w: W.MixedWorkload, window_left: int = -1, repeats: int = 1):
     t = W.make_mixed_tensors(w)
     lay = sp.layout(t["num_blocks"], 1, 0, w.hkv, w.block_size, w.head_dim)
     P, T0 = w.num_prefill_seqs, w.num_prefill_tokens
@@ -29,11 +29,18 @@ def _run(w: W.MixedWorkload, window_left: int = -1):
              f"{w.num_decode_seqs} decode seqs, window {window_left}")
     sp.kv_append(t["k_pool"], t["v_pool"], lay, t["k_new"], t["v_new"], t["slot_mapping"])
     scale = w.head_dim ** -0.5
-    sp.ragged_paged_attention(t["out"], t["q"], t["k_pool"], t["v_pool"], lay, t["block_tables"],
-                              t["cu_seqlens_q"], t["context_lens"], num_prefill_seqs=P,
-                              num_prefill_tokens=T0, prefill_max_seqlen_q=pmax,
-                              decode_max_context_len=dmax, scale=scale, window_left=window_left,
-                              workspace=ws)
+    first = None
+    for r in range(repeats):
+        t["out"].fill_(float("nan"))
+        sp.ragged_paged_attention(t["out"], t["q"], t["k_pool"], t["v_pool"], lay,
+                                  t["block_tables"], t["cu_seqlens_q"], t["context_lens"],
+                                  num_prefill_seqs=P, num_prefill_tokens=T0,
+                                  prefill_max_seqlen_q=pmax, decode_max_context_len=dmax,
+                                  scale=scale, window_left=window_left, workspace=ws)
+        if r == 0:
+            first = t["out"].clone()
+        else:
+            assert torch.equal(t["out"], first), f"call {r} differs from the first"
     # the same halves through their own entry points, each with the workspace it asks for
     if P:
         pre = torch.full_like(t["q"][:T0], float("nan"))
@@ -88,6 +95,19 @@ def test_ragged_small_mixed(window):
                         np.array([0, 500, 40], np.int32),
                         np.array([1, 17, 300, 64, 129], np.int32), 8, 2, 128, "bf16")
     _run(w, window_left=window)
+
+
+def test_ragged_split_prefill_with_decode():
+    """A short chunk on a long context splits its key walk (partials in the back of the
+    workspace) while the decode half's partials take the front: both halves through one call,
+    three calls in a row giving the same bits."""
+    w = W.MixedWorkload("mixed-split", 80, np.array([64, 100], np.int32),
+                        np.array([4000, 2500], np.int32),
+                        np.array([3000, 17, 1500, 640, 2049, 1], np.int32), 8, 2, 128, "bf16")
+    t_lay = sp.layout(4096, 1, 0, w.hkv, w.block_size, w.head_dim)
+    mb = int(-(-int(w.context_lens.max()) // w.block_size))
+    assert sp.paged_prefill_workspace_size(2, 100, w.hq, t_lay, mb) > 0, "the plan must split"
+    _run(w, repeats=3)
 
 
 def test_ragged_decode_only_and_prefill_only():
