@@ -149,7 +149,7 @@ void BatchedPagedAttention::forward(size_t layer_idx, const DeviceRaggedBatch& b
              "sp_kv_append");
   }
   // 2. attention: chunked prefill over the chunks [0, P), decode over the one-token entries
-  //    [P, B): one sp_ragged_paged_attention call, two launches on the cache's stream
+  //    [P, B): one sp_ragged_paged_attention call, ordered on the cache's stream
   const int32_t P = hb.num_prefill_seqs, B = (int32_t)hb.num_seqs();
   const size_t need = sp_ragged_attention_workspace_size(B, P, hb.prefill_max_seqlen_q,
                                                          hb.decode_max_context_len, hq, -1,

@@ -16,8 +16,9 @@
 //     adding one token, each group in the caller's order, so that both groups are contiguous in
 //     the packed token stream and in the per-sequence arrays;
 //   - one layer appends K/V for every token (rotating K and Q when RoPE tables are given), then
-//     runs chunked prefill over the chunk group and decode over the one-token group: two
-//     launches on one stream. Both reduce to the reference's per-sequence forward_cached
+//     runs chunked prefill over the chunk group and decode over the one-token group, the
+//     decode on the library's side stream joined back into the cache's stream so the two
+//     overlap. Both reduce to the reference's per-sequence forward_cached
 //     (transformer.rs:184-254): no mask for one new token (llama.rs:255-260), and
 //     prefill_causal_mask (llama.rs:374-388) for a chunk.
 #pragma once
@@ -101,8 +102,8 @@ struct RopeTables {
 // One attention layer of a ragged batch over a paged cache (the batched form of
 // PagedAttentionCache::update_layer + forward_cached). q and out are [T, Hq, D], k_new / v_new
 // [T, Hkv, D], packed in batch order. Keeps one workspace between calls for the decode partials
-// and the chunked prefill's split-key partials (grown to what sp_paged_decode_workspace_size /
-// sp_paged_prefill_workspace_size ask for). Failures throw std::runtime_error with the
+// and the chunked prefill's split-key partials, side by side (grown to what
+// sp_ragged_attention_workspace_size asks for). Failures throw std::runtime_error with the
 // library's message.
 class BatchedPagedAttention {
  public:
