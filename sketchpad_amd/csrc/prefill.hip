@@ -125,6 +125,14 @@ __device__ __forceinline__ void lds_dma16_sbase(const char* sbase, int voff, cha
                : "memory");
 }
 
+// Stands in for cu_seqlens when a batch has none, so the kernel's length loads need no branch.
+__constant__ int32_t kPrefillZeroPair[2] = {0, 0};
+
+// Metadata the kernel only reads, seen through the constant address space so that uniform
+// loads of it become scalar loads.
+typedef const __attribute__((address_space(4))) int32_t* kconst_i32;
+__device__ __forceinline__ kconst_i32 as_const(const int32_t* p) { return (kconst_i32)p; }
+
 template <typename T, int D, bool PAGED>
 __global__ void __launch_bounds__(256, 2) prefill_kernel(PrefillArgs a) {
   using C = PrefillCfg<D>;
@@ -144,6 +152,9 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PrefillArgs a) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = wave_uniform(tid >> 6);
+  // the metadata pointers are read with the grid shape, in the first batch of argument loads
+  const int32_t* const cu_q_p = a.cu_q;
+  const int32_t* const cu_k_p = PAGED ? a.context_lens : a.cu_k;
   int id = blockIdx.x;
   const int kvh = id % a.hkv;
   id /= a.hkv;
@@ -155,18 +166,25 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PrefillArgs a) {
   const int qblk = a.num_qblocks - 1 - id / a.nsplit;
   const int h = kvh * a.group + gm;
 
-  const int q_begin = a.cu_q ? a.cu_q[seq] : 0;
-  const int Lq = a.cu_q ? a.cu_q[seq + 1] - q_begin : a.lq;
+  // Sequence offsets and lengths. The scalar loads are issued whatever the layout (a batch
+  // without cu_q / cu_k reads a zero pair instead), so they go out together and are waited for
+  // once.
+  const kconst_i32 cq = cu_q_p ? as_const(cu_q_p) + seq : as_const(kPrefillZeroPair);
+  const kconst_i32 ck = PAGED || cu_k_p ? as_const(cu_k_p) + seq : as_const(kPrefillZeroPair);
+  const int cq0 = cq[0], cq1 = cq[1], ck0 = ck[0], ck1 = PAGED ? 0 : ck[1];
+  asm volatile("" ::"s"(ck0), "s"(ck1));  // keep the key-length loads ahead of the early exit
+  const int q_begin = cq0;
+  const int Lq = cu_q_p ? cq1 - cq0 : a.lq;
+  int Lk, k_begin = 0;
+  if constexpr (PAGED) {
+    Lk = min(ck0, a.max_blocks_per_seq * a.block_size);
+  } else {
+    k_begin = ck0;
+    Lk = cu_k_p ? ck1 - ck0 : a.lk;
+  }
   const int qs = qblk * kPrefillBM;
   if (qs >= Lq) return;
   const int qe = min(qs + kPrefillBM, Lq);
-  int Lk, k_begin = 0;
-  if constexpr (PAGED) {
-    Lk = min(a.context_lens[seq], a.max_blocks_per_seq * a.block_size);
-  } else {
-    k_begin = a.cu_k ? a.cu_k[seq] : 0;
-    Lk = a.cu_k ? a.cu_k[seq + 1] - k_begin : a.lk;
-  }
   const int pos_off = (a.causal == SP_CAUSAL_TOP_LEFT) ? 0 : Lk - Lq;
   // keys any query of this workgroup can see: [kv_lo, kv_hi)
   int kv_lo = 0, kv_hi = Lk;
