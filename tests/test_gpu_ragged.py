@@ -120,3 +120,45 @@ def test_ragged_decode_only_and_prefill_only():
                                np.array([10, 0], np.int32), np.zeros(0, np.int32),
                                8, 2, 64, "bf16")
     _run(only_pre)
+
+
+def test_ragged_mixed_graph_capture():
+    """The mixed step's fork / join (decode on the library's side stream) captured into a HIP
+    graph through torch: four replays, each after eager work that overwrites the output, each
+    bit-identical to the eager call."""
+    w = W.MixedWorkload("mixed-graph", 81, np.array([64, 100], np.int32),
+                        np.array([4000, 300], np.int32),
+                        np.array([3000, 17, 1500, 640], np.int32), 8, 2, 128, "bf16")
+    t = W.make_mixed_tensors(w)
+    lay = sp.layout(t["num_blocks"], 1, 0, w.hkv, w.block_size, w.head_dim)
+    P, T0 = w.num_prefill_seqs, w.num_prefill_tokens
+    pmax, dmax = int(w.chunk_lens.max()), int(w.decode_lens.max())
+    mb = t["block_tables"].shape[1]
+    ws = sp.alloc_ragged_workspace(w.num_seqs, P, pmax, dmax, w.hq, lay, mb)
+    sp.kv_append(t["k_pool"], t["v_pool"], lay, t["k_new"], t["v_new"], t["slot_mapping"])
+
+    def call(stream):
+        sp.ragged_paged_attention(t["out"], t["q"], t["k_pool"], t["v_pool"], lay,
+                                  t["block_tables"], t["cu_seqlens_q"], t["context_lens"],
+                                  num_prefill_seqs=P, num_prefill_tokens=T0,
+                                  prefill_max_seqlen_q=pmax, decode_max_context_len=dmax,
+                                  scale=w.head_dim ** -0.5, workspace=ws, stream=stream)
+
+    announce("ragged mixed step under graph capture")
+    call(torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    eager = t["out"].clone()
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            call(s.cuda_stream)
+    torch.cuda.current_stream().wait_stream(s)
+    for r in range(4):
+        t["out"].fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(t["out"], eager), f"replay {r} differs from the eager call"
+
