@@ -110,6 +110,28 @@ def test_ragged_split_prefill_with_decode():
     _run(w, repeats=3)
 
 
+@pytest.mark.parametrize("seed", range(8))
+def test_ragged_random_batches(seed):
+    """Seeded random mixed batches: 0-4 chunks of 1-300 new tokens on 0-3000 cached tokens,
+    0-12 one-token sequences of 1-2500 tokens, GQA groups 1-8, head_dim 64 / 128, block size
+    16 / 32, with and without a window; every row against the oracle and each half bit for bit
+    against its own entry point."""
+    rng = np.random.default_rng(1000 + seed)
+    n_chunks = int(rng.integers(0, 5))
+    n_dec = int(rng.integers(0 if n_chunks else 1, 13))
+    hkv = int(rng.choice([1, 2, 4]))
+    group = int(rng.choice([1, 2, 4, 7, 8]))
+    d = int(rng.choice([64, 128]))
+    bs = int(rng.choice([16, 32]))
+    chunks = rng.integers(1, 301, n_chunks).astype(np.int32)
+    ctx = rng.integers(0, 3001, n_chunks).astype(np.int32)
+    dec = rng.integers(1, 2501, n_dec).astype(np.int32)
+    window = int(rng.choice([-1, int(rng.integers(0, 600))]))
+    w = W.MixedWorkload(f"mixed-random-{seed}", 2000 + seed, chunks, ctx, dec, hkv * group, hkv,
+                        d, "bf16", block_size=bs)
+    _run(w, window_left=window)
+
+
 def test_ragged_decode_only_and_prefill_only():
     """The two degenerate batches: no chunks (decode alone) and no decode sequences."""
     only_dec = W.MixedWorkload("mixed-decode-only", 78, np.zeros(0, np.int32),
