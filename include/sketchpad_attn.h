@@ -13,12 +13,14 @@
  *
  * Conventions (all entry points):
  *   - Plain pointers and sizes only. Device pointers are HIP device addresses; the stream is a
- *     hipStream_t passed as void* (NULL = the default stream). Work is enqueued on that stream
- *     and nothing synchronises the host.
+ *     hipStream_t passed as void* (NULL = the default stream) of the current HIP device. Work
+ *     is enqueued on that stream and nothing synchronises the host.
  *   - Return SP_OK (0) on success, a nonzero sp_status otherwise; sp_last_error() then returns a
  *     thread-local message. Nothing is thrown, aborted or exited across the ABI.
  *   - No entry point allocates device memory. Scratch space is caller-owned (workspace).
  *   - Calls are stateless and re-entrant; two calls that share a workspace must not overlap.
+ *     (sp_ragged_paged_attention keeps one side stream and two events per device, made on its
+ *     first mixed batch there; sp_paged_decode_noalloc one scratch array per device.)
  *
  * Paged pool layout (the reference's, paged_attention.rs:152-155):
  *   pool[num_blocks][num_layers][num_kv_heads][block_size][head_dim], one pool for K, one for V.
