@@ -598,6 +598,17 @@ int sp_ragged_paged_attention(void* out, const void* q, const void* k_pool, cons
       ragged_decode_bytes(nd, num_q_heads, decode_max_context_len, window_left, layout);
   void* pws = workspace && workspace_bytes > d_bytes ? (char*)workspace + d_bytes : nullptr;
   const size_t pws_bytes = pws ? workspace_bytes - d_bytes : 0;
+  // the decode half is validated before anything is enqueued (the prefill validates itself
+  // before its launch)
+  DecodeArgs da{};
+  if (int rc = decode_setup(fn, (char*)out + num_prefill_tokens * row,
+                            (const char*)q + num_prefill_tokens * row, k_pool, v_pool, layout,
+                            block_tables + (int64_t)num_prefill_seqs * max_blocks_per_seq,
+                            max_blocks_per_seq, context_lens + num_prefill_seqs,
+                            decode_max_context_len, nd, num_q_heads, scale, window_left, dtype,
+                            workspace, workspace_bytes < d_bytes ? workspace_bytes : d_bytes, &da))
+    return rc;
+  pool_strides(layout, dtype_size(dtype), &da.block_stride_b, &da.layer_off_b);
   const hipStream_t caller = (hipStream_t)stream;
   std::lock_guard<std::mutex> lock(g_fork_mu);
   ForkJoin* fj = nullptr;
@@ -607,10 +618,7 @@ int sp_ragged_paged_attention(void* out, const void* q, const void* k_pool, cons
   if (e != hipSuccess) return fail(SP_EHIP, "%s: fork: %s", fn, hipGetErrorString(e));
   // the chunks' long key walks are dispatched first, the decode's short workgroups after them
   const int rc_p = prefill_half(pws, pws_bytes, stream);
-  const int rc = rc_p ? rc_p
-                      : decode_half(workspace,
-                                    workspace_bytes < d_bytes ? workspace_bytes : d_bytes,
-                                    fj->side);
+  const int rc = rc_p ? rc_p : launch_paged_decode(da, dtype, layout->head_dim, fj->side);
   // the join is recorded whatever the launches returned, so the side stream never stays forked
   e = hipEventRecord(fj->join, fj->side);
   if (e == hipSuccess) e = hipStreamWaitEvent(caller, fj->join, 0);

@@ -242,6 +242,9 @@ def test_ragged_paged_attention_validation(sp_lib):
     assert call(tok=-1) == _lib.SP_EINVAL
     assert call(cu=None) == _lib.SP_EINVAL
     assert call(num_seqs=0, num_prefill=0) == _lib.SP_OK
+    # both halves: the decode half's workspace is checked before anything is enqueued
+    assert call() == _lib.SP_ENOSPACE
+    assert "required" in sp_lib.sp_last_error().decode()
     # C4's shape: the chunks do not split, so the decode partials are all
     dec = sp_lib.sp_paged_decode_workspace_size(128, 28, 4096, -1, ctypes.byref(lay))
     assert dec > 0
