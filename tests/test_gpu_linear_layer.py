@@ -46,7 +46,8 @@ def _linear_tol(x, w, prod, ref, dtype):
 @pytest.mark.parametrize("m,k,n", [(1, 64, 32), (64, 4096, 6144), (7, 96, 40), (300, 512, 1024),
                                    (129, 136, 130), (65, 1024, 4096), (2, 8192, 1027),
                                    (512, 128, 256), (1000, 512, 523), (777, 1024, 1000),
-                                   (1024, 4096, 1536)])
+                                   (1024, 4096, 1536), (1, 4096, 4096), (17, 2048, 2048),
+                                   (64, 512, 3000), (33, 1024, 2050)])
 @pytest.mark.parametrize("with_bias", [False, True])
 def test_linear(dtype, m, k, n, with_bias):
     """y = x . w^T (+ b) with w [out, in]; M/N tails, K not a multiple of the 32-deep stage,
