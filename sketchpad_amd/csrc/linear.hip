@@ -14,9 +14,9 @@
 // (16 consecutive rows at one chunk per 16 lanes) are bank-conflict free. A wave computes
 // C^T = w . x^T on v_mfma_f32_32x32x16: A = 32 rows of w, B = 32 rows of x, both 16 contiguous
 // bytes per lane, and the accumulator hands each lane 4 consecutive output columns (one 8-byte
-// store). BM = 128 for large M, 64 for M <= 64 (decode); when the tiles alone cannot fill the
-// chip, K is split and fp32 partials [split][M][N] are summed in a fixed order by a second
-// kernel (deterministic). fp32 runs a plain LDS-tiled FMA kernel.
+// store). Tiles are 128 x 128 for large M and 64 x 64 for M <= 64 (decode); when the tiles
+// alone cannot fill the chip, K is split and fp32 partials [split][M][N] are summed in a fixed
+// order by a second kernel (deterministic). fp32 runs a plain LDS-tiled FMA kernel.
 #include "linear.hpp"
 
 namespace sp {
@@ -445,11 +445,14 @@ LinearPlan plan_linear(int64_t M, int64_t K, int64_t N, size_t max_ws) {
     p.ws_bytes = 0;
     return p;
   }
+  // decode-sized x (M <= 64): 64 x 64 tiles, twice as many as 64 x 128 for the same weight
   p.tile_m = M <= 64 ? 64 : 128;
-  const int64_t tiles = ((M + p.tile_m - 1) / p.tile_m) * ((N + 127) / 128);
+  const int64_t tile_n = p.tile_m == 64 ? 64 : 128;
+  const int64_t tiles = ((M + p.tile_m - 1) / p.tile_m) * ((N + tile_n - 1) / tile_n);
   int splits = 1;
-  // split K while the tiles cannot fill the chip twice over, keeping >= 512 of K per split
-  while (tiles * splits < 512 && K / (splits * 2) >= 512 && splits < 8 &&
+  // split K while the tiles cannot fill the chip three times over (three resident workgroups
+  // per CU), keeping >= 512 of K per split
+  while (tiles * splits < 768 && K / (splits * 2) >= 512 && splits < 8 &&
          (size_t)(splits * 2) * M * N * 4 <= max_ws)
     splits *= 2;
   p.k_per_split = ((K + splits - 1) / splits + kLinStage - 1) / kLinStage * kLinStage;
@@ -471,8 +474,8 @@ static int launch_t(const LinArgs& a0, const LinearPlan& p, hipStream_t stream) 
     return check_launch("linear_big_kernel");
   }
   if (p.tile_m == 64) {
-    const dim3 grid((unsigned)((a.N + 127) / 128), (unsigned)((a.M + 63) / 64), p.splits);
-    hipLaunchKernelGGL((linear_kernel<T, 64, 128, 1, 4>), grid, block, 0, stream, a);
+    const dim3 grid((unsigned)((a.N + 63) / 64), (unsigned)((a.M + 63) / 64), p.splits);
+    hipLaunchKernelGGL((linear_kernel<T, 64, 64, 2, 2>), grid, block, 0, stream, a);
   } else {
     const dim3 grid((unsigned)((a.N + 127) / 128), (unsigned)((a.M + 127) / 128), p.splits);
     hipLaunchKernelGGL((linear_kernel<T, 128, 128, 2, 2>), grid, block, 0, stream, a);
