@@ -184,3 +184,61 @@ def test_ragged_mixed_graph_capture():
         torch.cuda.synchronize()
         assert torch.equal(t["out"], eager), f"replay {r} differs from the eager call"
 
+
+def test_ragged_mixed_from_two_host_threads():
+    """Two host threads issue mixed steps on their own streams, with their own buffers, at the
+    same time (the library's per-device side stream and events are shared): every output is
+    bit-identical to the same call made alone."""
+    import threading
+    w = W.MixedWorkload("mixed-threads", 82, np.array([64, 100], np.int32),
+                        np.array([2000, 300], np.int32),
+                        np.array([3000, 17, 1500, 640], np.int32), 8, 2, 128, "bf16")
+    runs = []
+    for _ in range(2):
+        t = W.make_mixed_tensors(w)
+        lay = sp.layout(t["num_blocks"], 1, 0, w.hkv, w.block_size, w.head_dim)
+        P, T0 = w.num_prefill_seqs, w.num_prefill_tokens
+        pmax, dmax = int(w.chunk_lens.max()), int(w.decode_lens.max())
+        ws = sp.alloc_ragged_workspace(w.num_seqs, P, pmax, dmax, w.hq, lay,
+                                       t["block_tables"].shape[1])
+        sp.kv_append(t["k_pool"], t["v_pool"], lay, t["k_new"], t["v_new"], t["slot_mapping"])
+        runs.append((t, lay, ws, torch.cuda.Stream()))
+    torch.cuda.synchronize()
+
+    def call(r):
+        t, lay, ws, st = r
+        sp.ragged_paged_attention(t["out"], t["q"], t["k_pool"], t["v_pool"], lay,
+                                  t["block_tables"], t["cu_seqlens_q"], t["context_lens"],
+                                  num_prefill_seqs=w.num_prefill_seqs,
+                                  num_prefill_tokens=w.num_prefill_tokens,
+                                  prefill_max_seqlen_q=int(w.chunk_lens.max()),
+                                  decode_max_context_len=int(w.decode_lens.max()),
+                                  scale=w.head_dim ** -0.5, workspace=ws, stream=st.cuda_stream)
+
+    announce("ragged mixed steps from two host threads")
+    call(runs[0])
+    torch.cuda.synchronize()
+    alone = runs[0][0]["out"].clone()
+    errors = []
+
+    def worker(r, n):
+        try:
+            for _ in range(n):
+                call(r)
+        except Exception as e:  # surfaced below
+            errors.append(e)
+
+    for _ in range(3):
+        for r in runs:
+            r[0]["out"].fill_(float("nan"))
+        torch.cuda.synchronize()
+        th = [threading.Thread(target=worker, args=(r, 20)) for r in runs]
+        for x in th:
+            x.start()
+        for x in th:
+            x.join()
+        torch.cuda.synchronize()
+        assert not errors, errors
+        for r in runs:
+            assert torch.equal(r[0]["out"], alone), "a concurrent call differs from the call alone"
+
