@@ -262,27 +262,25 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PrefillArgs a) {
     return t0 >= kv_lo && t0 + BN <= kv_hi;
   };
   // Paged fast path: the block ids of the rows of the next tile this wave loads, fetched one
-  // tile ahead (scalar loads) so that no load waits on a dependent block-table read.
-  int nblk[NLD];
-#pragma unroll
-  for (int u = 0; u < NLD; ++u) nblk[u] = 0;
+  // tile ahead so that no load waits on a dependent block-table read. Lane u < NLD fetches load
+  // u's id with a vector load: it completes with the tile loads at the next step's wait, where a
+  // scalar load would sit in lgkmcnt ahead of the LDS operand reads of the QK product and make
+  // each of their waits a wait for the table read.
+  int nblk = 0;
   auto fetch_blocks = [&](int t0) __attribute__((always_inline)) {
     if constexpr (PAGED) {
-      if (paged_fast && t0 < kv_end && tile_interior(t0)) {
-#pragma unroll
-        for (int u = 0; u < NLD; ++u) nblk[u] = table[(t0 + wrow0 + u * RPI) / a.block_size];
-      }
+      if (paged_fast && t0 < kv_end && tile_interior(t0))
+        nblk = table[(t0 + wrow0 + min(lane, NLD - 1) * RPI) / a.block_size];
     }
   };
   auto issue_tile = [&](int t0, char* buf) __attribute__((always_inline)) {
     char* dst = buf + wrow0 * RB;
     if (tile_interior(t0) && (!PAGED || paged_fast)) {
       if constexpr (PAGED) {
-        // block ids fetched by fetch_blocks(t0); the readfirstlane keeps the base scalar (a no-op
-        // when the id is already in an SGPR), and the asm's wait states cover it otherwise
+        // block ids fetched by fetch_blocks(t0), load u's in lane u
 #pragma unroll
         for (int u = 0; u < NLD; ++u) {
-          int blk = __builtin_amdgcn_readfirstlane(nblk[u]);
+          int blk = __builtin_amdgcn_readlane(nblk, u);
           blk = (blk >= 0 && blk < a.num_blocks) ? blk : 0;  // never outside the pool
           const char* sb = src_base + (int64_t)blk * a.block_stride_b + head_off;
           lds_dma16_s(sb, voff[u], dst + u * 1024);
