@@ -277,13 +277,19 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PrefillArgs a) {
     char* dst = buf + wrow0 * RB;
     if (tile_interior(t0) && (!PAGED || paged_fast)) {
       if constexpr (PAGED) {
-        // block ids fetched by fetch_blocks(t0), load u's in lane u
+        // block ids fetched by fetch_blocks(t0), load u's in lane u: every lane turns its id
+        // into its load's base address at once (vector ops), and each load reads its base out
+        // of lane u (two readlanes), instead of a scalar chain of compares and 64-bit multiplies
+        // per load
+        const int bl = (nblk >= 0 && nblk < a.num_blocks) ? nblk : 0;  // never outside the pool
+        const uint64_t vb =
+            (uint64_t)(uintptr_t)(src_base + head_off) + (uint64_t)bl * (uint64_t)a.block_stride_b;
+        const int vb_lo = (int)(uint32_t)vb, vb_hi = (int)(uint32_t)(vb >> 32);
 #pragma unroll
         for (int u = 0; u < NLD; ++u) {
-          int blk = __builtin_amdgcn_readlane(nblk, u);
-          blk = (blk >= 0 && blk < a.num_blocks) ? blk : 0;  // never outside the pool
-          const char* sb = src_base + (int64_t)blk * a.block_stride_b + head_off;
-          lds_dma16_s(sb, voff[u], dst + u * 1024);
+          const uint64_t lo = (uint32_t)__builtin_amdgcn_readlane(vb_lo, u);
+          const uint64_t hi = (uint32_t)__builtin_amdgcn_readlane(vb_hi, u);
+          lds_dma16_s((const char*)(uintptr_t)((hi << 32) | lo), voff[u], dst + u * 1024);
         }
       } else {
         const char* sb = src_base + (int64_t)t0 * row_pitch;
