@@ -116,13 +116,22 @@ __device__ __forceinline__ void swap_halves(float x, float& a, float& b) {
   b = __uint_as_float(r[1]);
 }
 
-// global_load_lds_dwordx4 from a base the compiler keeps in SGPRs (wave-uniform, computed by
-// scalar code) plus a per-lane byte offset; the s_nop covers the M0 write -> LDS DMA wait state.
-// Completion is awaited explicitly (s_waitcnt vmcnt(0) + barrier) before the data is read.
-__device__ __forceinline__ void lds_dma16_sbase(const char* sbase, int voff, char* lds_dst) {
+// Four 1 KiB LDS DMAs that share one M0 write: load u (0-3) reads base_u + v_u + 1024u and
+// writes lds_dst + 1024u + 16 lane (the instruction offset applies to both addresses). The s_nop
+// covers the M0 write (and, for bases read out of vector lanes, the SGPR write) -> LDS DMA wait
+// states. Completion is awaited explicitly (s_waitcnt vmcnt(0) + barrier) before the data is read.
+__device__ __forceinline__ void lds_dma16x4(const char* b0, const char* b1, const char* b2,
+                                            const char* b3, int v0, int v1, int v2, int v3,
+                                            char* lds_dst) {
   const unsigned m0 = (unsigned)(uintptr_t)(lds_void*)lds_dst;
-  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "{m0}"(m0)
-               : "memory");
+  asm volatile(
+      "s_nop 4\n\t"
+      "global_load_lds_dwordx4 %0, %4\n\t"
+      "global_load_lds_dwordx4 %1, %5 offset:1024\n\t"
+      "global_load_lds_dwordx4 %2, %6 offset:2048\n\t"
+      "global_load_lds_dwordx4 %3, %7 offset:3072" ::"v"(v0),
+      "v"(v1), "v"(v2), "v"(v3), "s"(b0), "s"(b1), "s"(b2), "s"(b3), "{m0}"(m0)
+      : "memory");
 }
 
 // Stands in for cu_seqlens when a batch has none, so the kernel's length loads need no branch.
@@ -258,6 +267,13 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PrefillArgs a) {
     const int64_t row_b = PAGED ? (int64_t)(r % max(a.block_size, 1)) * RB : (int64_t)r * row_pitch;
     voff[u] = (int)row_b + 16 * ((lane % CPR) ^ C::swz(r));
   }
+  static_assert(NLD % 4 == 0, "tile loads go out in groups of four");
+  // Interior tiles issue their loads in groups of four with instruction offsets 0, 1, 2, 3 KiB.
+  // Contiguous K/V: the offsets come out of the lane offsets (still >= 0: load u's rows start at
+  // u RPI rows of at least RB bytes, u RPI RB = 1024 u). Paged: out of the per-load bases.
+  int voff_g[NLD];
+#pragma unroll
+  for (int u = 0; u < NLD; ++u) voff_g[u] = PAGED ? voff[u] : voff[u] - (u & 3) * 1024;
   auto tile_interior = [&](int t0) __attribute__((always_inline)) {
     return t0 >= kv_lo && t0 + BN <= kv_hi;
   };
@@ -266,36 +282,49 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PrefillArgs a) {
   // u's id with a vector load: it completes with the tile loads at the next step's wait, where a
   // scalar load would sit in lgkmcnt ahead of the LDS operand reads of the QK product and make
   // each of their waits a wait for the table read.
+  // block_size divides the 64-key tile here, so it is a power of two and every tile start t0 is
+  // a multiple of it: the id of the block holding row t0 + r is table[(t0 >> shift) + (r >> shift)].
   int nblk = 0;
+  const int bs_shift = paged_fast ? wave_uniform(31 - __builtin_clz(max(a.block_size, 1))) : 0;
+  const int lane_blk = (wrow0 + min(lane, NLD - 1) * RPI) >> bs_shift;
   auto fetch_blocks = [&](int t0) __attribute__((always_inline)) {
     if constexpr (PAGED) {
-      if (paged_fast && t0 < kv_end && tile_interior(t0))
-        nblk = table[(t0 + wrow0 + min(lane, NLD - 1) * RPI) / a.block_size];
+      if (paged_fast && t0 < kv_end && tile_interior(t0)) nblk = table[(t0 >> bs_shift) + lane_blk];
+    }
+  };
+  // Interior tile: its loads go out in groups of four that share one M0 write.
+  auto issue_interior = [&](int t0, char* buf) __attribute__((always_inline)) {
+    char* dst = buf + wrow0 * RB;
+    if constexpr (PAGED) {
+      // block ids fetched by fetch_blocks(t0), load u's in lane u: every lane turns its id into
+      // its load's base address at once (vector ops), and each load reads its base out of lane u
+      // (two readlanes), instead of a scalar chain of compares and 64-bit multiplies per load.
+      // The base is taken less the load's instruction offset; the sum is the block's row address.
+      const int bl = (nblk >= 0 && nblk < a.num_blocks) ? nblk : 0;  // never outside the pool
+      const uint64_t vb = (uint64_t)(uintptr_t)(src_base + head_off) +
+                          (uint64_t)bl * (uint64_t)a.block_stride_b - (uint64_t)((lane & 3) * 1024);
+      const int vb_lo = (int)(uint32_t)vb, vb_hi = (int)(uint32_t)(vb >> 32);
+      auto base_of = [&](int u) __attribute__((always_inline)) {
+        const uint64_t lo = (uint32_t)__builtin_amdgcn_readlane(vb_lo, u);
+        const uint64_t hi = (uint32_t)__builtin_amdgcn_readlane(vb_hi, u);
+        return (const char*)(uintptr_t)((hi << 32) | lo);
+      };
+#pragma unroll
+      for (int g = 0; g < NLD; g += 4)
+        lds_dma16x4(base_of(g), base_of(g + 1), base_of(g + 2), base_of(g + 3), voff_g[g],
+                    voff_g[g + 1], voff_g[g + 2], voff_g[g + 3], dst + g * 1024);
+    } else {
+      const char* sb = src_base + (int64_t)t0 * row_pitch;
+#pragma unroll
+      for (int g = 0; g < NLD; g += 4)
+        lds_dma16x4(sb, sb, sb, sb, voff_g[g], voff_g[g + 1], voff_g[g + 2], voff_g[g + 3],
+                    dst + g * 1024);
     }
   };
   auto issue_tile = [&](int t0, char* buf) __attribute__((always_inline)) {
     char* dst = buf + wrow0 * RB;
     if (tile_interior(t0) && (!PAGED || paged_fast)) {
-      if constexpr (PAGED) {
-        // block ids fetched by fetch_blocks(t0), load u's in lane u: every lane turns its id
-        // into its load's base address at once (vector ops), and each load reads its base out
-        // of lane u (two readlanes), instead of a scalar chain of compares and 64-bit multiplies
-        // per load
-        const int bl = (nblk >= 0 && nblk < a.num_blocks) ? nblk : 0;  // never outside the pool
-        const uint64_t vb =
-            (uint64_t)(uintptr_t)(src_base + head_off) + (uint64_t)bl * (uint64_t)a.block_stride_b;
-        const int vb_lo = (int)(uint32_t)vb, vb_hi = (int)(uint32_t)(vb >> 32);
-#pragma unroll
-        for (int u = 0; u < NLD; ++u) {
-          const uint64_t lo = (uint32_t)__builtin_amdgcn_readlane(vb_lo, u);
-          const uint64_t hi = (uint32_t)__builtin_amdgcn_readlane(vb_hi, u);
-          lds_dma16_s((const char*)(uintptr_t)((hi << 32) | lo), voff[u], dst + u * 1024);
-        }
-      } else {
-        const char* sb = src_base + (int64_t)t0 * row_pitch;
-#pragma unroll
-        for (int u = 0; u < NLD; ++u) lds_dma16_sbase(sb, voff[u], dst + u * 1024);
-      }
+      issue_interior(t0, buf);
       return;
     }
     // Edge tiles are rare: the lane id goes through an empty asm so that the per-lane source
@@ -528,13 +557,16 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PrefillArgs a) {
     }
   };
 
-  // wave-uniform: does this wave see any key of the tile
-  auto visits = [&](int t0) __attribute__((always_inline)) {
-    bool v = wave_active && t0 < kv_end;
-    if (a.causal != SP_CAUSAL_NONE) v = v && t0 <= wq_hi + pos_off;
-    if (a.window_left >= 0) v = v && t0 + BN - 1 >= wq_lo + pos_off - a.window_left;
-    return v;
-  };
+  // wave-uniform: does this wave see any key of the tile. The conditions (the wave has queries,
+  // the tile starts before kv_end, at or before the causal diagonal of the wave's last query, and
+  // ends at or after the window edge of its first query) bound t0 from both sides, so they
+  // reduce to one range [vis_lo, vis_hi) worked out once.
+  int vis_lo = -(1 << 30), vis_hi = wave_active ? kv_end : -(1 << 30);
+  if (a.causal != SP_CAUSAL_NONE) vis_hi = min(vis_hi, wq_hi + pos_off + 1);
+  if (a.window_left >= 0) vis_lo = wq_lo + pos_off - a.window_left - BN + 1;
+  vis_lo = wave_uniform(vis_lo);
+  vis_hi = wave_uniform(vis_hi);
+  auto visits = [&](int t0) __attribute__((always_inline)) { return t0 >= vis_lo && t0 < vis_hi; };
 
   // One pipeline step on tile t0 (its K in kcur's tile one step ago, now its S^T in sc; its V
   // in vcur): wait until this step's tiles are in (own loads, then everyone's), start the loads
