@@ -5,9 +5,11 @@
     python bench.py --calibrate-copy    # plain 512 MiB device copies (HBM counter calibration)
 
 A step is one decode step of the headline workload (C2, Llama-3-8B shape): append the
-step's new K/V row of each of the 64 sequences into the paged pool (sp_kv_append), then paged
-decode attention over every sequence's context (sp_paged_decode). Inputs are resident in HBM
-before the timed region starts. Prints one JSON line:
+step's new K/V row of each of the 64 sequences into the paged pool, then paged decode attention
+over every sequence's context, both in one sp_paged_append_decode call (the append runs inside
+the decode kernel; ms_per_step_separate_calls times the same step as sp_kv_append followed by
+sp_paged_decode). Inputs are resident in HBM before the timed region starts. Prints one JSON
+line:
   value      algorithmic bytes of the step (append + decode) / measured step time, GB/s
   roofline   the decode call: algorithmic bytes / its average duration (HIP events on the
              launch stream around K back-to-back calls) against MI355X's 8 TB/s HBM peak
@@ -117,21 +119,32 @@ def time_decode_config(w, steps: int, warmup: int):
                         t["context_lens"], max_ctx, scale, window_left=w.window_left,
                         workspace=ws, stream=stream.cuda_stream)
 
-    _warm(lambda: (append(), decode()), warmup)
+    def append_decode():
+        sp.paged_append_decode(t["out"], t["q"], t["k_pool"], t["v_pool"], lay, t["k_new"],
+                               t["v_new"], t["block_tables"], t["context_lens"], max_ctx, scale,
+                               window_left=w.window_left, workspace=ws,
+                               stream=stream.cuda_stream)
+
+    _warm(lambda: (append(), decode(), append_decode()), warmup)
     torch.cuda.synchronize()
 
-    # whole-step timing
-    t0 = time.perf_counter()
-    for _ in range(steps):
-        append()
-        decode()
-    torch.cuda.synchronize()
-    step_s = (time.perf_counter() - t0) / steps
+    # whole-step timing: the step as one sp_paged_append_decode call, and as the two calls
+    # sp_kv_append + sp_paged_decode
+    def step_time(fn):
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            fn()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) / steps
+
+    step_s = step_time(append_decode)
+    step_s_separate = step_time(lambda: (append(), decode()))
 
     # the decode call's duration: HIP events on the launch stream around `steps` back-to-back calls
     dec_avg, dec_min = _event_times(stream, decode, steps)
     return {
         "step_s": step_s,
+        "step_s_separate": step_s_separate,
         "decode_ms_avg": dec_avg,
         "decode_ms_min": dec_min,
         "decode_bytes": w.decode_bytes(),
@@ -727,13 +740,15 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(r["step_s"] * 1e3, 4),
+        "ms_per_step_separate_calls": round(r["step_s_separate"] * 1e3, 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": w.dtype,
         "data": "synthetic",
         "config": {
-            "workload": f"{w.name}: append + paged decode, B={w.num_seqs}, Hq={w.hq}, "
+            "workload": f"{w.name}: append + paged decode in one sp_paged_append_decode call, "
+                        f"B={w.num_seqs}, Hq={w.hq}, "
                         f"Hkv={w.hkv}, D={w.head_dim}, BS={w.block_size}, "
                         f"L~U[{int(w.context_lens.min())},{int(w.context_lens.max())}] "
                         f"(sum {int(w.context_lens.sum())}), seed {w.seed:#x}",

@@ -190,6 +190,31 @@ int sp_paged_decode(void* out, const void* q,
                     void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * One decode step's append and attention in a single call: sp_kv_append of each sequence's new
+ * token followed by sp_paged_decode, with the append done inside the decode kernel. Replaces
+ * PagedAttentionCache::update_layer for one new token per sequence (store_kv,
+ * paged_attention.rs:230-310, :519-548) followed by the decode attention (transformer.rs:227-243).
+ *   k_new, v_new : the step's new token of sequence s, KV head h, at element offset
+ *                  s*token_stride + h*head_stride (for [num_seqs, Hkv, D] contiguous:
+ *                  token_stride = Hkv*D, head_stride = D); 16-byte aligned, as are the strides
+ *                  in bytes.
+ * The new token of sequence s is its last position, context_lens[s] - 1: it is written into the
+ * pools at the slot its block table gives that position (not written when that block id lies
+ * outside the pool, as sp_kv_append skips such a slot) and attended from k_new / v_new in the
+ * same launch. Everything else is sp_paged_decode's (same arguments, workspace and results, bit
+ * for bit, as sp_kv_append with those slots followed by sp_paged_decode). A sequence with
+ * context_lens[s] == 0 has no new token: nothing is written and its output is zeros.
+ */
+int sp_paged_append_decode(void* out, const void* q, void* k_pool, void* v_pool,
+                           const sp_cache_layout* layout, const void* k_new, const void* v_new,
+                           int64_t token_stride, int64_t head_stride,
+                           const int32_t* block_tables, int32_t max_blocks_per_seq,
+                           const int32_t* context_lens, int32_t max_context_len,
+                           int32_t num_seqs, int32_t num_q_heads,
+                           float scale, int32_t window_left, sp_dtype dtype,
+                           void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * sp_paged_decode without a workspace argument: the split partials go to a scratch array the
  * library holds on each GPU it runs on (32 MiB, kept until the process ends), so the call
  * allocates nothing. No counterpart in the reference: it is for callers that cannot allocate

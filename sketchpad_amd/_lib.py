@@ -72,6 +72,11 @@ _SIGNATURES = {
     "sp_paged_decode": (c_int32, [c_void_p, c_void_p, c_void_p, c_void_p, POINTER(CacheLayout),
                                   c_void_p, c_int32, c_void_p, c_int32, c_int32, c_int32,
                                   c_float, c_int32, c_int32, c_void_p, c_size_t, c_void_p]),
+    "sp_paged_append_decode": (c_int32, [c_void_p, c_void_p, c_void_p, c_void_p,
+                                         POINTER(CacheLayout), c_void_p, c_void_p, c_int64,
+                                         c_int64, c_void_p, c_int32, c_void_p, c_int32, c_int32,
+                                         c_int32, c_float, c_int32, c_int32, c_void_p, c_size_t,
+                                         c_void_p]),
     "sp_paged_decode_noalloc": (c_int32, [c_void_p, c_void_p, c_void_p, c_void_p,
                                           POINTER(CacheLayout), c_void_p, c_int32, c_void_p,
                                           c_int32, c_int32, c_int32, c_float, c_int32, c_int32,
@@ -249,6 +254,21 @@ def paged_decode_workspace_size(num_seqs: int, num_q_heads: int, max_context_len
                                 window_left: int, lay: CacheLayout) -> int:
     return int(load().sp_paged_decode_workspace_size(num_seqs, num_q_heads, max_context_len,
                                                      window_left, ctypes.byref(lay)))
+
+
+def paged_append_decode(out, q, k_pool, v_pool, lay: CacheLayout, k_new, v_new, block_tables,
+                        context_lens, max_context_len: int, scale: float, *, window_left: int = -1,
+                        workspace=None, stream=None) -> None:
+    """sp_paged_append_decode. k_new/v_new are [num_seqs, Hkv, D] (any strides the C call takes);
+    the rest as paged_decode."""
+    num_seqs, hq = q.shape[0], q.shape[1]
+    ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    check(load().sp_paged_append_decode(_ptr(out), _ptr(q), _ptr(k_pool), _ptr(v_pool),
+                                        ctypes.byref(lay), _ptr(k_new), _ptr(v_new),
+                                        k_new.stride(0), k_new.stride(1), _ptr(block_tables),
+                                        block_tables.shape[1], _ptr(context_lens),
+                                        max_context_len, num_seqs, hq, scale, window_left,
+                                        sp_dtype(q), _ptr(workspace), ws_bytes, _stream(stream)))
 
 
 def paged_decode(out, q, k_pool, v_pool, lay: CacheLayout, block_tables, context_lens,

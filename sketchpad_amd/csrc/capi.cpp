@@ -304,6 +304,34 @@ int sp_paged_decode(void* out, const void* q, const void* k_pool, const void* v_
   return launch_paged_decode(a, dtype, layout->head_dim, (hipStream_t)stream);
 }
 
+int sp_paged_append_decode(void* out, const void* q, void* k_pool, void* v_pool,
+                           const sp_cache_layout* layout, const void* k_new, const void* v_new,
+                           int64_t token_stride, int64_t head_stride, const int32_t* block_tables,
+                           int32_t max_blocks_per_seq, const int32_t* context_lens,
+                           int32_t max_context_len, int32_t num_seqs, int32_t num_q_heads,
+                           float scale, int32_t window_left, sp_dtype dtype, void* workspace,
+                           size_t workspace_bytes, void* stream) {
+  const char* fn = "sp_paged_append_decode";
+  DecodeArgs a{};
+  if (int rc = decode_setup(fn, out, q, k_pool, v_pool, layout, block_tables, max_blocks_per_seq,
+                            context_lens, max_context_len, num_seqs, num_q_heads, scale,
+                            window_left, dtype, workspace, workspace_bytes, &a))
+    return rc;
+  if (num_seqs == 0) return SP_OK;
+  if (!k_new || !v_new) return fail(SP_EINVAL, "%s: NULL pointer argument", fn);
+  if (token_stride < 0 || head_stride < 0) return fail(SP_EINVAL, "%s: negative stride", fn);
+  const int es = dtype_size(dtype);
+  if ((((uintptr_t)k_new | (uintptr_t)v_new) & 15) || ((token_stride * es) & 15) ||
+      ((head_stride * es) & 15))
+    return fail(SP_EINVAL, "%s: k_new, v_new and their strides must be 16-byte aligned", fn);
+  pool_strides(layout, es, &a.block_stride_b, &a.layer_off_b);
+  a.k_new = (const char*)k_new;
+  a.v_new = (const char*)v_new;
+  a.new_tok_stride_b = token_stride * es;
+  a.new_head_stride_b = head_stride * es;
+  return launch_paged_decode(a, dtype, layout->head_dim, (hipStream_t)stream);
+}
+
 int sp_paged_decode_noalloc(void* out, const void* q, const void* k_pool, const void* v_pool,
                             const sp_cache_layout* layout, const int32_t* block_tables,
                             int32_t max_blocks_per_seq, const int32_t* context_lens,

@@ -19,6 +19,9 @@
 //     coalesced 16-byte stores and read back column-wise (padded pitch, conflict-free).
 // The next tile's loads are issued as soon as the current K has entered the MFMAs and V is in
 // LDS, so they stay in flight through the softmax and PV of the current tile.
+// sp_paged_append_decode runs the step's append in the same launch: the last split of each
+// (sequence, KV head) unit stores the new token's rows (store_kv, paged_attention.rs:230-310)
+// and reads them from the input rather than the pool.
 // The four waves merge in LDS. A sequence that needs one split writes its output directly;
 // otherwise each split stores (m, l, acc[D]) and decode_combine_kernel merges them. (Merging in
 // the last-arriving split instead needs an agent-scope release/acquire per split, which on
@@ -203,6 +206,30 @@ __global__ void __launch_bounds__(64 * kDecodeWaves, decode_min_waves<T>())
   const int64_t head_off = a.layer_off_b + (int64_t)kvh * a.block_size * RB;
   char* vst = smem + wave * C::WAVE_LDS;
 
+  // Fused append (sp_paged_append_decode): the step's new token of this sequence is its last
+  // position L - 1. The split that holds it stores the token's K and V rows of this KV head in
+  // the pool, at the slot the block table gives position L - 1 (skipped when that block id lies
+  // outside the pool, as sp_kv_append skips such a slot), and the tile holding L - 1 reads the
+  // row from k_new / v_new instead of the pool, so no other kernel has to run first.
+  const char* knew_row = nullptr;
+  const char* vnew_row = nullptr;
+  if (a.k_new) {
+    const int64_t off_new = (int64_t)seq * a.new_tok_stride_b + (int64_t)kvh * a.new_head_stride_b;
+    knew_row = a.k_new + off_new;
+    vnew_row = a.v_new + off_new;
+    if (split == nsplit - 1 && wave == 0) {
+      const int p = L - 1;
+      const int blk = table[p / a.block_size];
+      if (blk >= 0 && blk < a.num_blocks) {
+        const int64_t dst = (int64_t)blk * a.block_stride_b + head_off + (int64_t)(p % a.block_size) * RB;
+        for (int o = lane * 16; o < RB; o += 64 * 16) {
+          *(uint4*)((char*)a.kpool + dst + o) = *(const uint4*)(knew_row + o);
+          *(uint4*)((char*)a.vpool + dst + o) = *(const uint4*)(vnew_row + o);
+        }
+      }
+    }
+  }
+
   // Block ids of this split's tiles, fetched once up front: lane j holds the block of tile
   // t_begin + j in blk0 and of tile t_begin + 64 + j in blk1 (tps <= 128), so no tile load waits
   // on a dependent block-table read.
@@ -232,6 +259,26 @@ __global__ void __launch_bounds__(64 * kDecodeWaves, decode_min_waves<T>())
     const int64_t base = (int64_t)(ok ? blk : 0) * a.block_stride_b + head_off +
                          (int64_t)(pos0 % a.block_size) * RB;
     const int rlo = max(start_tok - pos0, 0), rhi = min(L - pos0, kTile) - 1;  // valid rows
+    if (knew_row && pos0 + kTile > L - 1) {
+      // the tile holding the fused append's token: its row rhi = L - 1 - pos0 (and the rows
+      // clamped onto it) come from k_new / v_new
+      if constexpr (kF32) {
+        const int kr_row = min(max(n, rlo), rhi);
+        const char* kb = kr_row == rhi ? knew_row : a.kpool + base + kr_row * RB;
+#pragma unroll
+        for (int c = 0; c < NL; ++c) kr[c] = ldnt(kb + c * 64 + g * 16);
+      }
+#pragma unroll
+      for (int i = 0; i < NL; ++i) {
+        const int off = (i * 64 + lane) * 16;
+        const int row = min(max(off / RB, rlo), rhi);
+        const bool nw = row == rhi;
+        const int o = row * RB + off % RB;
+        if constexpr (!kF32) kr[i] = ldnt(nw ? knew_row + off % RB : a.kpool + base + o);
+        vr[i] = ldnt(nw ? vnew_row + off % RB : a.vpool + base + o);
+      }
+      return;
+    }
     if constexpr (kF32) {
       const int kr_row = min(max(n, rlo), rhi);
 #pragma unroll

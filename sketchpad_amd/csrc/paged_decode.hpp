@@ -47,6 +47,12 @@ struct DecodeArgs {
   int tps;
   int max_splits;
   float scale_log2;  // softmax scale * log2(e)
+  // Fused append (sp_paged_append_decode), or null: the step's new token of sequence s, for KV
+  // head h, at k_new + s * new_tok_stride_b + h * new_head_stride_b (same for v_new).
+  const char* k_new;
+  const char* v_new;
+  int64_t new_tok_stride_b;
+  int64_t new_head_stride_b;
 };
 
 int launch_paged_decode(const DecodeArgs& a, sp_dtype dtype, int head_dim, hipStream_t stream);
