@@ -351,19 +351,17 @@ __global__ void __launch_bounds__(64 * kDecodeWaves, 4) polar_decode_kernel(Deco
   const int seq = unit / a.hkv, kvh = unit - seq * a.hkv;
   const int G = a.group;
 
-  // Block ids of the split's tiles: lane j holds tile t_begin + j in blk0 and t_begin + 64 + j in
-  // blk1 (tps <= 128), so no tile load waits on a dependent block-table read. Without a window
+  // Block ids of the split's tiles: lane j holds tile t_begin + j (tps <= 64), so no tile load
+  // waits on a dependent block-table read. Without a window
   // t_begin = split * tps does not depend on the context length, and the table read is issued
   // together with it (one memory round trip before the first tile instead of two).
   const int32_t* table = a.block_tables + (int64_t)seq * a.max_blocks_per_seq;
-  auto fetch_blocks = [&](int t0, int n_tiles, int& b0, int& b1) {
+  auto fetch_blocks = [&](int t0, int n_tiles, int& b0) {
     const int i0 = ((t0 + lane) * kPTile) / a.block_size;
-    const int i1 = ((t0 + 64 + lane) * kPTile) / a.block_size;
     b0 = (lane < n_tiles && i0 < a.max_blocks_per_seq) ? table[i0] : 0;
-    b1 = (lane + 64 < n_tiles && i1 < a.max_blocks_per_seq) ? table[i1] : 0;
   };
-  int blk0 = 0, blk1 = 0;
-  if (a.window_left < 0) fetch_blocks(split * a.tps, a.tps, blk0, blk1);
+  int blk0 = 0;
+  if (a.window_left < 0) fetch_blocks(split * a.tps, a.tps, blk0);
 
   int L = a.context_lens[seq];
   L = min(L, min(a.max_context_len, a.max_blocks_per_seq * a.block_size));
@@ -383,7 +381,7 @@ __global__ void __launch_bounds__(64 * kDecodeWaves, 4) polar_decode_kernel(Deco
   if (split >= nsplit) return;
   const int t_begin = first_tile + split * a.tps;
   const int t_end = min(t_begin + a.tps, last_tile + 1);
-  if (a.window_left >= 0) fetch_blocks(t_begin, t_end - t_begin, blk0, blk1);
+  if (a.window_left >= 0) fetch_blocks(t_begin, t_end - t_begin, blk0);
 
   // Q^T operand in the unpack order: for word c of lane (g, n), pairs P..P+3 with
   // P = g * HB/4 + 4c hold dimensions 2P..2P+7, and the unpacked elements are dimensions
@@ -428,6 +426,21 @@ __global__ void __launch_bounds__(64 * kDecodeWaves, 4) polar_decode_kernel(Deco
 
   const int64_t head_off = a.layer_off_b + (int64_t)kvh * polar_region_bytes(a.block_size, D);
   const int mag_off = a.block_size * HB;
+  // Each lane turns its tile's block id into the tile's code-plane and norm-plane byte offsets
+  // (block 0 for an id outside the pool, whose tile is masked: bit j of okm clear), so a tile's
+  // loads read their bases out of one lane instead of a scalar chain of compares, a 64-bit
+  // multiply and a signed remainder per tile. Splits of PolarQuant batches span at most 64 tiles
+  // (plan_decode), so lane j holds tile t_begin + j.
+  int64_t coff, moff;
+  uint64_t okm;
+  {
+    const bool ok = blk0 >= 0 && blk0 < a.num_blocks;
+    const int sl0 = ((t_begin + lane) * kPTile) % a.block_size;
+    const int64_t base = (int64_t)(ok ? blk0 : 0) * a.block_stride_b + head_off;
+    coff = base + (int64_t)sl0 * HB;  // K codes; V token quads start at the same offset
+    moff = base + mag_off + 2 * sl0;  // binary16 norms
+    okm = __ballot(ok);
+  }
 
   // One tile's loads: lane (g, n) holds 16 (D=64: 8) bytes of token n's K code row, 16 (8)
   // bytes of the V token-quad g, and the binary16 norms of tokens 4g..4g+3.
@@ -440,18 +453,19 @@ __global__ void __launch_bounds__(64 * kDecodeWaves, 4) polar_decode_kernel(Deco
   const uint32_t k_lane = n * HB + g * (HB / 4);
   const uint32_t v_lane = g * HB * 4 + n * (4 * NW);
   const uint32_t m_lane = 8 * g;
+  auto readlane64 = [](int64_t v, int l) {
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, l);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)((uint64_t)v >> 32), l);
+    return (int64_t)(((uint64_t)hi << 32) | lo);
+  };
   auto load_tile = [&](int t, Stage& s) {
-    const int ti = t - t_begin;
-    const int b0 = __builtin_amdgcn_readlane(blk0, ti & 63);
-    const int b1 = __builtin_amdgcn_readlane(blk1, ti & 63);
-    const int blk = ti < 64 ? b0 : b1;
-    s.ok = blk >= 0 && blk < a.num_blocks;
-    const int sl0 = (t * kPTile) % a.block_size;
-    const int64_t base = (int64_t)(s.ok ? blk : 0) * a.block_stride_b + head_off;
-    const char* kt = a.kpool + (base + (int64_t)sl0 * HB);
-    const char* vt = a.vpool + (base + (int64_t)(sl0 >> 2) * HB * 4);
-    const char* kmt = a.kpool + (base + mag_off + 2 * sl0);
-    const char* vmt = a.vpool + (base + mag_off + 2 * sl0);
+    const int ti = t - t_begin;  // < tps <= 64
+    s.ok = (okm >> ti) & 1;
+    const int64_t c = readlane64(coff, ti), m = readlane64(moff, ti);
+    const char* kt = a.kpool + c;
+    const char* vt = a.vpool + c;
+    const char* kmt = a.kpool + m;
+    const char* vmt = a.vpool + m;
     s.kw = *(const W*)(kt + k_lane);
     s.vw = *(const W*)(vt + v_lane);
     s.km = *(const uint2*)(kmt + m_lane);
@@ -698,6 +712,9 @@ static int launch_decode_typed(const DecodeArgs& a, sp_dtype dtype, hipStream_t 
 }
 
 int launch_polar_decode(const DecodeArgs& a, sp_dtype dtype, int head_dim, hipStream_t stream) {
+  // the kernel holds one tile per lane of a wave (plan_decode's PolarQuant splits: <= 64 tiles)
+  if (a.tps < 1 || a.tps > 64)
+    return fail(SP_EINVAL, "polar decode: %d tiles per split (at most 64)", a.tps);
   if (dtype == SP_BF16) {
     if (head_dim == 64) return launch_decode_typed<bf16_t, 64>(a, dtype, stream);
     if (head_dim == 128) return launch_decode_typed<bf16_t, 128>(a, dtype, stream);
