@@ -25,7 +25,8 @@
 // K/V tiles go HBM -> LDS with global_load_lds_dwordx4 (no register staging) into double
 // buffers: K runs two tiles ahead of the PV product (its QK product runs one tile early), V one
 // tile ahead; interior tiles take one scalar base per tile (per block when paged, with the block
-// ids fetched a tile ahead). Rows are stored with the 16-byte chunks XOR-swizzled so that the K
+// ids fetched a tile ahead), and their loads go out four per M0 write through the instruction
+// offset. Rows are stored with the 16-byte chunks XOR-swizzled so that the K
 // reads (16 rows x one chunk) and the V transpose reads (4 rows x 64 bytes) are bank-conflict
 // free.
 // Only tiles that cross the causal diagonal, the window edge or the sequence end are masked.
