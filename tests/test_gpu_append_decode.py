@@ -135,3 +135,49 @@ def test_append_decode_long_contexts_many_splits():
 @pytest.mark.parametrize("name", ["C2", "C5"])
 def test_append_decode_full_size_configs(name):
     fused_vs_separate(W.DECODE_CONFIGS[name]())
+
+
+def test_append_decode_graph_capture():
+    """The fused step captured into a HIP graph through torch: four replays, each after eager
+    work that overwrites the output and clears the new rows' pool slots, each giving the eager
+    call's output and pools bit for bit."""
+    w = W.random_decode(seed=5600, num_seqs=6, hq=32, hkv=8, head_dim=128, block_size=16,
+                        dtype="bf16", min_len=1, max_len=3000)
+    t = W.make_decode_tensors(w)
+    lay = w.layout()
+    max_ctx = w.max_context_len
+    ws = sp.alloc_decode_workspace(w.num_seqs, w.hq, max_ctx, -1, lay)
+    slots = torch.from_numpy(_slots(w)).long().cuda()
+
+    def call(stream):
+        sp.paged_append_decode(t["out"], t["q"], t["k_pool"], t["v_pool"], lay, t["k_new"],
+                               t["v_new"], t["block_tables"], t["context_lens"], max_ctx,
+                               w.head_dim ** -0.5, workspace=ws, stream=stream)
+
+    blk, row = slots // w.block_size, slots % w.block_size
+
+    def clear_new_slots():  # pools are [blocks, layers, Hkv, BS, D]
+        for pool in (t["k_pool"], t["v_pool"]):
+            pool[blk, 0, :, row, :] = 0
+
+    announce("fused append + decode under graph capture")
+    call(torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    eager = t["out"].clone()
+    kp, vp = t["k_pool"].clone(), t["v_pool"].clone()
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            call(s.cuda_stream)
+    torch.cuda.current_stream().wait_stream(s)
+    for r in range(4):
+        t["out"].fill_(float("nan"))
+        clear_new_slots()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(t["out"], eager), f"replay {r}: output differs from the eager call"
+        assert torch.equal(t["k_pool"], kp) and torch.equal(t["v_pool"], vp), \
+            f"replay {r}: pools differ from the eager call"
