@@ -432,7 +432,7 @@ __global__ void __launch_bounds__(64 * kDecodeWaves, 4) polar_decode_kernel(Deco
   // multiply and a signed remainder per tile. Splits of PolarQuant batches span at most 64 tiles
   // (plan_decode), so lane j holds tile t_begin + j.
   int64_t coff, moff;
-  uint64_t okm;
+  uint64_t okm, fullm;
   {
     const bool ok = blk0 >= 0 && blk0 < a.num_blocks;
     const int sl0 = ((t_begin + lane) * kPTile) % a.block_size;
@@ -440,6 +440,10 @@ __global__ void __launch_bounds__(64 * kDecodeWaves, 4) polar_decode_kernel(Deco
     coff = base + (int64_t)sl0 * HB;  // K codes; V token quads start at the same offset
     moff = base + mag_off + 2 * sl0;  // binary16 norms
     okm = __ballot(ok);
+    // bit j of fullm: tile t_begin + j lies inside [start_tok, L) and its block in the pool, so
+    // it needs no masking
+    const int rel = (t_begin + lane) * kPTile - start_tok;
+    fullm = __ballot(ok && rel >= 0 && rel + kPTile <= L - start_tok);
   }
 
   // One tile's loads: lane (g, n) holds 16 (D=64: 8) bytes of token n's K code row, 16 (8)
@@ -447,7 +451,7 @@ __global__ void __launch_bounds__(64 * kDecodeWaves, 4) polar_decode_kernel(Deco
   struct Stage {
     W kw, vw;
     uint2 km, vm;
-    bool ok;
+    bool ok, full;
   };
   // per-lane byte offsets inside a tile (the tile's base is wave-uniform: scalar address math)
   const uint32_t k_lane = n * HB + g * (HB / 4);
@@ -461,6 +465,7 @@ __global__ void __launch_bounds__(64 * kDecodeWaves, 4) polar_decode_kernel(Deco
   auto load_tile = [&](int t, Stage& s) {
     const int ti = t - t_begin;  // < tps <= 64
     s.ok = (okm >> ti) & 1;
+    s.full = (fullm >> ti) & 1;
     const int64_t c = readlane64(coff, ti), m = readlane64(moff, ti);
     const char* kt = a.kpool + c;
     const char* vt = a.vpool + c;
@@ -493,8 +498,7 @@ __global__ void __launch_bounds__(64 * kDecodeWaves, 4) polar_decode_kernel(Deco
       u[j] = s[j] * f16_bits_to_f32((uint16_t)((j < 2 ? cur.km.x : cur.km.y) >> (16 * (j & 1))));
       mv[j] = f16_bits_to_f32((uint16_t)((j < 2 ? cur.vm.x : cur.vm.y) >> (16 * (j & 1))));
     }
-    const int rel_tile = t * kPTile - start_tok;  // wave-uniform
-    if (!(cur.ok && rel_tile >= 0 && rel_tile + kPTile <= (int)span)) {
+    if (!cur.full) {
       // a tile that straddles start_tok or L, or an invalid block: mask its tokens (score -inf,
       // |v| 0). The empty asm keeps this a branch: full tiles do no masking work.
       asm volatile("");
