@@ -271,10 +271,14 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PrefillArgs a) {
   static_assert(NLD % 4 == 0, "tile loads go out in groups of four");
   // Interior tiles issue their loads in groups of four with instruction offsets 0, 1, 2, 3 KiB.
   // Contiguous K/V: the offsets come out of the lane offsets (still >= 0: load u's rows start at
-  // u RPI rows of at least RB bytes, u RPI RB = 1024 u). Paged: out of the per-load bases.
+  // u RPI rows of at least RB bytes, u RPI RB = 1024 u). Paged with blocks that hold whole groups
+  // (block_size a multiple of 4 RPI rows, so a group's rows lie in one block): the same, with one
+  // base per group. Smaller blocks: out of the per-load bases.
+  const bool group_blk = wave_uniform(PAGED && a.block_size % (4 * RPI) == 0);
   int voff_g[NLD];
 #pragma unroll
-  for (int u = 0; u < NLD; ++u) voff_g[u] = PAGED ? voff[u] : voff[u] - (u & 3) * 1024;
+  for (int u = 0; u < NLD; ++u)
+    voff_g[u] = (!PAGED || group_blk) ? voff[u] - (u & 3) * 1024 : voff[u];
   auto tile_interior = [&](int t0) __attribute__((always_inline)) {
     return t0 >= kv_lo && t0 + BN <= kv_hi;
   };
@@ -310,10 +314,19 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PrefillArgs a) {
         const uint64_t hi = (uint32_t)__builtin_amdgcn_readlane(vb_hi, u);
         return (const char*)(uintptr_t)((hi << 32) | lo);
       };
+      if (group_blk) {  // lane g (g % 4 == 0) holds its group's block; no offset taken off
 #pragma unroll
-      for (int g = 0; g < NLD; g += 4)
-        lds_dma16x4(base_of(g), base_of(g + 1), base_of(g + 2), base_of(g + 3), voff_g[g],
-                    voff_g[g + 1], voff_g[g + 2], voff_g[g + 3], dst + g * 1024);
+        for (int g = 0; g < NLD; g += 4) {
+          const char* b = base_of(g);
+          lds_dma16x4(b, b, b, b, voff_g[g], voff_g[g + 1], voff_g[g + 2], voff_g[g + 3],
+                      dst + g * 1024);
+        }
+      } else {
+#pragma unroll
+        for (int g = 0; g < NLD; g += 4)
+          lds_dma16x4(base_of(g), base_of(g + 1), base_of(g + 2), base_of(g + 3), voff_g[g],
+                      voff_g[g + 1], voff_g[g + 2], voff_g[g + 3], dst + g * 1024);
+      }
     } else {
       const char* sb = src_base + (int64_t)t0 * row_pitch;
 #pragma unroll
