@@ -702,6 +702,367 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PrefillArgs a) {
     }
 }
 
+// Contiguous-K/V variant for grids of several rounds of workgroups: 32-key tiles, so that the
+// workgroup fits three per CU (32 x 168 VGPRs per lane and 48 KiB of LDS), and a plain per-wave
+// order QK -> softmax -> PV on each tile, with the waves of the two other workgroups on the SIMD
+// filling its MFMA pipe while one wave runs its softmax (where prefill_kernel, at two workgroups
+// per CU, overlaps the two inside each wave instead). A workgroup's start-up (metadata, Q, the
+// first tiles) is then hidden behind two other workgroups rather than one. Tiles go HBM -> LDS
+// two ahead through three buffers. Same semantics, masks and arguments as prefill_kernel
+// (contiguous K/V, no key split).
+template <typename T, int D>
+__global__ void __launch_bounds__(256, 3) prefill_k32_kernel(PrefillArgs a) {
+  using M = PrefillMfma<T>;
+  constexpr int BN = 32, RB = D * 2, CPR = RB / 16, TILE = BN * RB;
+  constexpr int KC = D / 16, DB = D / 32;
+  constexpr int RPI = 1024 / RB;    // rows per 1 KiB load
+  constexpr int NLD = TILE / 2048;  // loads per wave per tile: waves 0-1 fill K, 2-3 fill V
+  constexpr int WROWS = NLD * RPI;  // rows of a tile one wave loads (half the tile)
+  static_assert(WROWS * 2 == BN, "two waves fill one tile");
+  static_assert(NLD == 4, "one group of four loads per wave and tile");
+  using C = PrefillCfg<D>;  // the row swizzle
+  __shared__ __attribute__((aligned(1024))) char kl[3][TILE];
+  __shared__ __attribute__((aligned(1024))) char vl[3][TILE];
+
+  // ---- workgroup -> (kv head, group member, sequence, query block), heavy query blocks first
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = wave_uniform(tid >> 6);
+  const int32_t* const cu_q_p = a.cu_q;
+  const int32_t* const cu_k_p = a.cu_k;
+  int id = blockIdx.x;
+  const int kvh = id % a.hkv;
+  id /= a.hkv;
+  const int gm = id % a.group;
+  id /= a.group;
+  const int seq = id % a.num_seqs;
+  const int qblk = a.num_qblocks - 1 - id / a.num_seqs;
+  const int h = kvh * a.group + gm;
+
+  const kconst_i32 cq = cu_q_p ? as_const(cu_q_p) + seq : as_const(kPrefillZeroPair);
+  const kconst_i32 ck = cu_k_p ? as_const(cu_k_p) + seq : as_const(kPrefillZeroPair);
+  const int cq0 = cq[0], cq1 = cq[1], ck0 = ck[0], ck1 = ck[1];
+  asm volatile("" ::"s"(ck0), "s"(ck1));  // keep the key-length loads ahead of the early exit
+  const int q_begin = cq0;
+  const int Lq = cu_q_p ? cq1 - cq0 : a.lq;
+  const int k_begin = ck0;
+  const int Lk = cu_k_p ? ck1 - ck0 : a.lk;
+  const int qs = qblk * kPrefillBM;
+  if (qs >= Lq) return;
+  const int qe = min(qs + kPrefillBM, Lq);
+  const int pos_off = (a.causal == SP_CAUSAL_TOP_LEFT) ? 0 : Lk - Lq;
+  // keys any query of this workgroup can see: [kv_lo, kv_hi)
+  int kv_lo = 0, kv_hi = Lk;
+  if (a.causal != SP_CAUSAL_NONE) kv_hi = min(Lk, qe - 1 + pos_off + 1);
+  if (a.window_left >= 0) kv_lo = max(0, qs + pos_off - a.window_left);
+  const int t_first = (kv_lo / BN) * BN, kv_end = kv_hi;
+
+  const int l32 = lane & 31, hh = lane >> 5;  // MFMA column (query) and half
+  const int i16 = lane & 15, g4 = lane >> 4;  // 16-lane group for the transpose reads
+
+  const char* qbase = (const char*)a.q +
+      ((a.cu_q ? (int64_t)q_begin * a.q_tok : (int64_t)seq * a.q_batch) + (int64_t)h * a.q_head) * 2;
+  char* obase = (char*)a.out +
+      ((a.cu_q ? (int64_t)q_begin * a.o_tok : (int64_t)seq * a.o_batch) + (int64_t)h * a.o_head) *
+          dtype_size((sp_dtype)a.out_dtype);
+  const int64_t kv0 = (a.cu_k ? (int64_t)k_begin * a.kv_tok : (int64_t)seq * a.kv_batch) +
+                      (int64_t)kvh * a.kv_head;
+  const bool v_wave = wave >= 2;
+  const int64_t row_pitch = (int64_t)a.kv_tok * 2;
+  const char* src_base = (const char*)(v_wave ? a.v : a.k) + kv0 * 2;
+  const int wrow0 = (wave & 1) * WROWS;
+
+  // ---- HBM -> LDS tile loads: wave w's load u moves rows (w & 1) WROWS + u RPI .. of the tile
+  // (K for waves 0-1, V for waves 2-3); lane `lane` takes physical chunk lane % CPR of row
+  // lane / CPR and fetches the logical chunk the swizzle puts there. Interior tiles share one
+  // scalar base and one M0 write for the four loads (instruction offsets 0-3 KiB); edge tiles
+  // clamp their rows into [kv_lo, kv_hi) (those scores are masked) with per-lane addresses.
+  int voff_g[NLD];
+#pragma unroll
+  for (int u = 0; u < NLD; ++u) {
+    const int r = wrow0 + u * RPI + lane / CPR;
+    voff_g[u] = (int)((int64_t)r * row_pitch) + 16 * ((lane % CPR) ^ C::swz(r)) - u * 1024;
+  }
+  auto issue_tile = [&](int t0, char* buf) __attribute__((always_inline)) {
+    char* dst = buf + wrow0 * RB;
+    if (t0 >= kv_lo && t0 + BN <= kv_hi) {
+      const char* sb = src_base + (int64_t)t0 * row_pitch;
+      lds_dma16x4(sb, sb, sb, sb, voff_g[0], voff_g[1], voff_g[2], voff_g[3], dst);
+      return;
+    }
+    int ln = lane;
+    asm volatile("" : "+v"(ln));
+#pragma unroll
+    for (int u = 0; u < NLD; ++u) {
+      const int R = wrow0 + u * RPI + ln / CPR, p = ln % CPR;
+      const int j = min(max(t0 + R, kv_lo), kv_hi - 1);
+      lds_dma16(src_base + (int64_t)j * row_pitch + (p ^ C::swz(R)) * 16, dst + u * 1024);
+    }
+  };
+
+  // Prologue: the first two tiles' loads go out ahead of the Q loads, and one wait covers all
+  // of them, so that no wait inside the key loop refers to Q.
+  int t0 = t_first;
+  if (t0 < kv_end) {
+    issue_tile(t0, v_wave ? vl[0] : kl[0]);
+    if (t0 + BN < kv_end) issue_tile(t0 + BN, v_wave ? vl[1] : kl[1]);
+  }
+  // ---- Q^T operand (B of the S^T MFMA): query wq0 + l32, dims 16c + 8hh .. +7, unscaled.
+  const int wq0 = qs + 32 * wave;
+  const int my_q = wq0 + l32;
+  const float c2 = a.scale_log2;  // > 0 (checked on the host)
+  uint4 qreg[KC];
+  {
+    const char* qp = qbase + (int64_t)min(my_q, qe - 1) * a.q_tok * 2;
+#pragma unroll
+    for (int c = 0; c < KC; ++c)
+      qreg[c] = my_q < qe ? *(const uint4*)(qp + (16 * c + 8 * hh) * 2) : make_uint4(0, 0, 0, 0);
+  }
+  __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+
+  // Online softmax state of query l32 (both lanes of a query hold the same values): m_run, the
+  // running maximum of the exponents x = q.k * scale * log2(e) (-inf before the first visible
+  // key); m_used, the offset subtracted from x (m_run once that is finite, else 0).
+  float m_run = -INFINITY, m_used = 0.f, l_run = 0.f;
+  pf_f32x16 acc[DB];
+#pragma unroll
+  for (int db = 0; db < DB; ++db)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[db][r] = 0.f;
+  pf_f32x16 zero16;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) zero16[r] = 0.f;
+
+  const int wq_lo = wq0, wq_hi = min(wq0 + 32, qe) - 1;  // this wave's queries (inclusive)
+  const bool wave_active = wq_lo < qe;
+  const int qpos = my_q + pos_off;
+  const int sw = C::swz(l32);
+  // A tile needs masking iff t0 < mask_below or t0 > mask_above (wave-uniform bounds).
+  int mask_below = kv_lo, mask_above = Lk - BN;
+  if (a.causal != SP_CAUSAL_NONE) mask_above = min(mask_above, wq_lo + pos_off - BN + 1);
+  if (a.window_left >= 0) mask_below = max(mask_below, wq_hi + pos_off - a.window_left);
+  mask_below = wave_uniform(mask_below);
+  mask_above = wave_uniform(mask_above);
+
+  // Lane parts of the LDS operand addresses: every operand of a tile sits at (lane part ^
+  // constant) + immediate offset.
+  const int k_lane = (l32 * RB) | (16 * (hh ^ sw));
+  const int rl = (g4 >> 1) * 4 + (i16 >> 2);
+  const int chl = (g4 & 1) * 2 + ((i16 & 3) >> 1);
+  const int v_lane0 = rl * RB + 16 * (chl ^ C::swz(rl)) + 8 * (i16 & 1);
+  const int v_lane1 = (rl + 8) * RB + 16 * (chl ^ C::swz(rl + 8)) + 8 * (i16 & 1);
+
+  // 32-aligned causal diagonal: the tile that starts at the wave's first query position is the
+  // triangle 8(r/4) + r%4 <= l32 - 4hh (later tiles are not visited).
+  const int diag0 = wave_uniform(wq_lo + pos_off);
+  const bool tri_ok = a.causal != SP_CAUSAL_NONE && pos_off >= 0 && (pos_off & 31) == 0 &&
+                      qe - 1 + pos_off < Lk;
+  const int tri_lim = l32 - 4 * hh;
+
+  // QK product S^T = K Q^T of the tile in LDS buffer kb: K operand i (k-step i) is row l32,
+  // chunk 2i + hh: k_lane ^ 32i. Four operand reads run ahead of the MFMAs.
+  constexpr int AHK = 4;
+  auto qk = [&](const char* kb, pf_f32x16& s) __attribute__((always_inline)) {
+    int kbl = k_lane;
+    asm volatile("" : "+v"(kbl));
+    auto read_k = [&](int i) __attribute__((always_inline)) {
+      return *(const uint4*)(kb + (kbl ^ (32 * i)));
+    };
+    uint4 kop[AHK];
+#pragma unroll
+    for (int i = 0; i < AHK; ++i) kop[i] = read_k(i);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < KC; ++i) {
+      const uint4 cur = kop[i % AHK];
+      if (i + AHK < KC) kop[i % AHK] = read_k(i + AHK);
+      s = M::mma(cur, qreg[i], i < 1 ? zero16 : s);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+
+  // Masks, only on tiles that cross the sequence end, the window edge, kv_lo or the causal
+  // diagonal. Score r of this lane is key t0 + 4hh + 8(r/4) + r%4.
+  const float* mrow = a.mask ? a.mask + (int64_t)seq * a.mask_b + (int64_t)h * a.mask_h +
+                                   (int64_t)min(my_q, qe - 1) * a.mask_q
+                             : nullptr;
+  auto apply_mask = [&](int t0, pf_f32x16& s) __attribute__((always_inline)) {
+    if (mrow) {
+      const int jb = t0 + 4 * hh;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int key = min(jb + 8 * (r >> 2) + (r & 3), Lk - 1);
+        s[r] += mrow[key] * a.inv_scale;
+      }
+    }
+    if (t0 < mask_below || t0 > mask_above) {
+      if (tri_ok && t0 >= mask_below && t0 == diag0) {
+        int tl = tri_lim;
+        asm volatile("" : "+v"(tl));
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s[r] = (8 * (r >> 2) + (r & 3) <= tl) ? s[r] : -INFINITY;
+      } else {
+        int lo = kv_lo, hi = Lk - 1;
+        if (a.causal != SP_CAUSAL_NONE) hi = min(hi, qpos);
+        if (a.window_left >= 0) lo = max(lo, qpos - a.window_left);
+        const int jb = t0 + 4 * hh;
+        const int olo = lo - jb, ohi = hi - jb;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int off = (r >> 2) * 8 + (r & 3);
+          s[r] = (off >= olo && off <= ohi) ? s[r] : -INFINITY;
+        }
+      }
+    }
+  };
+
+  // Softmax weights of one tile (FlashAttention-2 online softmax, Dao 2023) with a lazily raised
+  // maximum, as in prefill_kernel: p = 2^(s * scale * log2 e - m_used) packed to 16 bits; pb[ks]
+  // word c holds scores 8ks + 2c, +1; the row sums add the 16-bit values the PV product uses.
+  uint4 pb[2];
+  float la = 0.f, lb = 0.f;
+  auto weights_all = [&](const pf_f32x16& s, float off) __attribute__((always_inline)) {
+    la = 0.f;
+    lb = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int k0 = 2 * e;
+      const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[k0], c2, -off));
+      const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[k0 + 1], c2, -off));
+      const uint32_t w = M::pack(p0, p1);
+      const int ks = k0 >> 3, c = (k0 >> 1) & 3;
+      if (c == 0) pb[ks].x = w;
+      else if (c == 1) pb[ks].y = w;
+      else if (c == 2) pb[ks].z = w;
+      else pb[ks].w = w;
+      if (ks < 1) la = M::sum2(w, la);
+      else lb = M::sum2(w, lb);
+    }
+  };
+  constexpr float kLazyBound = 4096.f;  // 2^12
+  // Raise the maximum when this lane's weights of the tile sum past 2^12 or while the query has
+  // no maximum yet, and recompute the weights against the exact new maximum.
+  auto finish_weights = [&](const pf_f32x16& s) __attribute__((always_inline)) {
+    float lsum = la + lb;
+    if (__any(lsum > kLazyBound || m_run == -INFINITY)) {
+      float x = max3f(s[0], s[1], s[2]);
+      float y = max3f(s[8], s[9], s[10]);
+      x = max3f(x, s[3], s[4]);
+      y = max3f(y, s[11], s[12]);
+      x = max3f(x, s[5], s[6]);
+      y = max3f(y, s[13], s[14]);
+      x = max3f(x, s[7], y);
+      x = __builtin_fmaxf(x, s[15]);
+      float x0, x1;
+      swap_halves(x, x0, x1);
+      const float m_new = __builtin_fmaxf(m_run, __builtin_fmaxf(x0, x1) * c2);
+      const float used_new = (m_new == -INFINITY) ? 0.f : m_new;
+      const float alpha = __builtin_amdgcn_exp2f(m_run - used_new);  // 0 while m_run = -inf
+      weights_all(s, used_new);
+      lsum = la + lb;
+      m_run = m_new;
+      m_used = used_new;
+      l_run *= alpha;
+#pragma unroll
+      for (int db = 0; db < DB; ++db) acc[db] *= alpha;
+    }
+    l_run += lsum;
+  };
+
+  // PV product O^T += V^T P^T of the tile in LDS buffer vb: K-step ks covers tile tokens
+  // 16ks .. 16ks+15 in the S^T order; the V^T operand (ks, db) is rows 16ks + rl (+ 8), chunk
+  // 4db + chl. The first AH operands are read before the softmax (their LDS latency runs under
+  // it), the rest AH ahead of the MFMAs.
+  constexpr int NV = 2 * DB, AH = 2;
+  pf_s16x8 vop[AH];
+  auto read_v = [&](const char* vb, int ks, int db) __attribute__((always_inline)) {
+    const char* a0 = vb + 16 * ks * RB + (v_lane0 ^ (64 * db));
+    const char* a1 = vb + 16 * ks * RB + (v_lane1 ^ (64 * db));
+    const pf_s16x4 v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(a0));
+    const pf_s16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(a1));
+    return __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7);
+  };
+  auto pv_pre = [&](const char* vb) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < AH; ++i) vop[i] = read_v(vb, i / DB, i % DB);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  auto pv = [&](const char* vb) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const pf_s16x8 cur = vop[i % AH];
+      if (i + AH < NV) vop[i % AH] = read_v(vb, (i + AH) / DB, (i + AH) % DB);
+      acc[i % DB] = M::mma(cur, pb[i / DB], acc[i % DB]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+
+  // wave-uniform: does this wave see any key of the tile ([vis_lo, vis_hi), worked out once)
+  int vis_lo = -(1 << 30), vis_hi = wave_active ? kv_end : -(1 << 30);
+  if (a.causal != SP_CAUSAL_NONE) vis_hi = min(vis_hi, wq_hi + pos_off + 1);
+  if (a.window_left >= 0) vis_lo = wq_lo + pos_off - a.window_left - BN + 1;
+  vis_lo = wave_uniform(vis_lo);
+  vis_hi = wave_uniform(vis_hi);
+
+  // One step on tile t0 (K in kcur, V in vcur): wait for this wave's loads of t0 (those of
+  // t0 + BN, NLD DMAs issued after them, may stay in flight; the last tile waits for all), then
+  // for every wave's; the barrier also frees the buffers of t0 - BN, which take t0 + 2 BN.
+  pf_f32x16 sc;
+  auto step = [&](int t0, const char* kcur, const char* vcur, char* kload, char* vload)
+      __attribute__((always_inline)) {
+    if (t0 + BN < kv_end) __builtin_amdgcn_s_waitcnt(0x0F70 | NLD);
+    else __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+    __syncthreads();
+    if (t0 + 2 * BN < kv_end) issue_tile(t0 + 2 * BN, v_wave ? vload : kload);
+    if (t0 >= vis_lo && t0 < vis_hi) {
+      qk(kcur, sc);
+      pv_pre(vcur);
+      apply_mask(t0, sc);
+      float off = m_used;
+      asm volatile("" : "+v"(off));
+      weights_all(sc, off);
+      finish_weights(sc);
+      pv(vcur);
+    }
+  };
+  while (t0 < kv_end) {
+    step(t0, kl[0], vl[0], kl[2], vl[2]);
+    t0 += BN;
+    if (t0 >= kv_end) break;
+    step(t0, kl[1], vl[1], kl[0], vl[0]);
+    t0 += BN;
+    if (t0 >= kv_end) break;
+    step(t0, kl[2], vl[2], kl[1], vl[1]);
+    t0 += BN;
+  }
+
+  // ---- normalise and store: lane holds O^T[d][query l32], d = 32db + 8(r/4) + 4hh + r%4
+  float x0, x1;
+  swap_halves(l_run, x0, x1);
+  const float l = x0 + x1;
+  if (my_q >= qe) return;
+  const float inv = l > 0.f ? 1.f / l : 0.f;
+  constexpr int kSelf = std::is_same<T, bf16_t>::value ? SP_BF16 : SP_F16;  // out = in type
+  const int oes = dtype_size((sp_dtype)a.out_dtype);
+  char* op = obase + (int64_t)my_q * a.o_tok * oes;
+#pragma unroll
+  for (int db = 0; db < DB; ++db)
+#pragma unroll
+    for (int rg = 0; rg < 4; ++rg) {
+      const int d0 = db * 32 + rg * 8 + hh * 4;
+      const float o0 = acc[db][rg * 4 + 0] * inv, o1 = acc[db][rg * 4 + 1] * inv;
+      const float o2 = acc[db][rg * 4 + 2] * inv, o3 = acc[db][rg * 4 + 3] * inv;
+      if (a.out_dtype == SP_F32) {
+        *(float4*)(op + d0 * 4) = make_float4(o0, o1, o2, o3);
+      } else if (a.out_dtype == kSelf) {
+        *(uint2*)(op + d0 * 2) = make_uint2(M::pack(o0, o1), M::pack(o2, o3));
+      } else {  // the other 16-bit type
+        using O = PrefillMfma<typename std::conditional<kSelf == SP_BF16, f16_t, bf16_t>::type>;
+        *(uint2*)(op + d0 * 2) = make_uint2(O::pack(o0, o1), O::pack(o2, o3));
+      }
+    }
+}
+
 // Merge the split partials of one (sequence, head, group of kCombineRows query rows):
 // out = sum_s 2^(m_s - M) acc_s / sum_s 2^(m_s - M) l_s, M = max_s m_s (zeros when no split saw
 // a key). D/4 lanes per row, four output elements each, one row per lane group, so every row's
@@ -763,12 +1124,26 @@ size_t prefill_partials_bytes(int num_seqs, int max_seqlen_q, int hq, int head_d
   return (size_t)num_seqs * max_seqlen_q * hq * nsplit * (head_dim + 4) * sizeof(float);
 }
 
+#ifndef SP_K32_MIN_WGS
+#define SP_K32_MIN_WGS 1536
+#endif
+// Contiguous 16-bit prefills of at least this many workgroups (two rounds of prefill_k32_kernel's
+// three per CU on 256 CUs) run on prefill_k32_kernel; smaller grids keep prefill_kernel, whose
+// in-wave overlap of softmax and MFMA does not depend on other workgroups sharing the SIMD.
+constexpr int64_t kK32MinWorkgroups = SP_K32_MIN_WGS;
+
 template <typename T, int D>
 static int launch_td(const PrefillArgs& a, bool paged, hipStream_t stream) {
   const int64_t base = (int64_t)a.num_qblocks * a.num_seqs * a.hq;
   const int64_t blocks = base * (a.nsplit > 1 ? a.nsplit : 1);
   if (blocks <= 0) return SP_OK;
   if (blocks > 0x7fffffff) return fail(SP_EINVAL, "prefill: grid of %lld workgroups", (long long)blocks);
+  if constexpr (D == 128) {
+    if (!paged && a.nsplit <= 1 && base >= kK32MinWorkgroups) {
+      hipLaunchKernelGGL((prefill_k32_kernel<T, D>), dim3((unsigned)blocks), dim3(256), 0, stream, a);
+      return check_launch("prefill_k32_kernel");
+    }
+  }
   if (paged)
     hipLaunchKernelGGL((prefill_kernel<T, D, true>), dim3((unsigned)blocks), dim3(256), 0, stream, a);
   else
