@@ -19,8 +19,9 @@
  *     thread-local message. Nothing is thrown, aborted or exited across the ABI.
  *   - No entry point allocates device memory. Scratch space is caller-owned (workspace).
  *   - Calls are stateless and re-entrant; two calls that share a workspace must not overlap.
- *     (sp_ragged_paged_attention keeps one side stream and two events per device, made on its
- *     first mixed batch there; sp_paged_decode_noalloc one scratch array per device.)
+ *     (sp_ragged_paged_attention keeps one side stream and two events per device and caller
+ *     stream, made on the first mixed batch issued on that stream; sp_paged_decode_noalloc one
+ *     scratch array per device.)
  *
  * Paged pool layout (the reference's, paged_attention.rs:152-155):
  *   pool[num_blocks][num_layers][num_kv_heads][block_size][head_dim], one pool for K, one for V.
@@ -220,8 +221,10 @@ int sp_paged_append_decode(void* out, const void* q, void* k_pool, void* v_pool,
  * allocates nothing. No counterpart in the reference: it is for callers that cannot allocate
  * device memory (code under HIP graph capture, tight serving loops, harnesses that forbid
  * allocation). Same arguments and results as sp_paged_decode with the workspace it asks for
- * (the same split plan, so the same kernels and merge order). A batch whose partials exceed the
- * scratch (sp_paged_decode_workspace_size() > 32 MiB) returns SP_ENOSPACE before any launch.
+ * (the same split plan, so the same kernels and merge order). A batch whose dense split plan
+ * needs more than 32 MiB of partials returns SP_ENOSPACE before any launch. The figure
+ * sp_paged_decode_workspace_size() returns is the larger of the dense and the PolarQuant plans'
+ * needs, so it can exceed 32 MiB for a batch that still runs here.
  * Every call on one GPU shares that GPU's scratch: calls that overlap on one GPU (other streams,
  * other threads) race and must be serialised by the caller.
  */
@@ -286,10 +289,13 @@ int sp_paged_prefill(void* out, const void* q,
  * add one token each: decode (sp_paged_decode, no mask, llama.rs:255-260). Replaces the
  * per-sequence forward_cached calls of one scheduler iteration (transformer.rs:184-254 with
  * start_pos and the mask chosen per sequence as Llama::forward does, llama.rs:247-260). With
- * both groups present the decode runs on a library-owned side stream of the current device
- * (created on first use, default priority), forked from `stream` and joined back into it with
- * events, so it overlaps the chunks' prefill; the call is ordered on `stream` like one launch
- * (work after it on `stream` sees both halves) and can be captured into a graph.
+ * both groups present the decode runs on a library-owned side stream that belongs to `stream`
+ * (one per device and caller stream, created on first use, default priority), forked from
+ * `stream` and joined back into it with events, so it overlaps the chunks' prefill; the call is
+ * ordered on `stream` like one launch (work after it on `stream` sees both halves), mixed steps
+ * on different caller streams do not wait for each other, and the call can be captured into a
+ * graph. Past 256 caller streams the library makes no more side streams: later ones run the
+ * two halves one after the other on `stream`.
  *   q, out          : [total_q, Hq, D], the chunks' tokens first (num_prefill_tokens of them),
  *                     then one token per decode sequence
  *   cu_seqlens_q    : [num_prefill_seqs + 1] token offsets of the chunks (device); may be NULL

@@ -7,7 +7,9 @@
 #include <stdio.h>
 #include <stdlib.h>
 
+#include <map>
 #include <mutex>
+#include <utility>
 #include <string>
 
 #include "kv_cache.hpp"
@@ -539,41 +541,51 @@ size_t sp_ragged_attention_workspace_size(int32_t num_seqs, int32_t num_prefill_
   return need;
 }
 
-// The side stream and fork / join events of a mixed batch on one device, made on first use
-// (default priority, events without timing). g_fork_mu guards their creation and keeps each
-// call's record / wait pairs together when several host threads issue mixed batches.
+// The side stream and fork / join events of mixed batches issued on one caller stream of one
+// device, made on first use (default priority, events without timing). Each (device, caller
+// stream) pair has its own, so mixed steps on independent caller streams never queue behind each
+// other on a shared side stream, and a caller stream under graph capture pulls only its own side
+// stream into the capture. g_fork_mu guards the table and keeps each call's record / wait pairs
+// together when several host threads issue mixed batches on one caller stream.
 struct ForkJoin {
   hipStream_t side = nullptr;
   hipEvent_t fork = nullptr, join = nullptr;
 };
 static std::mutex g_fork_mu;
+// Past this many (device, caller stream) pairs a mixed batch runs both halves on the caller's
+// stream, one after the other (the table is never pruned: a stream handle may be reused).
+constexpr size_t kMaxForkJoins = 256;
 
-static int fork_join_for_current_device(ForkJoin** out) {
-  constexpr int kMaxDevices = 64;
-  static ForkJoin per_device[kMaxDevices];
+// *out = the pair's resources, or nullptr when the table is full. Call with g_fork_mu held.
+static int fork_join_for(hipStream_t caller, ForkJoin** out) {
+  static std::map<std::pair<int, uintptr_t>, ForkJoin> table;
   int dev = -1;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return fail(SP_EHIP, "mixed batch: hipGetDevice: %s", hipGetErrorString(e));
-  if (dev < 0 || dev >= kMaxDevices)
-    return fail(SP_EUNSUPPORTED, "mixed batch: device %d past the %d the library tracks", dev,
-                kMaxDevices);
-  ForkJoin& fj = per_device[dev];
-  if (!fj.side) {
-    hipStream_t s = nullptr;
-    hipEvent_t f = nullptr, j = nullptr;
-    if ((e = hipStreamCreateWithFlags(&s, hipStreamNonBlocking)) != hipSuccess ||
-        (e = hipEventCreateWithFlags(&f, hipEventDisableTiming)) != hipSuccess ||
-        (e = hipEventCreateWithFlags(&j, hipEventDisableTiming)) != hipSuccess) {
-      if (j) (void)hipEventDestroy(j);
-      if (f) (void)hipEventDestroy(f);
-      if (s) (void)hipStreamDestroy(s);
-      return fail(SP_EHIP, "mixed batch: side stream on device %d: %s", dev,
-                  hipGetErrorString(e));
-    }
-    fj.fork = f;
-    fj.join = j;
-    fj.side = s;
+  const auto key = std::make_pair(dev, (uintptr_t)caller);
+  auto it = table.find(key);
+  if (it != table.end()) {
+    *out = &it->second;
+    return SP_OK;
   }
+  if (table.size() >= kMaxForkJoins) {
+    *out = nullptr;
+    return SP_OK;
+  }
+  hipStream_t s = nullptr;
+  hipEvent_t f = nullptr, j = nullptr;
+  if ((e = hipStreamCreateWithFlags(&s, hipStreamNonBlocking)) != hipSuccess ||
+      (e = hipEventCreateWithFlags(&f, hipEventDisableTiming)) != hipSuccess ||
+      (e = hipEventCreateWithFlags(&j, hipEventDisableTiming)) != hipSuccess) {
+    if (j) (void)hipEventDestroy(j);
+    if (f) (void)hipEventDestroy(f);
+    if (s) (void)hipStreamDestroy(s);
+    return fail(SP_EHIP, "mixed batch: side stream on device %d: %s", dev, hipGetErrorString(e));
+  }
+  ForkJoin& fj = table[key];
+  fj.side = s;
+  fj.fork = f;
+  fj.join = j;
   *out = &fj;
   return SP_OK;
 }
@@ -640,7 +652,11 @@ int sp_ragged_paged_attention(void* out, const void* q, const void* k_pool, cons
   const hipStream_t caller = (hipStream_t)stream;
   std::lock_guard<std::mutex> lock(g_fork_mu);
   ForkJoin* fj = nullptr;
-  if (int rc = fork_join_for_current_device(&fj)) return rc;
+  if (int rc = fork_join_for(caller, &fj)) return rc;
+  if (!fj) {  // no side stream left for this caller stream: both halves on the caller's
+    if (int rc = prefill_half(pws, pws_bytes, stream)) return rc;
+    return launch_paged_decode(da, dtype, layout->head_dim, caller);
+  }
   hipError_t e = hipEventRecord(fj->fork, caller);
   if (e == hipSuccess) e = hipStreamWaitEvent(fj->side, fj->fork, 0);
   if (e != hipSuccess) return fail(SP_EHIP, "%s: fork: %s", fn, hipGetErrorString(e));

@@ -171,8 +171,8 @@ __global__ void __launch_bounds__(64 * kDecodeWaves, decode_min_waves<T>())
   const int seq = unit / a.hkv, kvh = unit - seq * a.hkv;
   const int G = a.group;
 
-  int L = a.context_lens[seq];
-  L = min(L, min(a.max_context_len, a.max_blocks_per_seq * a.block_size));
+  const int L_raw = a.context_lens[seq];
+  const int L = min(L_raw, min(a.max_context_len, a.max_blocks_per_seq * a.block_size));
   if (L <= 0) {
     if (split == 0) {
       for (int i = threadIdx.x; i < G * D; i += blockDim.x)
@@ -206,25 +206,31 @@ __global__ void __launch_bounds__(64 * kDecodeWaves, decode_min_waves<T>())
   const int64_t head_off = a.layer_off_b + (int64_t)kvh * a.block_size * RB;
   char* vst = smem + wave * C::WAVE_LDS;
 
-  // Fused append (sp_paged_append_decode): the step's new token of this sequence is its last
-  // position L - 1. The split that holds it stores the token's K and V rows of this KV head in
-  // the pool, at the slot the block table gives position L - 1 (skipped when that block id lies
-  // outside the pool, as sp_kv_append skips such a slot), and the tile holding L - 1 reads the
-  // row from k_new / v_new instead of the pool, so no other kernel has to run first.
+  // Fused append (sp_paged_append_decode): the step's new token of this sequence sits at position
+  // context_lens[seq] - 1. The last split stores the token's K and V rows of this KV head in the
+  // pool, at the slot the block table gives that position (skipped when the position lies past
+  // the table or its block id outside the pool, as sp_kv_append skips such a slot). When the
+  // token is attended (the length was not clamped to max_context_len or the table), the tile
+  // holding it reads the row from k_new / v_new instead of the pool, so no other kernel has to
+  // run first; a clamped length attends [0, L) without it, as sp_paged_decode would.
   const char* knew_row = nullptr;
   const char* vnew_row = nullptr;
   if (a.k_new) {
     const int64_t off_new = (int64_t)seq * a.new_tok_stride_b + (int64_t)kvh * a.new_head_stride_b;
-    knew_row = a.k_new + off_new;
-    vnew_row = a.v_new + off_new;
-    if (split == nsplit - 1 && wave == 0) {
-      const int p = L - 1;
+    if (L == L_raw) {
+      knew_row = a.k_new + off_new;
+      vnew_row = a.v_new + off_new;
+    }
+    const int p = L_raw - 1;
+    if (split == nsplit - 1 && wave == 0 && p < a.max_blocks_per_seq * a.block_size) {
       const int blk = table[p / a.block_size];
+      const char* kn = a.k_new + off_new;
+      const char* vn = a.v_new + off_new;
       if (blk >= 0 && blk < a.num_blocks) {
         const int64_t dst = (int64_t)blk * a.block_stride_b + head_off + (int64_t)(p % a.block_size) * RB;
         for (int o = lane * 16; o < RB; o += 64 * 16) {
-          *(uint4*)((char*)a.kpool + dst + o) = *(const uint4*)(knew_row + o);
-          *(uint4*)((char*)a.vpool + dst + o) = *(const uint4*)(vnew_row + o);
+          *(uint4*)((char*)a.kpool + dst + o) = *(const uint4*)(kn + o);
+          *(uint4*)((char*)a.vpool + dst + o) = *(const uint4*)(vn + o);
         }
       }
     }

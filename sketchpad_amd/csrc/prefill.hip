@@ -1138,6 +1138,10 @@ static int launch_td(const PrefillArgs& a, bool paged, hipStream_t stream) {
   const int64_t blocks = base * (a.nsplit > 1 ? a.nsplit : 1);
   if (blocks <= 0) return SP_OK;
   if (blocks > 0x7fffffff) return fail(SP_EINVAL, "prefill: grid of %lld workgroups", (long long)blocks);
+  // the split merge writes the input element type at head_dim columns
+  constexpr int kSelf = std::is_same<T, bf16_t>::value ? SP_BF16 : SP_F16;
+  if (a.nsplit > 1 && (a.out_dtype != kSelf || a.dv != D))
+    return fail(SP_EUNSUPPORTED, "prefill: a key split needs out_dtype = the input type and Dv = D");
   if constexpr (D == 128) {
     if (!paged && a.nsplit <= 1 && base >= kK32MinWorkgroups) {
       hipLaunchKernelGGL((prefill_k32_kernel<T, D>), dim3((unsigned)blocks), dim3(256), 0, stream, a);

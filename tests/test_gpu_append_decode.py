@@ -24,14 +24,16 @@ def _slots(w: W.DecodeWorkload) -> np.ndarray:
     return np.where(ok, blk * w.block_size + pos % w.block_size, -1).astype(np.int32)
 
 
-def fused_vs_separate(w: W.DecodeWorkload, k_new=None, v_new=None, oracle=True):
+def fused_vs_separate(w: W.DecodeWorkload, k_new=None, v_new=None, oracle=True, max_ctx=None):
+    """max_ctx: the max_context_len both calls get (default: the longest context); contexts past
+    it are attended up to it, and their new token is still appended at position L - 1."""
     announce(f"append+decode {w.name} B={w.num_seqs} Hq={w.hq} Hkv={w.hkv} D={w.head_dim} "
              f"BS={w.block_size} {w.dtype} window={w.window_left} maxL={w.max_context_len}")
     t = W.make_decode_tensors(w)
     lay = w.layout()
     kn = t["k_new"] if k_new is None else k_new
     vn = t["v_new"] if v_new is None else v_new
-    max_ctx = max(w.max_context_len, 1)
+    max_ctx = max(w.max_context_len, 1) if max_ctx is None else max_ctx
     scale = w.head_dim ** -0.5
     kp2, vp2 = t["k_pool"].clone(), t["v_pool"].clone()
     out2 = torch.empty_like(t["out"])
@@ -55,7 +57,7 @@ def fused_vs_separate(w: W.DecodeWorkload, k_new=None, v_new=None, oracle=True):
         return t, out2
     olay = O.make_layout(w.num_blocks, w.num_layers, w.layer, w.hkv, w.block_size, w.head_dim)
     ref = O.paged_decode_f64(host_array(t["q"]), host_array(kp2), host_array(vp2), olay,
-                             w.block_tables, w.context_lens, scale=scale,
+                             w.block_tables, np.minimum(w.context_lens, max_ctx), scale=scale,
                              window_left=w.window_left, dtype=oracle_dtype(t["q"]))
     assert_attention_close(as_f64(out2), ref, w.dtype, w.name)
     return t, out2
@@ -104,6 +106,22 @@ def test_append_decode_zero_length_and_out_of_pool_block():
     _, out = fused_vs_separate(w, oracle=False)
     o = as_f64(out)
     assert (o[0] == 0).all() and (o[4] == 0).all()
+
+
+def test_append_decode_context_past_max_context_len():
+    """context_lens above max_context_len: both paths append the token at position L - 1 and
+    attend the first max_context_len keys only, so the fused call writes no attended row (the
+    token's slot lies past them) and matches the two calls bit for bit."""
+    lens = np.array([40, 300, 129, 17, 300], np.int32)
+    rng = np.random.default_rng(53)
+    nblk = int(((lens + 15) // 16).sum())
+    tables = W._tables_from_pool(rng, lens, 16, nblk)
+    w = W.DecodeWorkload("past-max-ctx", 53, len(lens), 16, 4, 128, 16, "bf16", lens, tables, nblk)
+    t, _ = fused_vs_separate(w, max_ctx=129)
+    # sequence 1's new row landed at position 299, past the attended 129 keys
+    kp = host_array(t["k_pool"])
+    blk = int(tables[1, 299 // 16])
+    assert np.array_equal(kp[blk, 0, :, 299 % 16], host_array(t["k_new"])[1])
 
 
 def test_append_decode_block_size_32_and_multi_layer():

@@ -187,7 +187,7 @@ def test_ragged_mixed_graph_capture():
 
 def test_ragged_mixed_from_two_host_threads():
     """Two host threads issue mixed steps on their own streams, with their own buffers, at the
-    same time (the library's per-device side stream and events are shared): every output is
+    same time (each caller stream has its own side stream and events): every output is
     bit-identical to the same call made alone."""
     import threading
     w = W.MixedWorkload("mixed-threads", 82, np.array([64, 100], np.int32),
@@ -242,3 +242,82 @@ def test_ragged_mixed_from_two_host_threads():
         for r in runs:
             assert torch.equal(r[0]["out"], alone), "a concurrent call differs from the call alone"
 
+
+
+_INDEPENDENCE_CHILD = r'''
+import sys, time
+sys.path.insert(0, sys.argv[1])
+import numpy as np, torch
+import sketchpad_amd as sp
+from sketchpad_amd import workloads as W
+w = W.MixedWorkload("mixed-streams", 83, np.array([64, 100], np.int32),
+                    np.array([2000, 300], np.int32),
+                    np.array([3000, 17, 1500, 640], np.int32), 8, 2, 128, "bf16")
+runs = []
+for _ in range(2):
+    t = W.make_mixed_tensors(w)
+    lay = sp.layout(t["num_blocks"], 1, 0, w.hkv, w.block_size, w.head_dim)
+    ws = sp.alloc_ragged_workspace(w.num_seqs, w.num_prefill_seqs, int(w.chunk_lens.max()),
+                                   int(w.decode_lens.max()), w.hq, lay, t["block_tables"].shape[1])
+    sp.kv_append(t["k_pool"], t["v_pool"], lay, t["k_new"], t["v_new"], t["slot_mapping"])
+    runs.append((t, lay, ws, torch.cuda.Stream()))
+def call(r):
+    t, lay, ws, st = r
+    sp.ragged_paged_attention(t["out"], t["q"], t["k_pool"], t["v_pool"], lay, t["block_tables"],
+                              t["cu_seqlens_q"], t["context_lens"],
+                              num_prefill_seqs=w.num_prefill_seqs,
+                              num_prefill_tokens=w.num_prefill_tokens,
+                              prefill_max_seqlen_q=int(w.chunk_lens.max()),
+                              decode_max_context_len=int(w.decode_lens.max()),
+                              scale=w.head_dim ** -0.5, workspace=ws, stream=st.cuda_stream)
+for r in runs:  # first calls make each caller stream's side stream
+    call(r)
+torch.cuda.synchronize()
+alone = runs[1][0]["out"].clone()
+sa, sb = runs[0][3], runs[1][3]
+# calibrate a spin kernel of about 200 ms on stream A
+e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+with torch.cuda.stream(sa):
+    e0.record(); torch.cuda._sleep(1 << 22); e1.record()
+torch.cuda.synchronize()
+cycles = int((1 << 22) * 200.0 / max(e0.elapsed_time(e1), 1e-3))
+with torch.cuda.stream(sa):
+    e0.record(); torch.cuda._sleep(cycles); e1.record()
+call(runs[0])  # A's mixed step waits behind the spin kernel on its stream
+b0, b1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+runs[1][0]["out"].fill_(float("nan"))
+with torch.cuda.stream(sb):
+    b0.record()
+call(runs[1])  # B's, enqueued after A's, on its own caller stream
+with torch.cuda.stream(sb):
+    b1.record()
+torch.cuda.synchronize()
+same = bool(torch.equal(runs[1][0]["out"], alone))
+print(f"RESULT spin_ms={e0.elapsed_time(e1):.3f} b_ms={b0.elapsed_time(b1):.3f} same={same}",
+      flush=True)
+'''
+
+
+def test_ragged_mixed_steps_on_two_streams_do_not_wait_for_each_other():
+    """Each caller stream forks to a side stream of its own: stream A holds a ~200 ms spin kernel
+    ahead of its mixed step, and stream B's mixed step, enqueued after A's, completes in its own
+    time. (With one side stream shared by both callers, B's decode half would queue behind A's,
+    which waits for the spin kernel.) Run in a child process with eight hardware queues, so that
+    the four streams involved do not share one."""
+    import os
+    import subprocess
+    import sys
+    from pathlib import Path
+    root = str(Path(__file__).resolve().parent.parent)
+    announce("ragged mixed steps on two caller streams: independence (child process)")
+    env = dict(os.environ, GPU_MAX_HW_QUEUES="8")
+    proc = subprocess.run([sys.executable, "-c", _INDEPENDENCE_CHILD, root], env=env,
+                          stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True, timeout=240)
+    print(proc.stdout)
+    assert proc.returncode == 0, proc.stdout
+    line = [x for x in proc.stdout.splitlines() if x.startswith("RESULT")][-1]
+    vals = dict(kv.split("=") for kv in line.split()[1:])
+    spin, b = float(vals["spin_ms"]), float(vals["b_ms"])
+    assert vals["same"] == "True", "stream B's output differs from the call alone"
+    assert spin > 50.0, f"the spin kernel took only {spin} ms"
+    assert b < spin / 4, f"stream B's mixed step took {b} ms behind A's {spin} ms spin kernel"

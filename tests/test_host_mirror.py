@@ -1,8 +1,9 @@
-"""The C++ mirror of the reference's paged/flash attention API and its iteration-level scheduler
-(sketchpad_amd/host/), through the test binary tests/cpp/test_paged_attention: the restated
-reference unit tests (paged_attention.rs, continuous_batching.rs) on the CPU, and the device paths
-(store/gather round trips, paged cache == concat cache, flash attention, ragged-batch metadata and
-a continuous-batching loop checked against float64 attention) on the GPU."""
+"""The C++ mirror of the reference's paged/flash attention API (sketchpad_amd/host/), through the
+test binary tests/cpp/test_paged_attention: the restated reference unit tests of
+paged_attention.rs (block table, memory-budget config, causal mask entries, Result errors) on the
+CPU, and the device paths on the GPU: allocation and scheduler counts, store/gather round trips,
+paged cache == concat cache, flash attention with its options, ragged-batch metadata, a serving
+loop driven by a test-local schedule and a three-layer step, checked against float64 attention."""
 import subprocess
 from pathlib import Path
 
@@ -21,8 +22,7 @@ def _run(args):
 
 
 def test_mirror_reference_unit_tests_cpu():
-    """test_block_table, test_config_from_memory_budget, causal mask entries, Result errors, and
-    the scheduler tests of continuous_batching.rs with its tie-breaking."""
+    """test_block_table, test_config_from_memory_budget, causal mask entries and Result errors."""
     _run(["--cpu-only"])
 
 

@@ -70,3 +70,32 @@ def test_noalloc_decode_rejects_batches_past_the_scratch():
         sp.paged_decode_noalloc(torch.empty_like(q), q, pool, pool, lay, tables, lens, 32768,
                                 128 ** -0.5)
     assert e.value.code == sp._lib.SP_ENOSPACE and "scratch" in e.value.message
+
+
+def test_noalloc_decode_runs_where_only_the_polar_plan_passes_the_scratch():
+    """sp_paged_decode_workspace_size covers both pool kinds, so it can exceed the 32 MiB scratch
+    for a batch whose dense split plan fits it: 89 sequences x 16 query heads over one KV head
+    with max_context_len 23,552 plan 23 dense splits (17.3 MB of partials) against 46 PolarQuant
+    ones (34.6 MB). The no-allocation call runs such a batch (the scratch check is the dense
+    plan's), bit-identical to sp_paged_decode with the workspace it asks for."""
+    w = W.random_decode(seed=779, num_seqs=89, hq=16, hkv=1, head_dim=128, block_size=16,
+                        dtype="bf16", min_len=1, max_len=300)
+    max_ctx = 23552
+    t = W.make_decode_tensors(w)
+    lay = w.layout()
+    need = sp.paged_decode_workspace_size(w.num_seqs, w.hq, max_ctx, -1, lay)
+    assert need > 32 << 20, need
+    ws = sp.alloc_decode_workspace(w.num_seqs, w.hq, max_ctx, -1, lay)
+    ref = torch.full_like(t["out"], float("nan"))
+    got = torch.full_like(t["out"], float("nan"))
+    # tables as wide as max_context_len needs; the columns past each context are unused (-1)
+    tables = torch.full((w.num_seqs, max_ctx // w.block_size), -1, dtype=torch.int32,
+                        device="cuda")
+    tables[:, :t["block_tables"].shape[1]] = t["block_tables"]
+    announce(f"decode noalloc past-polar-plan B={w.num_seqs} Hq={w.hq} maxL={max_ctx}")
+    sp.paged_decode(ref, t["q"], t["k_pool"], t["v_pool"], lay, tables,
+                    t["context_lens"], max_ctx, w.head_dim ** -0.5, workspace=ws)
+    sp.paged_decode_noalloc(got, t["q"], t["k_pool"], t["v_pool"], lay, tables,
+                            t["context_lens"], max_ctx, w.head_dim ** -0.5)
+    torch.cuda.synchronize()
+    assert torch.equal(got, ref)
