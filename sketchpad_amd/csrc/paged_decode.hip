@@ -146,12 +146,15 @@ struct DecodeCfg {
 };
 typedef __attribute__((address_space(3))) s16x4_v lds_s16x4_v;
 
-// 16-bit kernels fit four waves per SIMD (<= 128 VGPRs, no spills); f32 D=128 would spill.
-template <typename T>
-constexpr int decode_min_waves() { return Elem<T>::bytes == 4 ? 1 : 4; }
+// 16-bit kernels fit four waves per SIMD (<= 128 VGPRs, no spills), three for sub-tile blocks;
+// f32 D=128 would spill.
+template <typename T, bool SUB>
+constexpr int decode_min_waves() { return Elem<T>::bytes == 4 ? 1 : (SUB ? 3 : 4); }
 
-template <typename T, int D>
-__global__ void __launch_bounds__(64 * kDecodeWaves, decode_min_waves<T>())
+// SUB: block sizes below the 16-token tile (1, 2, 4 or 8, dividing it), so that a tile spans
+// several blocks; every row of a tile then takes the block its position maps to.
+template <typename T, int D, bool SUB>
+__global__ void __launch_bounds__(64 * kDecodeWaves, (decode_min_waves<T, SUB>()))
     paged_decode_kernel(DecodeArgs a) {
   using C = DecodeCfg<T, D>;
   constexpr int ES = C::ES, RB = C::RB, NL = C::NL, VP = C::VP, ND = C::ND;
@@ -240,11 +243,13 @@ __global__ void __launch_bounds__(64 * kDecodeWaves, decode_min_waves<T>())
   // t_begin + j in blk0 and of tile t_begin + 64 + j in blk1 (tps <= 128), so no tile load waits
   // on a dependent block-table read.
   int blk0 = 0, blk1 = 0;
-  {
+  if constexpr (!SUB) {
     const int n_tiles = t_end - t_begin;
     if (lane < n_tiles) blk0 = table[((t_begin + lane) * kTile) / a.block_size];
     if (lane + 64 < n_tiles) blk1 = table[((t_begin + 64 + lane) * kTile) / a.block_size];
   }
+  // SUB: the tile's rows lie in kTile / block_size blocks (block_size a power of two)
+  const int bs_shift = SUB ? 31 - __builtin_clz(a.block_size) : 0;
 
   // Tile loads. K in MFMA A-operand order (token n, 16 bytes at c*64 + g*16); V coalesced
   // (lane-linear 16-byte chunks of the contiguous 16 x RB tile). Rows outside [start_tok, L)
@@ -255,13 +260,14 @@ __global__ void __launch_bounds__(64 * kDecodeWaves, decode_min_waves<T>())
   auto ldnt = [](const char* p) {
     return __builtin_bit_cast(uint4, __builtin_nontemporal_load((const u32x4_v*)p));
   };
-  auto load_tile = [&](int t, uint4* kr, uint4* vr, bool& ok) {
+  auto load_tile_blk = [&](int t, uint4* kr, uint4* vr, uint32_t& okm) {
     const int pos0 = t * kTile;
     const int ti = t - t_begin;  // wave-uniform, < tps
     const int b0 = __builtin_amdgcn_readlane(blk0, ti & 63);
     const int b1 = __builtin_amdgcn_readlane(blk1, ti & 63);
     const int blk = ti < 64 ? b0 : b1;
-    ok = blk >= 0 && blk < a.num_blocks;
+    const bool ok = blk >= 0 && blk < a.num_blocks;
+    okm = ok ? 0xFFFFu : 0u;
     const int64_t base = (int64_t)(ok ? blk : 0) * a.block_stride_b + head_off +
                          (int64_t)(pos0 % a.block_size) * RB;
     const int rlo = max(start_tok - pos0, 0), rhi = min(L - pos0, kTile) - 1;  // valid rows
@@ -299,6 +305,44 @@ __global__ void __launch_bounds__(64 * kDecodeWaves, decode_min_waves<T>())
       vr[i] = ldnt(a.vpool + base + o);
     }
   };
+  // SUB: the rows of one tile lie in kTile / block_size blocks. Lane r < 16 reads the block id
+  // of row r (ok: bit r set when that block lies in the pool), and each load takes its row's
+  // block through a lane shuffle (every lane takes part in it).
+  auto load_tile_sub = [&](int t, uint4* kr, uint4* vr, uint32_t& okm) {
+    const int pos0 = t * kTile;
+    const int rlo = max(start_tok - pos0, 0), rhi = min(L - pos0, kTile) - 1;  // valid rows
+    int rblk = 0;
+    if (lane < kTile) rblk = table[min(pos0 + lane, L - 1) >> bs_shift];
+    const bool okr = rblk >= 0 && rblk < a.num_blocks;
+    okm = (uint32_t)__builtin_amdgcn_ballot_w64(okr) & 0xFFFFu;
+    rblk = okr ? rblk : 0;
+    auto row_off = [&](int r) -> int64_t {
+      const int b = __shfl(rblk, r, 64);
+      return (int64_t)b * a.block_stride_b + head_off +
+             (int64_t)((pos0 + r) & (a.block_size - 1)) * RB;
+    };
+    const bool has_new = knew_row && pos0 + kTile > L - 1;  // the fused append's token (row rhi)
+    if constexpr (kF32) {
+      const int kr_row = min(max(n, rlo), rhi);
+      const int64_t ko = row_off(kr_row);
+      const char* kb = has_new && kr_row == rhi ? knew_row : a.kpool + ko;
+#pragma unroll
+      for (int c = 0; c < NL; ++c) kr[c] = ldnt(kb + c * 64 + g * 16);
+    }
+#pragma unroll
+    for (int i = 0; i < NL; ++i) {
+      const int off = (i * 64 + lane) * 16;
+      const int row = min(max(off / RB, rlo), rhi);
+      const int64_t o = row_off(row) + off % RB;
+      const bool nw = has_new && row == rhi;
+      if constexpr (!kF32) kr[i] = ldnt(nw ? knew_row + off % RB : a.kpool + o);
+      vr[i] = ldnt(nw ? vnew_row + off % RB : a.vpool + o);
+    }
+  };
+  auto load_tile = [&](int t, uint4* kr, uint4* vr, uint32_t& okm) {
+    if constexpr (SUB) load_tile_sub(t, kr, vr, okm);
+    else load_tile_blk(t, kr, vr, okm);
+  };
 
   float m_run = -INFINITY, l_run = 0.f;
   f32x4_v acc[ND];
@@ -306,11 +350,11 @@ __global__ void __launch_bounds__(64 * kDecodeWaves, decode_min_waves<T>())
   for (int i = 0; i < ND; ++i) acc[i] = f32x4_v{0.f, 0.f, 0.f, 0.f};
 
   uint4 kc[NL], vc[NL];
-  bool ok_c = false;
+  uint32_t ok_c = 0;
   int t = t_begin + wave;
   if (t < t_end) load_tile(t, kc, vc, ok_c);
   for (; t < t_end; t += kDecodeWaves) {
-    const bool tile_ok = ok_c;
+    const uint32_t tile_ok = ok_c;
 
     f32x4_v s = {0.f, 0.f, 0.f, 0.f};
     if constexpr (kF32) {
@@ -360,7 +404,7 @@ __global__ void __launch_bounds__(64 * kDecodeWaves, decode_min_waves<T>())
     float sv[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const bool valid = tile_ok && pos + j >= start_tok && pos + j < L;
+      const bool valid = ((tile_ok >> (4 * g + j)) & 1) && pos + j >= start_tok && pos + j < L;
       sv[j] = valid ? s[j] * a.scale_log2 : -INFINITY;
     }
     float mt = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
@@ -569,7 +613,10 @@ DecodePlan plan_decode(int num_seqs, int hq, int hkv, int head_dim, int max_cont
 template <typename T, int D>
 static int launch_typed(const DecodeArgs& a, hipStream_t stream) {
   const dim3 grid(a.num_seqs * a.hkv, a.max_splits);
-  hipLaunchKernelGGL((paged_decode_kernel<T, D>), grid, dim3(64 * kDecodeWaves), 0, stream, a);
+  if (a.block_size < kTile)
+    hipLaunchKernelGGL((paged_decode_kernel<T, D, true>), grid, dim3(64 * kDecodeWaves), 0, stream, a);
+  else
+    hipLaunchKernelGGL((paged_decode_kernel<T, D, false>), grid, dim3(64 * kDecodeWaves), 0, stream, a);
   if (a.max_splits > 1)
     hipLaunchKernelGGL((decode_combine_kernel<T, D>), dim3(a.hq, a.num_seqs), dim3(64), 0, stream,
                        a);

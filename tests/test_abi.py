@@ -91,7 +91,9 @@ def test_decode_validation(sp_lib):
     _expect(_lib.SP_EOOB, call(_lay(), max_ctx=33), "exceeds the block tables")
     _expect(_lib.SP_EINVAL, call(_lay(), window=-2), "window_left")
     _expect(_lib.SP_EINVAL, call(_lay(), scale=float("inf")), "scale")
-    _expect(_lib.SP_EUNSUPPORTED, call(_lay(block_size=8), mbs=4), "block_size 8")
+    # block sizes must divide the 16-token tile or be multiples of it (8 and 32 run, 12 and 24 not)
+    _expect(_lib.SP_EUNSUPPORTED, call(_lay(block_size=12), mbs=4), "block_size 12")
+    _expect(_lib.SP_EUNSUPPORTED, call(_lay(block_size=24), mbs=4), "block_size 24")
     # a batch needing split-K partials refuses a missing workspace
     lay = _lay(num_blocks=4096)
     need = sp_lib.sp_paged_decode_workspace_size(3, 4, 4096, -1, ctypes.byref(lay))

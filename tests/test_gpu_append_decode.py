@@ -124,6 +124,16 @@ def test_append_decode_context_past_max_context_len():
     assert np.array_equal(kp[blk, 0, :, 299 % 16], host_array(t["k_new"])[1])
 
 
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("bs", [1, 4, 8])
+def test_append_decode_block_sizes_below_the_tile(dtype, bs):
+    """Tiles spanning several blocks: the new token's row comes from k_new / v_new whatever block
+    of its tile holds it."""
+    fused_vs_separate(W.random_decode(seed=5500 + bs + len(dtype), num_seqs=6, hq=16, hkv=4,
+                                      head_dim=128, block_size=bs, dtype=dtype, min_len=1,
+                                      max_len=600))
+
+
 def test_append_decode_block_size_32_and_multi_layer():
     fused_vs_separate(W.random_decode(seed=5300, num_seqs=4, hq=32, hkv=8, head_dim=128,
                                       block_size=32, dtype="bf16", min_len=1, max_len=700))

@@ -112,6 +112,55 @@ def test_decode_block_size_32():
     check(w)
 
 
+@pytest.mark.parametrize("dtype", ["f32", "bf16", "f16"])
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("bs", [1, 2, 4, 8])
+def test_decode_block_sizes_below_the_tile(dtype, d, bs):
+    """Block sizes that divide the 16-token tile (the reference's BlockTable takes any size; its
+    own test uses 4, paged_attention.rs:568-598): every tile then spans several blocks of a
+    shuffled table. Lengths cross many tile and block edges, and split the keys."""
+    w = W.random_decode(seed=600 + bs * 10 + d + len(dtype), num_seqs=6, hq=16, hkv=4,
+                        head_dim=d, block_size=bs, dtype=dtype, min_len=1, max_len=1500)
+    check(w)
+
+
+@pytest.mark.parametrize("bs", [4, 8])
+def test_decode_block_sizes_below_the_tile_window(bs):
+    w = W.random_decode(seed=700 + bs, num_seqs=5, hq=32, hkv=8, head_dim=128, block_size=bs,
+                        dtype="bf16", min_len=50, max_len=900, window_left=200)
+    check(w)
+
+
+@pytest.mark.parametrize("bs", [4, 8])
+def test_decode_block_sizes_below_the_tile_out_of_pool_block(bs):
+    """A block id outside the pool in the middle of a tile masks that block's rows only (the
+    reference panics on such an id, "Block not allocated", paged_attention.rs:242; this build
+    skips the rows): the output is attention over the sequence's other keys, computed here in
+    float64 from the pool."""
+    w = W.random_decode(seed=800 + bs, num_seqs=3, hq=8, hkv=2, head_dim=128, block_size=bs,
+                        dtype="bf16", min_len=100, max_len=400)
+    bad = 16 // bs + 1  # the second block of the sequence's second tile
+    w.block_tables[1, bad] = -1
+    announce(f"decode sub-tile blocks BS={bs} with block {bad} of sequence 1 outside the pool")
+    t = run_step(w)
+    got = as_f64(t["out"])
+    kp = t["k_pool"].double().cpu().numpy()
+    vp = t["v_pool"].double().cpu().numpy()
+    q = t["q"].double().cpu().numpy()
+    for s_ in range(w.num_seqs):
+        L = int(w.context_lens[s_])
+        pos = [p for p in range(L) if w.block_tables[s_, p // bs] >= 0]
+        blk = [int(w.block_tables[s_, p // bs]) for p in pos]
+        for h in range(w.hq):
+            kvh = h // (w.hq // w.hkv)
+            k = np.stack([kp[b_, 0, kvh, p % bs] for b_, p in zip(blk, pos)])
+            v = np.stack([vp[b_, 0, kvh, p % bs] for b_, p in zip(blk, pos)])
+            sc = k @ q[s_, h] * w.head_dim ** -0.5
+            pr = np.exp(sc - sc.max())
+            ref = pr @ v / pr.sum()
+            assert np.abs(got[s_, h] - ref).max() <= 2e-2, (s_, h)
+
+
 def test_decode_many_splits_and_repeat_calls():
     """Long contexts (many split-K partials); a second call on the same workspace matches."""
     w = W.random_decode(seed=321, num_seqs=3, hq=32, hkv=8, head_dim=128, block_size=16,
