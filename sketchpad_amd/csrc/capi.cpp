@@ -249,8 +249,10 @@ static int decode_setup(const char* fn, void* out, const void* q, const void* k_
     return fail(SP_EUNSUPPORTED, "%s: GQA group %d > %d has no kernel", fn, group,
                 kDecodeMaxGroup);
   const int D = layout->head_dim;
-  if (D != 64 && D != 128)
-    return fail(SP_EUNSUPPORTED, "%s: head_dim %d has no kernel (64, 128)", fn, D);
+  const bool d256 = D == 256 && dtype != SP_F32 && kind == DecodeKind::Dense;
+  if (D != 64 && D != 128 && !d256)
+    return fail(SP_EUNSUPPORTED,
+                "%s: head_dim %d has no kernel (64, 128; 256 for 16-bit dense pools)", fn, D);
   if (window_left < -1) return fail(SP_EINVAL, "%s: window_left %d < -1", fn, window_left);
   if ((int64_t)max_context_len > (int64_t)max_blocks_per_seq * layout->block_size)
     return fail(SP_EOOB, "%s: max_context_len %d exceeds the block tables (%d blocks of %d)", fn,
@@ -366,7 +368,8 @@ int sp_paged_decode_noalloc(void* out, const void* q, const void* k_pool, const 
 }
 
 // dense_f32: the dense f32 path (flash_attention), which also takes head dims 40, 80, 160 and
-// 256 and a value head dim of its own; everything else runs head_dim 64 or 128, Dv == D.
+// 256 and a value head dim of its own; everything else runs head_dim 64 or 128, Dv == D (and
+// 256 for 16-bit tensors).
 static int check_prefill_common(const char* fn, int32_t num_seqs, int32_t max_seqlen_q,
                                 int32_t hq, int32_t hkv, int32_t D, float scale,
                                 int32_t causal, int32_t window_left, sp_dtype dtype,
@@ -386,10 +389,11 @@ static int check_prefill_common(const char* fn, int32_t num_seqs, int32_t max_se
                   "%s: f32 head_dim %d / value head_dim %d has no kernel (head_dim 40, 64, 80, "
                   "128, 160 or 256; value head_dim a multiple of 4 up to 256)",
                   fn, D, Dv);
-  } else if ((D != 64 && D != 128) || Dv != D) {
+  } else if ((D != 64 && D != 128 && !(D == 256 && dtype != SP_F32)) || Dv != D) {
     return fail(SP_EUNSUPPORTED,
-                "%s: head_dim %d / value head_dim %d has no %s kernel (64 or 128, equal)", fn, D,
-                Dv, dtype_name(dtype));
+                "%s: head_dim %d / value head_dim %d has no %s kernel (64 or 128, and 256 for "
+                "16-bit tensors; equal)",
+                fn, D, Dv, dtype_name(dtype));
   }
   if (causal < SP_CAUSAL_NONE || causal > SP_CAUSAL_TOP_LEFT)
     return fail(SP_EINVAL, "%s: unknown causal mode %d", fn, causal);
@@ -445,6 +449,7 @@ int sp_varlen_prefill(void* out, const void* q, const void* k, const void* v,
 // bound is the block tables' width), lowered until the partials fit the caller's workspace.
 static int prefill_splits(int32_t num_seqs, int32_t max_seqlen_q, int32_t num_q_heads,
                           int32_t head_dim, int64_t max_context, size_t workspace_bytes) {
+  if (head_dim == 256) return 1;  // the head-dim-256 kernel walks every key tile itself
   const int64_t base = (int64_t)((max_seqlen_q + kPrefillBM - 1) / kPrefillBM) * num_seqs *
                        num_q_heads;
   int s = plan_prefill_splits(base, (max_context + kPrefillBN - 1) / kPrefillBN);

@@ -139,22 +139,26 @@ struct DecodeCfg {
   static constexpr int LDS = (kDecodeWaves * WAVE_LDS > MERGE_LDS) ? kDecodeWaves * WAVE_LDS : MERGE_LDS;
   // Chunk swizzle of the 16-bit stages: the K operand read (16 rows at one logical chunk) and
   // the V transpose read (8 consecutive rows x 32 bytes per 32 lanes) hit distinct banks.
+  // (Rows of 32 chunks, D = 256, take the 16-chunk pattern: it only needs to separate the rows
+  // within 256 bytes of banks.)
   __device__ __forceinline__ static int swz(int row) {
-    if constexpr (CPR == 16) return ((row & 7) << 1) | ((row >> 3) & 1);
+    if constexpr (CPR >= 16) return ((row & 7) << 1) | ((row >> 3) & 1);
     else return (((row >> 1) & 3) << 1) | ((row >> 3) & 1);
   }
 };
 typedef __attribute__((address_space(3))) s16x4_v lds_s16x4_v;
 
-// 16-bit kernels fit four waves per SIMD (<= 128 VGPRs, no spills), three for sub-tile blocks;
-// f32 D=128 would spill.
-template <typename T, bool SUB>
-constexpr int decode_min_waves() { return Elem<T>::bytes == 4 ? 1 : (SUB ? 3 : 4); }
+// 16-bit kernels fit four waves per SIMD (<= 128 VGPRs, no spills), three for sub-tile blocks
+// and two at head_dim 256; f32 D=128 would spill.
+template <typename T, int D, bool SUB>
+constexpr int decode_min_waves() {
+  return Elem<T>::bytes == 4 ? 1 : (D == 256 ? 2 : (SUB ? 3 : 4));
+}
 
 // SUB: block sizes below the 16-token tile (1, 2, 4 or 8, dividing it), so that a tile spans
 // several blocks; every row of a tile then takes the block its position maps to.
 template <typename T, int D, bool SUB>
-__global__ void __launch_bounds__(64 * kDecodeWaves, (decode_min_waves<T, SUB>()))
+__global__ void __launch_bounds__(64 * kDecodeWaves, (decode_min_waves<T, D, SUB>()))
     paged_decode_kernel(DecodeArgs a) {
   using C = DecodeCfg<T, D>;
   constexpr int ES = C::ES, RB = C::RB, NL = C::NL, VP = C::VP, ND = C::ND;
@@ -628,6 +632,9 @@ static int launch_t(const DecodeArgs& a, int head_dim, hipStream_t stream) {
   switch (head_dim) {
     case 64: return launch_typed<T, 64>(a, stream);
     case 128: return launch_typed<T, 128>(a, stream);
+    case 256:  // 16-bit pools only (Gemma-4's sliding layers, griffin)
+      if constexpr (Elem<T>::bytes == 2) return launch_typed<T, 256>(a, stream);
+      [[fallthrough]];
     default: return fail(SP_EUNSUPPORTED, "paged decode: head_dim %d has no kernel", head_dim);
   }
 }

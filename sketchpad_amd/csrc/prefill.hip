@@ -99,8 +99,10 @@ struct PrefillCfg {
   // XOR swizzle of a row's 16-byte chunks (a permutation of 0..CPR-1 that depends on the row's
   // low four bits). Chosen so that 16 consecutive rows at one logical chunk, and 4 consecutive
   // rows x 64 logical bytes, land on distinct LDS banks.
+  // (Rows of 32 chunks, D = 256, take the 16-chunk permutation: it only has to separate rows
+  // within 256 bytes of banks.)
   __device__ __forceinline__ static int swz(int row) {
-    if constexpr (CPR == 16) return ((row & 3) << 2) | ((row >> 2) & 3);
+    if constexpr (CPR >= 16) return ((row & 3) << 2) | ((row >> 2) & 3);
     else return (((row >> 1) & 1) << 2) | ((row >> 2) & 3);
   }
 };
@@ -1063,6 +1065,510 @@ __global__ void __launch_bounds__(256, 3) prefill_k32_kernel(PrefillArgs a) {
     }
 }
 
+// Head dim 256 (Gemma-4's sliding-window layers, gemma4.rs:94-102; griffin.rs:63): prefill_kernel's
+// per-wave state does not fit at this width (O^T alone is 128 VGPRs per lane), so 32-key tiles
+// (one 32 x 32 score block, 16 VGPRs) with the softmax between the two products, two workgroups
+// per CU and the tiles loaded one ahead through two buffers (64 KiB of LDS). Contiguous and
+// paged K/V, the same masks and arguments as prefill_kernel; no key split.
+template <typename T, int D, bool PAGED>
+__global__ void __launch_bounds__(256, 2) prefill_wide_kernel(PrefillArgs a) {
+  using C = PrefillCfg<D>;  // the row swizzle
+  using M = PrefillMfma<T>;
+  constexpr int BN = 32, RB = C::RB, CPR = C::CPR, TILE = BN * RB;
+  constexpr int KC = C::KC, DB = C::DB;
+  constexpr int RPI = 1024 / RB;       // rows per 1 KiB load
+  constexpr int NLD = TILE / 2048;     // loads per wave per tile: waves 0-1 fill K, 2-3 fill V
+  constexpr int WROWS = NLD * RPI;     // rows of a tile one wave loads (half the tile)
+  static_assert(WROWS * 2 == BN, "two waves fill one tile");
+  __shared__ __attribute__((aligned(1024))) char kl[2][TILE];
+  __shared__ __attribute__((aligned(1024))) char vl[2][TILE];
+
+  // ---- workgroup -> (kv head, group member, sequence, split, query block), heavy query blocks
+  // first; wave w takes queries 32w .. 32w + 31 of the block
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = wave_uniform(tid >> 6);
+  // the metadata pointers are read with the grid shape, in the first batch of argument loads
+  const int32_t* const cu_q_p = a.cu_q;
+  const int32_t* const cu_k_p = PAGED ? a.context_lens : a.cu_k;
+  int id = blockIdx.x;
+  const int kvh = id % a.hkv;
+  id /= a.hkv;
+  const int gm = id % a.group;
+  id /= a.group;
+  const int seq = id % a.num_seqs;
+  id /= a.num_seqs;
+  const int split = id % a.nsplit;
+  const int qblk = a.num_qblocks - 1 - id / a.nsplit;
+  const int h = kvh * a.group + gm;
+
+  // Sequence offsets and lengths. The scalar loads are issued whatever the layout (a batch
+  // without cu_q / cu_k reads a zero pair instead), so they go out together and are waited for
+  // once.
+  const kconst_i32 cq = cu_q_p ? as_const(cu_q_p) + seq : as_const(kPrefillZeroPair);
+  const kconst_i32 ck = PAGED || cu_k_p ? as_const(cu_k_p) + seq : as_const(kPrefillZeroPair);
+  const int cq0 = cq[0], cq1 = cq[1], ck0 = ck[0], ck1 = PAGED ? 0 : ck[1];
+  asm volatile("" ::"s"(ck0), "s"(ck1));  // keep the key-length loads ahead of the early exit
+  const int q_begin = cq0;
+  const int Lq = cu_q_p ? cq1 - cq0 : a.lq;
+  int Lk, k_begin = 0;
+  if constexpr (PAGED) {
+    Lk = min(ck0, a.max_blocks_per_seq * a.block_size);
+  } else {
+    k_begin = ck0;
+    Lk = cu_k_p ? ck1 - ck0 : a.lk;
+  }
+  const int qs = qblk * kPrefillBM;
+  if (qs >= Lq) return;
+  const int qe = min(qs + kPrefillBM, Lq);
+  const int pos_off = (a.causal == SP_CAUSAL_TOP_LEFT) ? 0 : Lk - Lq;
+  // keys any query of this workgroup can see: [kv_lo, kv_hi)
+  int kv_lo = 0, kv_hi = Lk;
+  if (a.causal != SP_CAUSAL_NONE) kv_hi = min(Lk, qe - 1 + pos_off + 1);
+  if (a.window_left >= 0) kv_lo = max(0, qs + pos_off - a.window_left);
+  // This workgroup's key tiles: all of [kv_lo, kv_hi), or its 1/nsplit share of them (masks and
+  // row clamps keep using the full range; only the walk stops at kv_end).
+  int t_first = (kv_lo / BN) * BN, kv_end = kv_hi;
+  if (a.nsplit > 1) {
+    const int ntiles = kv_hi > t_first ? (kv_hi - t_first + BN - 1) / BN : 0;
+    const int tps = (ntiles + a.nsplit - 1) / a.nsplit;
+    t_first += split * tps * BN;
+    kv_end = min(kv_hi, t_first + tps * BN);
+  }
+
+  const int l32 = lane & 31, hh = lane >> 5;        // MFMA column (query) and half
+  const int i16 = lane & 15, g4 = lane >> 4;        // 16-lane group for the transpose reads
+
+  // ---- per-sequence base addresses
+  const char* qbase = (const char*)a.q +
+      ((a.cu_q ? (int64_t)q_begin * a.q_tok : (int64_t)seq * a.q_batch) + (int64_t)h * a.q_head) * 2;
+  char* obase = (char*)a.out +
+      ((a.cu_q ? (int64_t)q_begin * a.o_tok : (int64_t)seq * a.o_batch) + (int64_t)h * a.o_head) *
+          dtype_size((sp_dtype)a.out_dtype);
+  const char* kbase = nullptr;
+  const char* vbase = nullptr;
+  const int32_t* table = nullptr;
+  int64_t head_off = 0;
+  if constexpr (PAGED) {
+    table = a.block_tables + (int64_t)seq * a.max_blocks_per_seq;
+    head_off = a.layer_off_b + (int64_t)kvh * a.block_size * RB;
+  } else {
+    const int64_t kv0 = (a.cu_k ? (int64_t)k_begin * a.kv_tok : (int64_t)seq * a.kv_batch) +
+                        (int64_t)kvh * a.kv_head;
+    kbase = (const char*)a.k + kv0 * 2;
+    vbase = (const char*)a.v + kv0 * 2;
+  }
+
+  // ---- Q^T operand (B of the S^T MFMA): query wq0 + l32, dims 16c + 8hh .. +7, unscaled.
+  const int wq0 = qs + 32 * wave;
+  const int my_q = wq0 + l32;
+  const float c2 = a.scale_log2;  // > 0 (checked on the host)
+  uint4 qreg[KC];
+  {
+    const char* qp = qbase + (int64_t)min(my_q, qe - 1) * a.q_tok * 2;
+#pragma unroll
+    for (int c = 0; c < KC; ++c)
+      qreg[c] = my_q < qe ? *(const uint4*)(qp + (16 * c + 8 * hh) * 2) : make_uint4(0, 0, 0, 0);
+  }
+
+  // ---- HBM -> LDS tile loads. Waves 0-1 fill K tiles and waves 2-3 V tiles, one tile ahead of
+  // the step that reads them. Wave w's load u moves 1 KiB = RPI rows, r_u = (w & 1) * WROWS + u * RPI ..;
+  // lane `lane` takes physical chunk p = lane % CPR of row r_u + lane / CPR and fetches the
+  // logical chunk that the swizzle puts there. Interior tiles (every row inside [kv_lo, kv_hi))
+  // take the fast path: one scalar base per tile (non-paged) or per block (paged) plus a constant
+  // lane offset per load. Edge tiles clamp rows outside [kv_lo, kv_hi) to a valid row (their
+  // scores are masked) and compute per-lane addresses.
+  const bool v_wave = wave >= 2;
+  const int wrow0 = (wave & 1) * WROWS;
+  const int64_t row_pitch = PAGED ? (int64_t)RB : (int64_t)a.kv_tok * 2;
+  const char* src_base = PAGED ? (v_wave ? a.vpool : a.kpool) : (v_wave ? vbase : kbase);
+  // paged fast path: a wave's WROWS rows of a tile lie in whole blocks (block_size divides the
+  // 32-row tile, and a load never straddles blocks)
+  const bool paged_fast = PAGED && a.block_size % RPI == 0 && BN % a.block_size == 0;
+  int voff[NLD];  // lane part of each load's source offset (bytes), row offset included
+#pragma unroll
+  for (int u = 0; u < NLD; ++u) {
+    const int r = wrow0 + u * RPI + lane / CPR;  // tile row
+    const int64_t row_b = PAGED ? (int64_t)(r % max(a.block_size, 1)) * RB : (int64_t)r * row_pitch;
+    voff[u] = (int)row_b + 16 * ((lane % CPR) ^ C::swz(r));
+  }
+  static_assert(NLD % 4 == 0, "tile loads go out in groups of four");
+  // Interior tiles issue their loads in groups of four with instruction offsets 0, 1, 2, 3 KiB.
+  // Contiguous K/V: the offsets come out of the lane offsets (still >= 0: load u's rows start at
+  // u RPI rows of at least RB bytes, u RPI RB = 1024 u). Paged with blocks that hold whole groups
+  // (block_size a multiple of 4 RPI rows, so a group's rows lie in one block): the same, with one
+  // base per group. Smaller blocks: out of the per-load bases.
+  const bool group_blk = wave_uniform(PAGED && a.block_size % (4 * RPI) == 0);
+  int voff_g[NLD];
+#pragma unroll
+  for (int u = 0; u < NLD; ++u)
+    voff_g[u] = (!PAGED || group_blk) ? voff[u] - (u & 3) * 1024 : voff[u];
+  auto tile_interior = [&](int t0) __attribute__((always_inline)) {
+    return t0 >= kv_lo && t0 + BN <= kv_hi;
+  };
+  // Paged fast path: the block ids of the rows of the next tile this wave loads, fetched one
+  // tile ahead so that no load waits on a dependent block-table read. Lane u < NLD fetches load
+  // u's id with a vector load: it completes with the tile loads at the next step's wait, where a
+  // scalar load would sit in lgkmcnt ahead of the LDS operand reads of the QK product and make
+  // each of their waits a wait for the table read.
+  // block_size divides the 32-key tile here, so it is a power of two and every tile start t0 is
+  // a multiple of it: the id of the block holding row t0 + r is table[(t0 >> shift) + (r >> shift)].
+  int nblk = 0;
+  const int bs_shift = paged_fast ? wave_uniform(31 - __builtin_clz(max(a.block_size, 1))) : 0;
+  const int lane_blk = (wrow0 + min(lane, NLD - 1) * RPI) >> bs_shift;
+  auto fetch_blocks = [&](int t0) __attribute__((always_inline)) {
+    if constexpr (PAGED) {
+      if (paged_fast && t0 < kv_end && tile_interior(t0)) nblk = table[(t0 >> bs_shift) + lane_blk];
+    }
+  };
+  // Interior tile: its loads go out in groups of four that share one M0 write.
+  auto issue_interior = [&](int t0, char* buf) __attribute__((always_inline)) {
+    char* dst = buf + wrow0 * RB;
+    if constexpr (PAGED) {
+      // block ids fetched by fetch_blocks(t0), load u's in lane u: every lane turns its id into
+      // its load's base address at once (vector ops), and each load reads its base out of lane u
+      // (two readlanes), instead of a scalar chain of compares and 64-bit multiplies per load.
+      // The base is taken less the load's instruction offset; the sum is the block's row address.
+      const int bl = (nblk >= 0 && nblk < a.num_blocks) ? nblk : 0;  // never outside the pool
+      const uint64_t vb = (uint64_t)(uintptr_t)(src_base + head_off) +
+                          (uint64_t)bl * (uint64_t)a.block_stride_b - (uint64_t)((lane & 3) * 1024);
+      const int vb_lo = (int)(uint32_t)vb, vb_hi = (int)(uint32_t)(vb >> 32);
+      auto base_of = [&](int u) __attribute__((always_inline)) {
+        const uint64_t lo = (uint32_t)__builtin_amdgcn_readlane(vb_lo, u);
+        const uint64_t hi = (uint32_t)__builtin_amdgcn_readlane(vb_hi, u);
+        return (const char*)(uintptr_t)((hi << 32) | lo);
+      };
+      if (group_blk) {  // lane g (g % 4 == 0) holds its group's block; no offset taken off
+#pragma unroll
+        for (int g = 0; g < NLD; g += 4) {
+          const char* b = base_of(g);
+          lds_dma16x4(b, b, b, b, voff_g[g], voff_g[g + 1], voff_g[g + 2], voff_g[g + 3],
+                      dst + g * 1024);
+        }
+      } else {
+#pragma unroll
+        for (int g = 0; g < NLD; g += 4)
+          lds_dma16x4(base_of(g), base_of(g + 1), base_of(g + 2), base_of(g + 3), voff_g[g],
+                      voff_g[g + 1], voff_g[g + 2], voff_g[g + 3], dst + g * 1024);
+      }
+    } else {
+      const char* sb = src_base + (int64_t)t0 * row_pitch;
+#pragma unroll
+      for (int g = 0; g < NLD; g += 4)
+        lds_dma16x4(sb, sb, sb, sb, voff_g[g], voff_g[g + 1], voff_g[g + 2], voff_g[g + 3],
+                    dst + g * 1024);
+    }
+  };
+  auto issue_tile = [&](int t0, char* buf) __attribute__((always_inline)) {
+    char* dst = buf + wrow0 * RB;
+    if (tile_interior(t0) && (!PAGED || paged_fast)) {
+      issue_interior(t0, buf);
+      return;
+    }
+    // Edge tiles are rare: the lane id goes through an empty asm so that the per-lane source
+    // addresses are derived here, not hoisted out of the key loop as live registers.
+    int ln = lane;
+    asm volatile("" : "+v"(ln));
+#pragma unroll
+    for (int u = 0; u < NLD; ++u) {
+      const int R = wrow0 + u * RPI + ln / CPR, p = ln % CPR;
+      const int c = p ^ C::swz(R);
+      const int j = min(max(t0 + R, kv_lo), kv_hi - 1);
+      const char* src;
+      if constexpr (PAGED) {
+        int blk = table[j / a.block_size];
+        blk = (blk >= 0 && blk < a.num_blocks) ? blk : 0;  // never dereference outside the pool
+        src = src_base + (int64_t)blk * a.block_stride_b + head_off +
+              (int64_t)(j % a.block_size) * RB + c * 16;
+      } else {
+        src = src_base + (int64_t)j * row_pitch + c * 16;
+      }
+      lds_dma16(src, dst + u * 1024);
+    }
+  };
+
+  // Online softmax state of query l32 (both lanes of a query hold the same values).
+  // m_run: running maximum of the exponents x = q.k * scale * log2(e) seen (-inf before the
+  // first visible key); m_used: the offset subtracted from x (m_run once that is finite, else 0).
+  float m_run = -INFINITY, m_used = 0.f, l_run = 0.f;
+  pf_f32x16 acc[DB];
+#pragma unroll
+  for (int db = 0; db < DB; ++db)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[db][r] = 0.f;
+  pf_f32x16 zero16;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) zero16[r] = 0.f;
+
+  const int wq_lo = wq0, wq_hi = min(wq0 + 32, qe) - 1;  // this wave's queries (inclusive)
+  const bool wave_active = wq_lo < qe;
+  const int qpos = my_q + pos_off;
+  const int sw = C::swz(l32);     // swizzle of the K rows this lane reads (row & 15 == l32 & 15)
+  // A tile needs masking iff t0 < mask_below or t0 > mask_above (wave-uniform bounds): it starts
+  // before kv_lo or before the window edge of this wave's last query, or it runs past the
+  // sequence end or past the causal diagonal of this wave's first query.
+  int mask_below = kv_lo, mask_above = Lk - BN;
+  if (a.causal != SP_CAUSAL_NONE) mask_above = min(mask_above, wq_lo + pos_off - BN + 1);
+  if (a.window_left >= 0) mask_below = max(mask_below, wq_hi + pos_off - a.window_left);
+  mask_below = wave_uniform(mask_below);
+  mask_above = wave_uniform(mask_above);
+
+  // Lane parts of the LDS operand addresses (byte offsets inside a tile). With the XOR swizzle
+  // an operand's logical chunk index only flips bits the lane part owns alone, so every operand
+  // of a tile sits at (lane part ^ constant) + immediate offset.
+  const int k_lane = (l32 * RB) | (16 * (hh ^ sw));
+  const int rl = (g4 >> 1) * 4 + (i16 >> 2);
+  const int chl = (g4 & 1) * 2 + ((i16 & 3) >> 1);
+  const int v_lane0 = rl * RB + 16 * (chl ^ C::swz(rl)) + 8 * (i16 & 1);
+  const int v_lane1 = (rl + 8) * RB + 16 * (chl ^ C::swz(rl + 8)) + 8 * (i16 & 1);
+
+  // Causal diagonal at 32-key granularity (see the mask below).
+  const int diag0 = wave_uniform(wq_lo + pos_off);
+  const bool tri_ok = a.causal != SP_CAUSAL_NONE && pos_off >= 0 && (pos_off & 31) == 0 &&
+                      qe - 1 + pos_off < Lk;
+  const int tri_lim = l32 - 4 * hh;
+
+  // ---- the pieces of one key tile -------------------------------------------------------------
+  // QK product S^T = K Q^T of the tile in LDS buffer kb into s (one 32 x 32 block). K operand i
+  // (k-step i) is row l32, chunk 2i + hh: k_lane ^ 32i. `between(i)` runs after MFMA i.
+  constexpr int NK = KC, AHK = PAGED ? 1 : 2;  // paged: four VGPRs for the block bases
+  auto qk = [&](const char* kb, pf_f32x16& s, auto&& between) __attribute__((always_inline)) {
+    int kbl = k_lane;
+    asm volatile("" : "+v"(kbl));
+    auto read_k = [&](int i) __attribute__((always_inline)) {
+      return *(const uint4*)(kb + (kbl ^ (32 * i)));
+    };
+    uint4 kop[AHK];
+#pragma unroll
+    for (int i = 0; i < AHK; ++i) kop[i] = read_k(i);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < NK; ++i) {
+      const uint4 cur = kop[i % AHK];
+      if (i + AHK < NK) kop[i % AHK] = read_k(i + AHK);
+      s = M::mma(cur, qreg[i], i < 1 ? zero16 : s);
+      between(i);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+
+  // Masks, only on tiles that cross the sequence end, the window edge, kv_lo or the causal
+  // diagonal. Score r of this lane is key t0 + 4hh + off, off = 8(r/4) + r%4.
+  // this lane's row of the additive mask (dense path: the sequence index is the batch index)
+  const float* mrow = a.mask ? a.mask + (int64_t)seq * a.mask_b + (int64_t)h * a.mask_h +
+                                   (int64_t)min(my_q, qe - 1) * a.mask_q
+                             : nullptr;
+  auto apply_mask = [&](int t0, pf_f32x16& s) __attribute__((always_inline)) {
+    if (mrow) {
+      const int jb = t0 + 4 * hh;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int key = min(jb + 8 * (r >> 2) + (r & 3), Lk - 1);
+        s[r] += mrow[key] * a.inv_scale;
+      }
+    }
+    if (t0 < mask_below || t0 > mask_above) {
+      if (tri_ok && t0 >= mask_below && t0 == diag0) {
+        int tl = tri_lim;
+        asm volatile("" : "+v"(tl));
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s[r] = (8 * (r >> 2) + (r & 3) <= tl) ? s[r] : -INFINITY;
+      } else {
+        int lo = kv_lo, hi = Lk - 1;
+        if (a.causal != SP_CAUSAL_NONE) hi = min(hi, qpos);
+        if (a.window_left >= 0) lo = max(lo, qpos - a.window_left);
+        const int jb = t0 + 4 * hh;
+        const int olo = lo - jb, ohi = hi - jb;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int off = (r >> 2) * 8 + (r & 3);
+          s[r] = (off >= olo && off <= ohi) ? s[r] : -INFINITY;
+        }
+      }
+    }
+  };
+
+  // Softmax weights of one tile for query l32 (FlashAttention-2 online softmax, Dao 2023) with a
+  // lazily raised maximum: p = 2^(s * scale * log2 e - m_used), packed to 16 bits for the PV
+  // product; the row sum adds the 16-bit values the PV product uses (v_dot2 against ones).
+  // Slice e (of 8) computes the two scores 2e, 2e+1 of the lane.
+  uint4 pb[2];
+  float la = 0.f, lb = 0.f;
+  auto weights_slice = [&](const pf_f32x16& s, int e, float off) __attribute__((always_inline)) {
+    const int k0 = 2 * e;
+    const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[k0], c2, -off));
+    const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[k0 + 1], c2, -off));
+    const uint32_t w = M::pack(p0, p1);
+    const int ks = k0 >> 3, c = (k0 >> 1) & 3;  // pb[ks] word c holds scores 8ks + 2c, +1
+    if (c == 0) pb[ks].x = w;
+    else if (c == 1) pb[ks].y = w;
+    else if (c == 2) pb[ks].z = w;
+    else pb[ks].w = w;
+    if (ks < 1) la = M::sum2(w, la);
+    else lb = M::sum2(w, lb);
+  };
+  auto weights_all = [&](const pf_f32x16& s, float off) __attribute__((always_inline)) {
+    la = 0.f;
+    lb = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) weights_slice(s, e, off);
+  };
+  constexpr float kLazyBound = 4096.f;  // 2^kLazy, kLazy = 12
+  auto finish_weights = [&](const pf_f32x16& s) __attribute__((always_inline)) {
+    float lsum = la + lb;
+    if (__any(lsum > kLazyBound || m_run == -INFINITY)) {
+      float mq[2];
+#pragma unroll
+      for (int k = 0; k < 2; ++k) {
+        const int r0 = k * 8;
+        float x = max3f(s[r0], s[r0 + 1], s[r0 + 2]);
+        x = max3f(x, s[r0 + 3], s[r0 + 4]);
+        x = max3f(x, s[r0 + 5], s[r0 + 6]);
+        mq[k] = __builtin_fmaxf(x, s[r0 + 7]);
+      }
+      float mx = __builtin_fmaxf(mq[0], mq[1]);
+      float x0, x1;
+      swap_halves(mx, x0, x1);
+      const float m_new = __builtin_fmaxf(m_run, __builtin_fmaxf(x0, x1) * c2);
+      const float used_new = (m_new == -INFINITY) ? 0.f : m_new;
+      const float alpha = __builtin_amdgcn_exp2f(m_run - used_new);
+      weights_all(s, used_new);
+      lsum = la + lb;
+      m_run = m_new;
+      m_used = used_new;
+      l_run *= alpha;
+#pragma unroll
+      for (int db = 0; db < DB; ++db) acc[db] *= alpha;
+    }
+    l_run += lsum;
+  };
+
+  // PV product O^T += V^T P^T of the tile in LDS buffer vb: K-step ks covers tile tokens
+  // 16ks .. 16ks+15 in the S^T order. The V^T operand (ks, db) is rows 16ks + rl (+ 8), chunk
+  // 4db + chl: (v_lane0 ^ 64db) + 16ks RB (v_lane1 for the second row group), read AH ahead.
+  auto pv = [&](const char* vb) __attribute__((always_inline)) {
+    int vb0 = v_lane0, vb1 = v_lane1;
+    asm volatile("" : "+v"(vb0), "+v"(vb1));
+    auto read_v = [&](int ks, int db) __attribute__((always_inline)) {
+      const char* a0 = vb + 16 * ks * RB + (vb0 ^ (64 * db));
+      const char* a1 = vb + 16 * ks * RB + (vb1 ^ (64 * db));
+      const pf_s16x4 v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(a0));
+      const pf_s16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(a1));
+      return __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7);
+    };
+    constexpr int NV = 2 * DB, AH = PAGED ? 1 : 2;
+    pf_s16x8 vop[AH];
+#pragma unroll
+    for (int i = 0; i < AH; ++i) vop[i] = read_v(i / DB, i % DB);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const pf_s16x8 cur = vop[i % AH];
+      if (i + AH < NV) vop[i % AH] = read_v((i + AH) / DB, (i + AH) % DB);
+      acc[i % DB] = M::mma(cur, pb[i / DB], acc[i % DB]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+
+  // wave-uniform: does this wave see any key of the tile. The conditions (the wave has queries,
+  // the tile starts before kv_end, at or before the causal diagonal of the wave's last query, and
+  // ends at or after the window edge of its first query) bound t0 from both sides, so they
+  // reduce to one range [vis_lo, vis_hi) worked out once.
+  int vis_lo = -(1 << 30), vis_hi = wave_active ? kv_end : -(1 << 30);
+  if (a.causal != SP_CAUSAL_NONE) vis_hi = min(vis_hi, wq_hi + pos_off + 1);
+  if (a.window_left >= 0) vis_lo = wq_lo + pos_off - a.window_left - BN + 1;
+  vis_lo = wave_uniform(vis_lo);
+  vis_hi = wave_uniform(vis_hi);
+  auto visits = [&](int t0) __attribute__((always_inline)) { return t0 >= vis_lo && t0 < vis_hi; };
+
+  // One step on tile t0 (its K in kcur, its V in vcur): wait until this step's tiles are in (own
+  // loads, then everyone's; the barrier also guarantees every wave is done with the other
+  // buffers), start the next tile's loads into kload / vload, then QK product, softmax, PV.
+  pf_f32x16 sc;
+  auto step = [&](int t0, const char* kcur, const char* vcur, char* kload, char* vload)
+      __attribute__((always_inline)) {
+    __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+    __syncthreads();
+    {
+      const int lt = t0 + BN;
+      if (lt < kv_end) {
+        issue_tile(lt, v_wave ? vload : kload);
+        fetch_blocks(lt + BN);
+      }
+    }
+    if (visits(t0)) {
+      qk(kcur, sc, [](int) {});
+      apply_mask(t0, sc);
+      float off = m_used;
+      asm volatile("" : "+v"(off));
+      la = 0.f;
+      lb = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) weights_slice(sc, e, off);
+      finish_weights(sc);
+      pv(vcur);
+    }
+  };
+
+  int t0 = t_first;
+  if (t0 < kv_end) {
+    fetch_blocks(t0);
+    issue_tile(t0, v_wave ? vl[0] : kl[0]);
+    fetch_blocks(t0 + BN);
+  }
+  while (t0 < kv_end) {
+    step(t0, kl[0], vl[0], kl[1], vl[1]);
+    t0 += BN;
+    if (t0 >= kv_end) break;
+    step(t0, kl[1], vl[1], kl[0], vl[0]);
+    t0 += BN;
+  }
+
+  // ---- normalise and store: lane holds O^T[d][query l32], d = 32db + 8(r/4) + 4hh + r%4
+  float x0, x1;
+  swap_halves(l_run, x0, x1);
+  const float l = x0 + x1;
+  if (my_q >= qe) return;
+  if (a.nsplit > 1) {
+    // partial record (m, l, -, -, acc[D]) of this split; m is the offset the weights are
+    // relative to, -inf when the split saw no visible key (then l = 0 and acc = 0), so that the
+    // merge never takes an empty split's offset as the row maximum. Rows past max_q (a caller
+    // whose cu_seqlens exceed max_seqlen_q) have no record slot and are not written.
+    if (my_q >= a.max_q) return;
+    float* rec = a.partials +
+        ((((int64_t)seq * a.max_q + my_q) * a.hq + h) * a.nsplit + split) * (D + 4);
+    if (hh == 0) *(float2*)rec = make_float2(m_run == -INFINITY ? -INFINITY : m_used, l);
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int rg = 0; rg < 4; ++rg)
+        *(float4*)(rec + 4 + db * 32 + rg * 8 + hh * 4) =
+            make_float4(acc[db][rg * 4 + 0], acc[db][rg * 4 + 1], acc[db][rg * 4 + 2],
+                        acc[db][rg * 4 + 3]);
+    return;
+  }
+  const float inv = l > 0.f ? 1.f / l : 0.f;
+  constexpr int kSelf = std::is_same<T, bf16_t>::value ? SP_BF16 : SP_F16;  // out = in type
+  const int oes = dtype_size((sp_dtype)a.out_dtype);
+  char* op = obase + (int64_t)my_q * a.o_tok * oes;
+#pragma unroll
+  for (int db = 0; db < DB; ++db)
+#pragma unroll
+    for (int rg = 0; rg < 4; ++rg) {
+      const int d0 = db * 32 + rg * 8 + hh * 4;
+      const float o0 = acc[db][rg * 4 + 0] * inv, o1 = acc[db][rg * 4 + 1] * inv;
+      const float o2 = acc[db][rg * 4 + 2] * inv, o3 = acc[db][rg * 4 + 3] * inv;
+      if (a.out_dtype == SP_F32) {
+        *(float4*)(op + d0 * 4) = make_float4(o0, o1, o2, o3);
+      } else if (a.out_dtype == kSelf) {
+        *(uint2*)(op + d0 * 2) = make_uint2(M::pack(o0, o1), M::pack(o2, o3));
+      } else {  // the other 16-bit type
+        using O = PrefillMfma<typename std::conditional<kSelf == SP_BF16, f16_t, bf16_t>::type>;
+        *(uint2*)(op + d0 * 2) = make_uint2(O::pack(o0, o1), O::pack(o2, o3));
+      }
+    }
+}
+
 // Merge the split partials of one (sequence, head, group of kCombineRows query rows):
 // out = sum_s 2^(m_s - M) acc_s / sum_s 2^(m_s - M) l_s, M = max_s m_s (zeros when no split saw
 // a key). D/4 lanes per row, four output elements each, one row per lane group, so every row's
@@ -1163,11 +1669,25 @@ static int launch_td(const PrefillArgs& a, bool paged, hipStream_t stream) {
 }
 
 template <typename T>
+static int launch_wide(const PrefillArgs& a, bool paged, hipStream_t stream) {
+  if (a.nsplit > 1) return fail(SP_EUNSUPPORTED, "prefill: head_dim 256 takes no key split");
+  const int64_t blocks = (int64_t)a.num_qblocks * a.num_seqs * a.hq;
+  if (blocks <= 0) return SP_OK;
+  if (blocks > 0x7fffffff) return fail(SP_EINVAL, "prefill: grid of %lld workgroups", (long long)blocks);
+  if (paged)
+    hipLaunchKernelGGL((prefill_wide_kernel<T, 256, true>), dim3((unsigned)blocks), dim3(256), 0, stream, a);
+  else
+    hipLaunchKernelGGL((prefill_wide_kernel<T, 256, false>), dim3((unsigned)blocks), dim3(256), 0, stream, a);
+  return check_launch("prefill_wide_kernel");
+}
+
+template <typename T>
 static int launch_t(const PrefillArgs& a, int head_dim, bool paged, hipStream_t stream) {
   switch (head_dim) {
     case 64: return launch_td<T, 64>(a, paged, stream);
     case 128: return launch_td<T, 128>(a, paged, stream);
-    default: return fail(SP_EUNSUPPORTED, "prefill: head_dim %d has no kernel (64, 128)", head_dim);
+    case 256: return launch_wide<T>(a, paged, stream);
+    default: return fail(SP_EUNSUPPORTED, "prefill: head_dim %d has no kernel (64, 128, 256)", head_dim);
   }
 }
 
