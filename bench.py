@@ -27,6 +27,12 @@ line:
   configs    C4 (one mixed iteration through sp_ragged_paged_attention: the prefill half's
              fraction of the bf16 MFMA peak, the decode half's fraction of HBM, the call against
              the serial bound) and the C5 / C1 decode calls' fractions of HBM
+  gemma4_d256  head dim 256 (Gemma-4's sliding layers, 16 / 8 heads, 1024-key window): a paged
+             decode batch and a windowed varlen prefill, with their roofline fractions
+Decode legs whose working set is below 512 MB (C5's window, the PolarQuant pools, C1) rotate
+their timed calls over copies of the pools, so that more than 512 MB (twice the 256 MB MALL) of
+K/V is read between two reads of the same byte; each reports its working set, the rotation and
+the cache-warm time of the same call repeated on one copy beside it.
 Each leg runs its W warmup steps and then keeps warming until 0.3 s have passed before its
 timed region: a compute-bound kernel timed right after the GPU leaves idle runs at a lower
 clock (C4's mixed step measured 298 us after 5 warm calls and 253 us after 400).
@@ -175,17 +181,24 @@ def time_polar_decode(w, t, steps: int, warmup: int):
     ws = sp.alloc_decode_workspace(w.num_seqs, w.hq, max_ctx, w.window_left, lay)
     scale = w.head_dim ** -0.5
     stream = torch.cuda.current_stream()
+    db = w.polar_decode_bytes()
+    # copies of the compressed pools for the past-the-MALL timing (rotation_copies)
+    copies = rotation_copies(db)
+    pools = [(kp, vp)] + [(kp.clone(), vp.clone()) for _ in range(copies - 1)]
 
     def append():
         sp.polar_kv_append(kp, vp, lay, t["k_new"], t["v_new"], t["slot_mapping"],
                            stream=stream.cuda_stream)
 
-    def decode():
-        sp.polar_paged_decode(t["out"], t["q"], kp, vp, lay, t["block_tables"], t["context_lens"],
-                              max_ctx, scale, window_left=w.window_left, workspace=ws,
-                              stream=stream.cuda_stream)
+    def decode_on(kx, vx):
+        return lambda: sp.polar_paged_decode(t["out"], t["q"], kx, vx, lay, t["block_tables"],
+                                             t["context_lens"], max_ctx, scale,
+                                             window_left=w.window_left, workspace=ws,
+                                             stream=stream.cuda_stream)
 
-    _warm(lambda: (append(), decode()), warmup)
+    decode = decode_on(kp, vp)
+    calls = [decode_on(kx, vx) for kx, vx in pools]
+    _warm(lambda: (append(), [c() for c in calls]), warmup)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(steps):
@@ -193,16 +206,22 @@ def time_polar_decode(w, t, steps: int, warmup: int):
         decode()
     torch.cuda.synchronize()
     step_s = (time.perf_counter() - t0) / steps
-    dec_ms, dec_min = _event_times(stream, decode, steps)
+    reps = max(steps, 4 * copies)
+    dec_ms = _rotated_event_ms(stream, calls, reps)
+    warm_ms = _rotated_event_ms(stream, calls[:1], reps)
     app_ms, _ = _event_times(stream, append, steps)
-    db = w.polar_decode_bytes()
     return {
         "ms_per_step": round(step_s * 1e3, 4),
         "decode_ms": round(dec_ms, 5),
-        "decode_ms_min": round(dec_min, 5),
         "decode_bytes": db,
         "decode_GBs": round(db / (dec_ms * 1e-3) / 1e9, 2),
         "frac_hbm": round(db / (dec_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "working_set_bytes": db,
+        "rotation": {"pool_copies": copies, "bytes_between_reuse": db * max(copies - 1, 1),
+                     "protocol": "consecutive calls of the timed region read different copies of "
+                                 "the compressed pools (more than 512 MB between two reads of "
+                                 "the same byte)"},
+        "decode_ms_cache_warm": round(warm_ms, 5),
         "append_ms": round(app_ms, 5),
         "append_bytes": w.polar_append_bytes(),
         "kernel": "polar_decode_kernel + decode_combine_kernel (one sp_polar_paged_decode call)",
@@ -312,6 +331,68 @@ def _event_times(stream, fn, reps: int):
     return float(avg), float(np.min([x.elapsed_time(y) for x, y in ev]))
 
 
+MALL_CLEAR_BYTES = 512 << 20  # twice the 256 MB MALL
+
+
+def rotation_copies(working_set: int) -> int:
+    """Pool copies a timed region rotates over so that, between two reads of the same byte, more
+    than 512 MB (twice the 256 MB MALL) of other K/V is read: one copy when a call's own working
+    set is that large, else enough for the calls in between."""
+    if working_set >= MALL_CLEAR_BYTES:
+        return 1
+    return 1 + -(-MALL_CLEAR_BYTES // working_set)
+
+
+def _rotated_event_ms(stream, calls, reps: int):
+    """ms per call of a HIP-event region of `reps` back-to-back calls, call i being
+    calls[i % len(calls)] (each on its own copy of the pools)."""
+    import torch
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record(stream)
+    for i in range(reps):
+        calls[i % len(calls)]()
+    b.record(stream)
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / reps
+
+
+def time_decode_rotated(w, steps: int, warmup: int):
+    """A decode config's sp_paged_decode call timed past the MALL: the region rotates over
+    rotation_copies(working set) copies of the K/V pools (same tables and contexts), so no call
+    reads K/V a recent call left in the 256 MB MALL. Also reports the same call repeated on one
+    copy (cache-warm) beside it."""
+    import torch
+    import sketchpad_amd as sp
+    from sketchpad_amd import workloads as W
+
+    t = W.make_decode_tensors(w)
+    lay = w.layout()
+    ws_bytes = w.decode_bytes()
+    copies = rotation_copies(ws_bytes)
+    pools = [(t["k_pool"], t["v_pool"])] + [(t["k_pool"].clone(), t["v_pool"].clone())
+                                             for _ in range(copies - 1)]
+    max_ctx = w.max_context_len
+    ws = sp.alloc_decode_workspace(w.num_seqs, w.hq, max_ctx, w.window_left, lay)
+    scale = w.head_dim ** -0.5
+    stream = torch.cuda.current_stream()
+
+    def call(kp, vp):
+        return lambda: sp.paged_decode(t["out"], t["q"], kp, vp, lay, t["block_tables"],
+                                       t["context_lens"], max_ctx, scale,
+                                       window_left=w.window_left, workspace=ws,
+                                       stream=stream.cuda_stream)
+
+    calls = [call(kp, vp) for kp, vp in pools]
+    _warm(lambda: [c() for c in calls], warmup)
+    torch.cuda.synchronize()
+    reps = max(steps, 4 * copies)
+    ms = _rotated_event_ms(stream, calls, reps)
+    warm_ms = _rotated_event_ms(stream, calls[:1], reps)
+    return {"decode_ms": ms, "decode_ms_cache_warm": warm_ms, "decode_bytes": ws_bytes,
+            "working_set_bytes": ws_bytes, "rotation_copies": copies,
+            "bytes_between_reuse": ws_bytes * max(copies - 1, 1)}
+
+
 def time_prefill_c3(steps: int, warmup: int):
     """C3: append every token's K/V into the paged pool, then ragged causal prefill over the
     packed stream (sp_varlen_prefill). Returns per-launch times of both."""
@@ -376,7 +457,7 @@ def time_prefill_c3(steps: int, warmup: int):
             "peak": MFMA_BF16_PEAK_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
-            "kernel": "prefill_kernel<bf16,128,false> (one sp_varlen_prefill call)",
+            "kernel": "prefill_k32_kernel<bf16,128> (one sp_varlen_prefill call)",
             "algorithmic_flops": flops,
         },
         "append": {"ms": round(ap_ms, 5), "bytes": append_bytes,
@@ -384,6 +465,37 @@ def time_prefill_c3(steps: int, warmup: int):
         "rope_append": {"ms": round(ra_ms, 5), "bytes": rope_bytes,
                         "GBs": round(rope_bytes / (ra_ms * 1e-3) / 1e9, 2)},
     }
+
+
+def time_gemma4_d256(steps: int):
+    """Head dim 256 (Gemma-4's sliding-window layers, 16 query / 8 KV heads, a 1024-key window):
+    the paged decode of decode_gemma4_d256 timed past the MALL, and the windowed causal varlen
+    prefill of prefill_gemma4_d256 (TFLOP/s over the visible pairs)."""
+    import torch
+    import sketchpad_amd as sp
+    from sketchpad_amd import workloads as W
+
+    dec = time_decode_leg("gemma4-d256", steps, W.decode_gemma4_d256())
+    w = W.prefill_gemma4_d256()
+    t = W.make_prefill_tensors(w, with_pool=False)
+    stream = torch.cuda.current_stream()
+
+    def prefill():
+        sp.varlen_prefill(t["out"], t["q"], t["k"], t["v"], t["cu_seqlens"], t["cu_seqlens"],
+                          w.max_seqlen, w.head_dim ** -0.5, window_left=w.window_left,
+                          stream=stream.cuda_stream)
+
+    _warm(prefill, 3)
+    torch.cuda.synchronize()
+    ms, _ = _event_times(stream, prefill, max(10, steps))
+    tflops = w.flops() / (ms * 1e-3) / 1e12
+    return {"decode": dec,
+            "prefill": {"workload": f"{w.name}: B={w.num_seqs}, lens={[int(x) for x in w.lens]}, "
+                                    f"Hq={w.hq}, Hkv={w.hkv}, D={w.head_dim}, causal, "
+                                    f"window_left {w.window_left}",
+                        "ms": round(ms, 5), "flops": w.flops(), "tflops": round(tflops, 2),
+                        "frac_mfma": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
+                        "kernel": "prefill_wide_kernel<bf16,256,false>"}}
 
 
 def time_layer(steps: int, warmup: int, hidden: int = 4096):
@@ -663,18 +775,25 @@ def time_mixed_c4(steps: int, warmup: int):
     }
 
 
-def time_decode_leg(name: str, steps: int):
-    """A decode config's sp_paged_decode call: ms, GB/s over its algorithmic bytes, fraction of
-    HBM."""
+def time_decode_leg(name: str, steps: int, w=None):
+    """A decode config's sp_paged_decode call timed past the MALL (time_decode_rotated): ms,
+    GB/s over its algorithmic bytes, fraction of HBM, the working set and the rotation used."""
     from sketchpad_amd import workloads as W
-    wx = W.DECODE_CONFIGS[name]()
-    rx = time_decode_config(wx, steps, 2)
-    gbs = rx["decode_bytes"] / (rx["decode_ms_avg"] * 1e-3) / 1e9
+    wx = W.DECODE_CONFIGS[name]() if w is None else w
+    rx = time_decode_rotated(wx, steps, 2)
+    gbs = rx["decode_bytes"] / (rx["decode_ms"] * 1e-3) / 1e9
     return {"workload": f"{wx.name}: B={wx.num_seqs}, Hq={wx.hq}, Hkv={wx.hkv}, D={wx.head_dim}, "
                         f"{wx.dtype}, window {wx.window_left}, "
                         f"L~U[{int(wx.context_lens.min())},{int(wx.context_lens.max())}]",
-            "decode_ms": round(rx["decode_ms_avg"], 5), "decode_bytes": rx["decode_bytes"],
-            "decode_GBs": round(gbs, 2), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
+            "decode_ms": round(rx["decode_ms"], 5), "decode_bytes": rx["decode_bytes"],
+            "decode_GBs": round(gbs, 2), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
+            "working_set_bytes": rx["working_set_bytes"],
+            "rotation": {"pool_copies": rx["rotation_copies"],
+                         "bytes_between_reuse": rx["bytes_between_reuse"],
+                         "protocol": "consecutive calls of the timed region read different copies "
+                                     "of the pools, so more than 512 MB (twice the MALL) of K/V "
+                                     "is read between two reads of the same byte"},
+            "decode_ms_cache_warm": round(rx["decode_ms_cache_warm"], 5)}
 
 
 def main():
@@ -786,6 +905,7 @@ def main():
             if name != args.config:
                 cfg[name] = time_decode_leg(name, max(10, args.steps // 2))
         line["configs"] = cfg
+        line["gemma4_d256"] = time_gemma4_d256(max(10, args.steps // 2))
     if args.secondary:
         sec = line.setdefault("secondary", {})
         sec["C4-chunked-prefill"] = time_chunked_c4(10, 2)

@@ -158,6 +158,19 @@ def decode_c5() -> DecodeWorkload:
                           tables, nblk, window_left=4096)
 
 
+def decode_gemma4_d256() -> DecodeWorkload:
+    """Gemma-4's sliding-window layers (head_dim_swa 256, 16 query / 8 KV heads, a window of
+    1024 keys: window_left 1023; gemma4.rs:94-102, :1086-1108) at C2's batch: 64 sequences with
+    contexts U[512, 4096], bf16, block size 16. Not one of the five benchmark configurations."""
+    seed = seed_for(6)
+    rng = np.random.default_rng(seed)
+    lens = rng.integers(512, 4096, size=64, endpoint=True).astype(np.int32)
+    nblk = int(((lens + 15) // 16).sum())
+    tables = _tables_from_pool(rng, lens, 16, nblk)
+    return DecodeWorkload("gemma4-d256-window-decode", seed, 64, 16, 8, 256, 16, "bf16", lens,
+                          tables, nblk, window_left=1023)
+
+
 DECODE_CONFIGS = {"C1": decode_c1, "C2": decode_c2, "C4": decode_c4, "C5": decode_c5}
 
 
@@ -226,6 +239,7 @@ class PrefillWorkload:
     head_dim: int
     dtype: str
     block_size: int = 16
+    window_left: int = -1     # -1: causal only; W keys [p - W + 1, p] (gemma-4) -> W - 1
 
     @property
     def num_seqs(self) -> int:
@@ -244,9 +258,16 @@ class PrefillWorkload:
         return int(self.lens.max())
 
     def flops(self) -> int:
-        """4 * Hq * D per visible (query, key) pair; causal: L(L+1)/2 pairs per sequence."""
+        """4 * Hq * D per visible (query, key) pair; causal: L(L+1)/2 pairs per sequence, and
+        query i sees min(i + 1, window_left + 1) keys under a window."""
         L = self.lens.astype(np.int64)
-        return int(4 * self.hq * self.head_dim * (L * (L + 1) // 2).sum())
+        if self.window_left < 0:
+            pairs = (L * (L + 1) // 2).sum()
+        else:
+            w = self.window_left + 1
+            full = np.minimum(L, w)  # queries 0 .. full-1 see i + 1 keys, the rest w keys
+            pairs = (full * (full + 1) // 2 + (L - full) * w).sum()
+        return int(4 * self.hq * self.head_dim * pairs)
 
     def pool_tables(self):
         rng = np.random.default_rng(self.seed + 1)
@@ -267,6 +288,16 @@ def prefill_c3() -> PrefillWorkload:
     rng = np.random.default_rng(seed)
     lens = rng.integers(256, 2048, size=8, endpoint=True).astype(np.int32)
     return PrefillWorkload("C3-llama3-8b-ragged-prefill", seed, lens, 32, 8, 128, "bf16")
+
+
+def prefill_gemma4_d256() -> PrefillWorkload:
+    """Gemma-4 sliding-layer prefill: C3's lengths drawn again (8 sequences U[256, 2048]) at
+    head_dim 256, 16 query / 8 KV heads, causal within a 1024-key window, bf16."""
+    seed = seed_for(7)
+    rng = np.random.default_rng(seed)
+    lens = rng.integers(256, 2048, size=8, endpoint=True).astype(np.int32)
+    return PrefillWorkload("gemma4-d256-window-prefill", seed, lens, 16, 8, 256, "bf16",
+                           window_left=1023)
 
 
 def make_prefill_tensors(w: PrefillWorkload, device="cuda", with_pool: bool = True) -> dict:
