@@ -84,6 +84,11 @@ def parse_args():
                     help="skip the PolarQuant compressed-cache decode leg")
     ap.add_argument("--polar-only", action="store_true",
                     help="only the decode config's PolarQuant leg (profiling)")
+    ap.add_argument("--decode-leg", choices=["C1", "C4", "C5"],
+                    help="only that config's decode leg, timed as in the default line (pool "
+                         "copies rotated past the MALL), for profiling; prints its JSON object")
+    ap.add_argument("--gemma-only", action="store_true",
+                    help="only the head-dim-256 Gemma-4 decode and prefill legs (profiling)")
     ap.add_argument("--layer", action="store_true",
                     help="also time a whole attention layer (projections + RoPE append + "
                          "attention) on the C2 decode step and the C3 prefill")
@@ -841,6 +846,13 @@ def main():
     if args.prefill_only:
         _, pf = time_prefill_c3(args.steps, args.warmup)
         print(json.dumps({"prefill": pf}), flush=True)
+        return
+    if args.decode_leg:
+        print(json.dumps({args.decode_leg: time_decode_leg(args.decode_leg, args.steps)}),
+              flush=True)
+        return
+    if args.gemma_only:
+        print(json.dumps({"gemma4_d256": time_gemma4_d256(args.steps)}), flush=True)
         return
     w = W.DECODE_CONFIGS[args.config]()
     if args.polar_only:
