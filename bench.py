@@ -361,11 +361,11 @@ def _rotated_event_ms(stream, calls, reps: int):
     return a.elapsed_time(b) / reps
 
 
-def time_decode_rotated(w, steps: int, warmup: int):
+def time_decode_rotated(w, steps: int, warmup: int, softcap: float = 0.0):
     """A decode config's sp_paged_decode call timed past the MALL: the region rotates over
     rotation_copies(working set) copies of the K/V pools (same tables and contexts), so no call
     reads K/V a recent call left in the 256 MB MALL. Also reports the same call repeated on one
-    copy (cache-warm) beside it."""
+    copy (cache-warm) beside it. softcap > 0: sp_paged_decode_softcap."""
     import torch
     import sketchpad_amd as sp
     from sketchpad_amd import workloads as W
@@ -385,7 +385,7 @@ def time_decode_rotated(w, steps: int, warmup: int):
         return lambda: sp.paged_decode(t["out"], t["q"], kp, vp, lay, t["block_tables"],
                                        t["context_lens"], max_ctx, scale,
                                        window_left=w.window_left, workspace=ws,
-                                       stream=stream.cuda_stream)
+                                       softcap=softcap, stream=stream.cuda_stream)
 
     calls = [call(kp, vp) for kp, vp in pools]
     _warm(lambda: [c() for c in calls], warmup)
@@ -472,35 +472,46 @@ def time_prefill_c3(steps: int, warmup: int):
     }
 
 
+GEMMA4_LOGIT_SOFTCAP = 50.0  # attn_logit_softcap (crates/sketchpad-llm/src/gemma4.rs:96)
+
+
 def time_gemma4_d256(steps: int):
     """Head dim 256 (Gemma-4's sliding-window layers, 16 query / 8 KV heads, a 1024-key window):
     the paged decode of decode_gemma4_d256 timed past the MALL, and the windowed causal varlen
-    prefill of prefill_gemma4_d256 (TFLOP/s over the visible pairs)."""
+    prefill of prefill_gemma4_d256 (TFLOP/s over the visible pairs), each as Gemma-4 runs it
+    (logit soft cap 50, the *_softcap entry points) and without the cap."""
     import torch
     import sketchpad_amd as sp
     from sketchpad_amd import workloads as W
 
+    cap = GEMMA4_LOGIT_SOFTCAP
     dec = time_decode_leg("gemma4-d256", steps, W.decode_gemma4_d256())
+    dec_cap = time_decode_leg("gemma4-d256", steps, W.decode_gemma4_d256(), softcap=cap)
     w = W.prefill_gemma4_d256()
     t = W.make_prefill_tensors(w, with_pool=False)
     stream = torch.cuda.current_stream()
 
-    def prefill():
-        sp.varlen_prefill(t["out"], t["q"], t["k"], t["v"], t["cu_seqlens"], t["cu_seqlens"],
-                          w.max_seqlen, w.head_dim ** -0.5, window_left=w.window_left,
-                          stream=stream.cuda_stream)
+    def prefill(softcap):
+        return lambda: sp.varlen_prefill(t["out"], t["q"], t["k"], t["v"], t["cu_seqlens"],
+                                         t["cu_seqlens"], w.max_seqlen, w.head_dim ** -0.5,
+                                         window_left=w.window_left, softcap=softcap,
+                                         stream=stream.cuda_stream)
 
-    _warm(prefill, 3)
-    torch.cuda.synchronize()
-    ms, _ = _event_times(stream, prefill, max(10, steps))
-    tflops = w.flops() / (ms * 1e-3) / 1e12
-    return {"decode": dec,
-            "prefill": {"workload": f"{w.name}: B={w.num_seqs}, lens={[int(x) for x in w.lens]}, "
-                                    f"Hq={w.hq}, Hkv={w.hkv}, D={w.head_dim}, causal, "
-                                    f"window_left {w.window_left}",
-                        "ms": round(ms, 5), "flops": w.flops(), "tflops": round(tflops, 2),
-                        "frac_mfma": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
-                        "kernel": "prefill_wide_kernel<bf16,256,false>"}}
+    res = {}
+    for key, c in (("prefill", 0.0), ("prefill_softcap", cap)):
+        fn = prefill(c)
+        _warm(fn, 3)
+        torch.cuda.synchronize()
+        ms, _ = _event_times(stream, fn, max(10, steps))
+        tflops = w.flops() / (ms * 1e-3) / 1e12
+        res[key] = {"workload": f"{w.name}: B={w.num_seqs}, lens={[int(x) for x in w.lens]}, "
+                                f"Hq={w.hq}, Hkv={w.hkv}, D={w.head_dim}, causal, "
+                                f"window_left {w.window_left}, logit softcap {c:g}",
+                    "ms": round(ms, 5), "flops": w.flops(), "tflops": round(tflops, 2),
+                    "frac_mfma": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
+                    "kernel": f"prefill_wide_kernel<bf16,256,false{',true' if c else ''}>"}
+    dec_cap["logit_softcap"] = cap
+    return {"decode": dec, "decode_softcap": dec_cap, **res}
 
 
 def time_layer(steps: int, warmup: int, hidden: int = 4096):
@@ -780,12 +791,12 @@ def time_mixed_c4(steps: int, warmup: int):
     }
 
 
-def time_decode_leg(name: str, steps: int, w=None):
+def time_decode_leg(name: str, steps: int, w=None, softcap: float = 0.0):
     """A decode config's sp_paged_decode call timed past the MALL (time_decode_rotated): ms,
     GB/s over its algorithmic bytes, fraction of HBM, the working set and the rotation used."""
     from sketchpad_amd import workloads as W
     wx = W.DECODE_CONFIGS[name]() if w is None else w
-    rx = time_decode_rotated(wx, steps, 2)
+    rx = time_decode_rotated(wx, steps, 2, softcap)
     gbs = rx["decode_bytes"] / (rx["decode_ms"] * 1e-3) / 1e9
     return {"workload": f"{wx.name}: B={wx.num_seqs}, Hq={wx.hq}, Hkv={wx.hkv}, D={wx.head_dim}, "
                         f"{wx.dtype}, window {wx.window_left}, "

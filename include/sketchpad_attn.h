@@ -180,8 +180,9 @@ size_t sp_paged_decode_workspace_size(int32_t num_seqs, int32_t num_q_heads,
  *   workspace      : device scratch of at least sp_paged_decode_workspace_size() bytes (no
  *                    initialisation needed). Calls that share a workspace must not overlap.
  * Softmax and accumulation are fp32 for every dtype. GQA groups (Hq / Hkv) up to 16, head_dim
- * 64 or 128, block_size a multiple of 16 or one of 1, 2, 4, 8 (a 16-token tile then spans
- * several blocks, each row read from the block its position maps to).
+ * 64 or 128 (and 256 for bf16 / f16: Gemma-4's sliding layers, gemma4.rs:94-102), block_size a
+ * multiple of 16 or one of 1, 2, 4, 8 (a 16-token tile then spans several blocks, each row read
+ * from the block its position maps to).
  */
 int sp_paged_decode(void* out, const void* q,
                     const void* k_pool, const void* v_pool, const sp_cache_layout* layout,
@@ -190,6 +191,23 @@ int sp_paged_decode(void* out, const void* q,
                     int32_t num_seqs, int32_t num_q_heads,
                     float scale, int32_t window_left, sp_dtype dtype,
                     void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * The logit soft cap of Gemma-4's attention (Gemma4Attention::forward, gemma4.rs:366-377, with
+ * attn_logit_softcap = 50, :96): every logit becomes logit_softcap * tanh(logit / logit_softcap),
+ * logit = (q . k) * scale, before the mask and the softmax. Each *_softcap entry point below is
+ * its namesake with that one argument added after `scale`; logit_softcap == 0 is the namesake
+ * itself, > 0 runs at head_dim 256 on bf16 / f16 tensors (the sliding-window layers the cap and
+ * the W-key window of gemma4.rs:1086-1108 come with; window_left = W - 1) and returns
+ * SP_EUNSUPPORTED elsewhere; a negative or non-finite cap is SP_EINVAL.
+ */
+int sp_paged_decode_softcap(void* out, const void* q,
+                            const void* k_pool, const void* v_pool, const sp_cache_layout* layout,
+                            const int32_t* block_tables, int32_t max_blocks_per_seq,
+                            const int32_t* context_lens, int32_t max_context_len,
+                            int32_t num_seqs, int32_t num_q_heads,
+                            float scale, float logit_softcap, int32_t window_left, sp_dtype dtype,
+                            void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * One decode step's append and attention in a single call: sp_kv_append of each sequence's new
@@ -215,6 +233,16 @@ int sp_paged_append_decode(void* out, const void* q, void* k_pool, void* v_pool,
                            int32_t num_seqs, int32_t num_q_heads,
                            float scale, int32_t window_left, sp_dtype dtype,
                            void* workspace, size_t workspace_bytes, void* stream);
+/* sp_paged_append_decode with Gemma-4's logit soft cap (see sp_paged_decode_softcap). */
+int sp_paged_append_decode_softcap(void* out, const void* q, void* k_pool, void* v_pool,
+                                   const sp_cache_layout* layout, const void* k_new,
+                                   const void* v_new, int64_t token_stride, int64_t head_stride,
+                                   const int32_t* block_tables, int32_t max_blocks_per_seq,
+                                   const int32_t* context_lens, int32_t max_context_len,
+                                   int32_t num_seqs, int32_t num_q_heads,
+                                   float scale, float logit_softcap, int32_t window_left,
+                                   sp_dtype dtype, void* workspace, size_t workspace_bytes,
+                                   void* stream);
 
 /*
  * sp_paged_decode without a workspace argument: the split partials go to a scratch array the
@@ -248,7 +276,7 @@ int sp_paged_decode_noalloc(void* out, const void* q,
  *   causal : sp_causal; window_left >= 0 adds the sliding window (see above).
  * Softmax and accumulation are fp32; a query that sees no key gets zeros. f32 (fp32 MFMA, fp32
  * weights: the reference flash_attention's element type), bf16 and f16 (16-bit weights on the
- * bf16/f16 MFMA), head_dim 64 or 128, GQA groups of any size.
+ * bf16/f16 MFMA), head_dim 64 or 128 (and 256 for bf16 / f16), GQA groups of any size.
  */
 int sp_varlen_prefill(void* out, const void* q, const void* k, const void* v,
                       const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
@@ -256,6 +284,13 @@ int sp_varlen_prefill(void* out, const void* q, const void* k, const void* v,
                       int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
                       float scale, int32_t causal, int32_t window_left,
                       sp_dtype dtype, void* stream);
+/* sp_varlen_prefill with Gemma-4's logit soft cap (see sp_paged_decode_softcap). */
+int sp_varlen_prefill_softcap(void* out, const void* q, const void* k, const void* v,
+                              const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+                              int32_t num_seqs, int32_t max_seqlen_q,
+                              int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                              float scale, float logit_softcap, int32_t causal,
+                              int32_t window_left, sp_dtype dtype, void* stream);
 
 /*
  * Chunked prefill against a paged cache: the new tokens of every sequence attend to that
@@ -281,6 +316,15 @@ int sp_paged_prefill(void* out, const void* q,
                      int32_t num_seqs, int32_t max_seqlen_q, int32_t num_q_heads,
                      float scale, int32_t window_left, sp_dtype dtype,
                      void* workspace, size_t workspace_bytes, void* stream);
+/* sp_paged_prefill with Gemma-4's logit soft cap (see sp_paged_decode_softcap). */
+int sp_paged_prefill_softcap(void* out, const void* q,
+                             const void* k_pool, const void* v_pool, const sp_cache_layout* layout,
+                             const int32_t* block_tables, int32_t max_blocks_per_seq,
+                             const int32_t* cu_seqlens_q, const int32_t* context_lens,
+                             int32_t num_seqs, int32_t max_seqlen_q, int32_t num_q_heads,
+                             float scale, float logit_softcap, int32_t window_left,
+                             sp_dtype dtype, void* workspace, size_t workspace_bytes,
+                             void* stream);
 
 /*
  * One mixed ragged batch over a paged cache: every sequence's new tokens attend to its whole
@@ -323,6 +367,19 @@ int sp_ragged_paged_attention(void* out, const void* q,
                               int32_t decode_max_context_len, int32_t num_q_heads, float scale,
                               int32_t window_left, sp_dtype dtype, void* workspace,
                               size_t workspace_bytes, void* stream);
+/* sp_ragged_paged_attention with Gemma-4's logit soft cap on both halves (see
+ * sp_paged_decode_softcap). */
+int sp_ragged_paged_attention_softcap(void* out, const void* q,
+                                      const void* k_pool, const void* v_pool,
+                                      const sp_cache_layout* layout,
+                                      const int32_t* block_tables, int32_t max_blocks_per_seq,
+                                      const int32_t* cu_seqlens_q, const int32_t* context_lens,
+                                      int32_t num_seqs, int32_t num_prefill_seqs,
+                                      int32_t num_prefill_tokens, int32_t prefill_max_seqlen_q,
+                                      int32_t decode_max_context_len, int32_t num_q_heads,
+                                      float scale, float logit_softcap, int32_t window_left,
+                                      sp_dtype dtype, void* workspace, size_t workspace_bytes,
+                                      void* stream);
 
 /*
  * Dense attention on [batch, heads, seq, dim] tensors with every option of the reference's

@@ -51,14 +51,17 @@ def sliding_window_prefill_mask(new_len: int, total_len: int, window: int) -> np
     return np.where(bad, -np.inf, 0.0).astype(np.float32)
 
 
-def attention(q, k, v, scale: float, mask=None) -> np.ndarray:
-    """q [Sq, Hq, D], k/v [Lk, Hkv, D] -> [Sq, Hq, D] float64; rows with no visible key are 0."""
+def attention(q, k, v, scale: float, mask=None, softcap: float = 0.0) -> np.ndarray:
+    """q [Sq, Hq, D], k/v [Lk, Hkv, D] -> [Sq, Hq, D] float64; rows with no visible key are 0.
+    softcap > 0: softcap * tanh(logits / softcap) before the mask (gemma4.rs:366-377)."""
     q, k, v = to_f64(q), to_f64(k), to_f64(v)
     hq, hkv = q.shape[1], k.shape[1]
     rep = hq // hkv
     kr = np.repeat(k, rep, axis=1)  # repeat_kv: head h -> kv head h // rep
     vr = np.repeat(v, rep, axis=1)
     s = np.einsum("ihd,jhd->hij", q, kr) * scale
+    if softcap > 0:
+        s = softcap * np.tanh(s / softcap)
     if mask is not None:
         s = s + mask[None].astype(np.float64)
     m = s.max(axis=2, keepdims=True)

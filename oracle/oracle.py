@@ -56,6 +56,10 @@ _SIG = {
                                    c_void_p, c_int64, c_int64, c_int32, c_int64, c_int64, c_int32,
                                    c_int32, c_int32, c_double, c_void_p, c_int32, c_int64,
                                    c_int64, c_int32, c_void_p]),
+    "spo_attention_f64_cap": (None, [c_void_p, c_int64, c_int64, c_void_p, c_int64, c_int64,
+                                     c_void_p, c_int64, c_int64, c_int32, c_int64, c_int64,
+                                     c_int32, c_int32, c_int32, c_double, c_double, c_void_p,
+                                     c_int32, c_int64, c_int64, c_int32, c_void_p]),
     "spo_attention_f64": (None, [c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_int64,
                                  c_int64, c_int64, c_int64, c_int, c_int, c_int, c_double,
                                  c_void_p, c_int, c_int64, c_int64, c_int, c_void_p]),
@@ -193,14 +197,23 @@ def sliding_window_prefill_mask(new_len: int, total_len: int, window: int) -> np
 # --- attention --------------------------------------------------------------------------------
 
 def attention_f64(q, k, v, *, scale: float, mask=None, causal: bool = False, q_pos0: int = 0,
-                  window_left: int = -1, dtype: int | None = None) -> np.ndarray:
+                  window_left: int = -1, dtype: int | None = None,
+                  softcap: float = 0.0) -> np.ndarray:
     """q [Sq, Hq, D], k [Lk, Hkv, D], v [Lk, Hkv, Dv] (float32, or uint16 bf16 bits) ->
-    float64 [Sq, Hq, Dv]. mask: additive [Sq, Lk] (replaces the causal / window predicate)."""
+    float64 [Sq, Hq, Dv]. mask: additive [Sq, Lk] (replaces the causal / window predicate).
+    softcap > 0: Gemma-4's logit soft cap on the scaled logits, before the mask."""
     q, k, v = _c(q), _c(k), _c(v)
     dt = _dtype_code(q, dtype)
     sq, hq, d = q.shape
     lk, hkv, _ = k.shape
     dv = v.shape[2]
+    if softcap:
+        out = np.empty((sq, hq, dv), dtype=np.float64)
+        m = None if mask is None else _c(mask, np.float32)
+        lib().spo_attention_f64_cap(_p(q), hq * d, d, _p(k), hkv * d, d, _p(v), hkv * dv, dv, dv,
+                                    sq, lk, hq, hkv, d, scale, softcap, _p(m), int(causal),
+                                    q_pos0, window_left, dt, _p(out))
+        return out
     if dv == d:
         out = np.empty((sq, hq, d), dtype=np.float64)
         m = None if mask is None else _c(mask, np.float32)
@@ -231,7 +244,8 @@ def attention_f32_refops(q, k, v, *, scale: float, mask=None, causal: bool = Fal
 
 
 def paged_decode_f64(q, k_pool, v_pool, lay: Layout, block_tables, context_lens, *, scale: float,
-                     window_left: int = -1, dtype: int | None = None) -> np.ndarray:
+                     window_left: int = -1, dtype: int | None = None,
+                     softcap: float = 0.0) -> np.ndarray:
     """Reference decode for a batch: per sequence gather_kv (paged_attention.rs:313-378), then
     softmax((q k^T) scale) v over all gathered keys (decode has no mask, llama.rs:255-260),
     optionally restricted to the last window_left+1 keys. -> float64 [B, Hq, D]."""
@@ -246,7 +260,7 @@ def paged_decode_f64(q, k_pool, v_pool, lay: Layout, block_tables, context_lens,
         kt = np.ascontiguousarray(kg.transpose(1, 0, 2))               # [L, Hkv, D]
         vt = np.ascontiguousarray(vg.transpose(1, 0, 2))
         out[s] = attention_f64(q[s:s + 1], kt, vt, scale=scale, causal=True, q_pos0=L - 1,
-                               window_left=window_left, dtype=dtype)[0]
+                               window_left=window_left, dtype=dtype, softcap=softcap)[0]
     return out
 
 

@@ -216,6 +216,15 @@ void spo_attention_f64_v(const void* q, int64_t q_tok, int64_t q_head, const voi
                          int64_t v_head, int dv, int64_t sq, int64_t lk, int hq, int hkv, int d,
                          double scale, const float* mask, int causal, int64_t q_pos0,
                          int64_t window_left, int dtype, double* out) {
+  spo_attention_f64_cap(q, q_tok, q_head, k, k_tok, k_head, v, v_tok, v_head, dv, sq, lk, hq,
+                        hkv, d, scale, 0.0, mask, causal, q_pos0, window_left, dtype, out);
+}
+
+void spo_attention_f64_cap(const void* q, int64_t q_tok, int64_t q_head, const void* k,
+                           int64_t k_tok, int64_t k_head, const void* v, int64_t v_tok,
+                           int64_t v_head, int dv, int64_t sq, int64_t lk, int hq, int hkv,
+                           int d, double scale, double softcap, const float* mask, int causal,
+                           int64_t q_pos0, int64_t window_left, int dtype, double* out) {
   const int rep = hq / hkv; /* repeat_kv: head h reads KV head h / rep (transformer.rs:263-270) */
   /* Work items are (head, block of 64 query rows), spread over OpenMP threads. Each output row
    * is still one sequential sum over the keys in ascending order, so the thread count does not
@@ -257,6 +266,9 @@ void spo_attention_f64_v(const void* q, int64_t q_tok, int64_t q_head, const voi
           double acc = 0.0;
           for (int c = 0; c < d; ++c) acc += qd[c] * kd[j * d + c];
           acc *= scale; /* scale after the product (transformer.rs:234-235) */
+          /* Gemma-4's logit soft cap, on the scaled logits and before the mask
+           * (gemma4.rs:366-377) */
+          if (softcap > 0.0) acc = softcap * tanh(acc / softcap);
           if (mask)
             acc += (double)mask[i * lk + j];
           else if (!visible(causal, q_pos0, window_left, i, j))

@@ -28,6 +28,10 @@
  *       pinned: torch.nn.functional.scaled_dot_product_attention in float64 (a library
  *               routine), closed forms (one key -> v; equal keys -> mean(v); dominant key -> its v),
  *               GQA == repeated-head MHA, mask-rule == explicit additive mask
+ *   spo_attention_f64_cap                                 + the logit soft cap, gemma4.rs:366-377
+ *       pinned: the two-key closed form p1 = 1 / (1 + exp(c tanh(l2/c) - c tanh(l1/c))) with
+ *               math.tanh, saturation (logits far past +-c weigh as e^{+-c}), a cap far above
+ *               the logits equal to no cap, and the cap applied before the window mask
  *   spo_attention_f32_refops                              transformer.rs:234-243 op order in f32
  *       pinned: within f32 rounding of spo_attention_f64 on every test case
  *   spo_rope_caches                                       rope.rs:60-102 (with_base + repeat_interleave)
@@ -118,6 +122,13 @@ void spo_attention_f64_v(const void* q, int64_t q_tok, int64_t q_head, const voi
                          int64_t v_head, int dv, int64_t sq, int64_t lk, int hq, int hkv, int d,
                          double scale, const float* mask, int causal, int64_t q_pos0,
                          int64_t window_left, int dtype, double* out);
+/* spo_attention_f64_v with Gemma-4's logit soft cap: every scaled logit x becomes
+ * softcap * tanh(x / softcap) before the mask (gemma4.rs:366-377); softcap <= 0: none. */
+void spo_attention_f64_cap(const void* q, int64_t q_tok, int64_t q_head, const void* k,
+                           int64_t k_tok, int64_t k_head, const void* v, int64_t v_tok,
+                           int64_t v_head, int dv, int64_t sq, int64_t lk, int hq, int hkv,
+                           int d, double scale, double softcap, const float* mask, int causal,
+                           int64_t q_pos0, int64_t window_left, int dtype, double* out);
 void spo_attention_f32_refops(const void* q, int64_t q_tok, int64_t q_head, const void* k,
                               const void* v, int64_t kv_tok, int64_t kv_head, int64_t sq,
                               int64_t lk, int hq, int hkv, int d, float scale, const float* mask,

@@ -98,6 +98,31 @@ _SIGNATURES = {
                                    c_void_p, c_int32, c_void_p, c_void_p, c_int32, c_int32,
                                    c_int32, c_float, c_int32, c_int32, c_void_p, c_size_t,
                                    c_void_p]),
+    # the *_softcap entry points: the namesake's arguments with logit_softcap after scale
+    "sp_paged_decode_softcap": (c_int32, [c_void_p, c_void_p, c_void_p, c_void_p,
+                                          POINTER(CacheLayout), c_void_p, c_int32, c_void_p,
+                                          c_int32, c_int32, c_int32, c_float, c_float, c_int32,
+                                          c_int32, c_void_p, c_size_t, c_void_p]),
+    "sp_paged_append_decode_softcap": (c_int32, [c_void_p, c_void_p, c_void_p, c_void_p,
+                                                 POINTER(CacheLayout), c_void_p, c_void_p,
+                                                 c_int64, c_int64, c_void_p, c_int32, c_void_p,
+                                                 c_int32, c_int32, c_int32, c_float, c_float,
+                                                 c_int32, c_int32, c_void_p, c_size_t,
+                                                 c_void_p]),
+    "sp_varlen_prefill_softcap": (c_int32, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+                                            c_void_p, c_int32, c_int32, c_int32, c_int32,
+                                            c_int32, c_float, c_float, c_int32, c_int32, c_int32,
+                                            c_void_p]),
+    "sp_paged_prefill_softcap": (c_int32, [c_void_p, c_void_p, c_void_p, c_void_p,
+                                           POINTER(CacheLayout), c_void_p, c_int32, c_void_p,
+                                           c_void_p, c_int32, c_int32, c_int32, c_float, c_float,
+                                           c_int32, c_int32, c_void_p, c_size_t, c_void_p]),
+    "sp_ragged_paged_attention_softcap": (c_int32, [c_void_p, c_void_p, c_void_p, c_void_p,
+                                                    POINTER(CacheLayout), c_void_p, c_int32,
+                                                    c_void_p, c_void_p, c_int32, c_int32,
+                                                    c_int32, c_int32, c_int32, c_int32, c_float,
+                                                    c_float, c_int32, c_int32, c_void_p,
+                                                    c_size_t, c_void_p]),
     "sp_flash_attention": (c_int32, [c_void_p, c_void_p, c_void_p, c_void_p, c_int32, c_int32,
                                      c_int32, c_int32, c_int32, c_float, c_int32, c_int32,
                                      c_void_p]),
@@ -258,30 +283,36 @@ def paged_decode_workspace_size(num_seqs: int, num_q_heads: int, max_context_len
 
 def paged_append_decode(out, q, k_pool, v_pool, lay: CacheLayout, k_new, v_new, block_tables,
                         context_lens, max_context_len: int, scale: float, *, window_left: int = -1,
-                        workspace=None, stream=None) -> None:
-    """sp_paged_append_decode. k_new/v_new are [num_seqs, Hkv, D] (any strides the C call takes);
-    the rest as paged_decode."""
+                        workspace=None, softcap: float = 0.0, stream=None) -> None:
+    """sp_paged_append_decode (sp_paged_append_decode_softcap when softcap != 0). k_new/v_new
+    are [num_seqs, Hkv, D] (any strides the C call takes); the rest as paged_decode."""
     num_seqs, hq = q.shape[0], q.shape[1]
     ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
-    check(load().sp_paged_append_decode(_ptr(out), _ptr(q), _ptr(k_pool), _ptr(v_pool),
-                                        ctypes.byref(lay), _ptr(k_new), _ptr(v_new),
-                                        k_new.stride(0), k_new.stride(1), _ptr(block_tables),
-                                        block_tables.shape[1], _ptr(context_lens),
-                                        max_context_len, num_seqs, hq, scale, window_left,
-                                        sp_dtype(q), _ptr(workspace), ws_bytes, _stream(stream)))
+    head = (_ptr(out), _ptr(q), _ptr(k_pool), _ptr(v_pool), ctypes.byref(lay), _ptr(k_new),
+            _ptr(v_new), k_new.stride(0), k_new.stride(1), _ptr(block_tables),
+            block_tables.shape[1], _ptr(context_lens), max_context_len, num_seqs, hq, scale)
+    tail = (window_left, sp_dtype(q), _ptr(workspace), ws_bytes, _stream(stream))
+    if softcap:
+        check(load().sp_paged_append_decode_softcap(*head, softcap, *tail))
+    else:
+        check(load().sp_paged_append_decode(*head, *tail))
 
 
 def paged_decode(out, q, k_pool, v_pool, lay: CacheLayout, block_tables, context_lens,
                  max_context_len: int, scale: float, *, window_left: int = -1, workspace=None,
-                 stream=None) -> None:
-    """sp_paged_decode. q/out are [num_seqs, Hq, D]; block_tables [num_seqs, max_blocks]."""
+                 softcap: float = 0.0, stream=None) -> None:
+    """sp_paged_decode (sp_paged_decode_softcap when softcap != 0). q/out are
+    [num_seqs, Hq, D]; block_tables [num_seqs, max_blocks]."""
     num_seqs, hq = q.shape[0], q.shape[1]
     ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
-    check(load().sp_paged_decode(_ptr(out), _ptr(q), _ptr(k_pool), _ptr(v_pool),
-                                 ctypes.byref(lay), _ptr(block_tables), block_tables.shape[1],
-                                 _ptr(context_lens), max_context_len, num_seqs, hq, scale,
-                                 window_left, sp_dtype(q), _ptr(workspace), ws_bytes,
-                                 _stream(stream)))
+    head = (_ptr(out), _ptr(q), _ptr(k_pool), _ptr(v_pool), ctypes.byref(lay),
+            _ptr(block_tables), block_tables.shape[1], _ptr(context_lens), max_context_len,
+            num_seqs, hq, scale)
+    tail = (window_left, sp_dtype(q), _ptr(workspace), ws_bytes, _stream(stream))
+    if softcap:
+        check(load().sp_paged_decode_softcap(*head, softcap, *tail))
+    else:
+        check(load().sp_paged_decode(*head, *tail))
 
 
 def paged_decode_noalloc(out, q, k_pool, v_pool, lay: CacheLayout, block_tables, context_lens,
@@ -300,16 +331,22 @@ def paged_decode_noalloc(out, q, k_pool, v_pool, lay: CacheLayout, block_tables,
 def ragged_paged_attention(out, q, k_pool, v_pool, lay: CacheLayout, block_tables, cu_seqlens_q,
                            context_lens, *, num_prefill_seqs: int, num_prefill_tokens: int,
                            prefill_max_seqlen_q: int, decode_max_context_len: int, scale: float,
-                           window_left: int = -1, workspace=None, stream=None) -> None:
-    """sp_ragged_paged_attention: one mixed batch, chunks [0, num_prefill_seqs) first, then one
-    token per decode sequence; q/out [total_q, Hq, D]."""
+                           window_left: int = -1, workspace=None, softcap: float = 0.0,
+                           stream=None) -> None:
+    """sp_ragged_paged_attention (sp_ragged_paged_attention_softcap when softcap != 0): one mixed
+    batch, chunks [0, num_prefill_seqs) first, then one token per decode sequence; q/out
+    [total_q, Hq, D]."""
     hq = q.shape[1]
     ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
-    check(load().sp_ragged_paged_attention(
-        _ptr(out), _ptr(q), _ptr(k_pool), _ptr(v_pool), ctypes.byref(lay), _ptr(block_tables),
-        block_tables.shape[1], _ptr(cu_seqlens_q), _ptr(context_lens), context_lens.numel(),
-        num_prefill_seqs, num_prefill_tokens, prefill_max_seqlen_q, decode_max_context_len, hq,
-        scale, window_left, sp_dtype(q), _ptr(workspace), ws_bytes, _stream(stream)))
+    head = (_ptr(out), _ptr(q), _ptr(k_pool), _ptr(v_pool), ctypes.byref(lay), _ptr(block_tables),
+            block_tables.shape[1], _ptr(cu_seqlens_q), _ptr(context_lens), context_lens.numel(),
+            num_prefill_seqs, num_prefill_tokens, prefill_max_seqlen_q, decode_max_context_len,
+            hq, scale)
+    tail = (window_left, sp_dtype(q), _ptr(workspace), ws_bytes, _stream(stream))
+    if softcap:
+        check(load().sp_ragged_paged_attention_softcap(*head, softcap, *tail))
+    else:
+        check(load().sp_ragged_paged_attention(*head, *tail))
 
 
 def alloc_ragged_workspace(num_seqs: int, num_prefill_seqs: int, prefill_max_seqlen_q: int,
@@ -335,12 +372,16 @@ def alloc_decode_workspace(num_seqs: int, num_q_heads: int, max_context_len: int
 
 def varlen_prefill(out, q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q: int, scale: float, *,
                    causal: int = SP_CAUSAL_BOTTOM_RIGHT, window_left: int = -1,
-                   stream=None) -> None:
-    """sp_varlen_prefill. q/out [total_q, Hq, D], k/v [total_k, Hkv, D] contiguous."""
-    check(load().sp_varlen_prefill(_ptr(out), _ptr(q), _ptr(k), _ptr(v), _ptr(cu_seqlens_q),
-                                   _ptr(cu_seqlens_k), cu_seqlens_q.numel() - 1, max_seqlen_q,
-                                   q.shape[1], k.shape[1], q.shape[2], scale, causal,
-                                   window_left, sp_dtype(q), _stream(stream)))
+                   softcap: float = 0.0, stream=None) -> None:
+    """sp_varlen_prefill (sp_varlen_prefill_softcap when softcap != 0). q/out [total_q, Hq, D],
+    k/v [total_k, Hkv, D] contiguous."""
+    head = (_ptr(out), _ptr(q), _ptr(k), _ptr(v), _ptr(cu_seqlens_q), _ptr(cu_seqlens_k),
+            cu_seqlens_q.numel() - 1, max_seqlen_q, q.shape[1], k.shape[1], q.shape[2], scale)
+    tail = (causal, window_left, sp_dtype(q), _stream(stream))
+    if softcap:
+        check(load().sp_varlen_prefill_softcap(*head, softcap, *tail))
+    else:
+        check(load().sp_varlen_prefill(*head, *tail))
 
 
 def paged_prefill_workspace_size(num_seqs: int, max_seqlen_q: int, num_q_heads: int,
@@ -358,16 +399,20 @@ def alloc_paged_prefill_workspace(num_seqs: int, max_seqlen_q: int, num_q_heads:
 
 def paged_prefill(out, q, k_pool, v_pool, lay: CacheLayout, block_tables, cu_seqlens_q,
                   context_lens, max_seqlen_q: int, scale: float, *, window_left: int = -1,
-                  workspace=None, stream=None) -> None:
-    """sp_paged_prefill. q/out [total_q, Hq, D]; the new tokens are already in the pools.
-    workspace: optional device tensor for the split-key partials (None: no split)."""
+                  workspace=None, softcap: float = 0.0, stream=None) -> None:
+    """sp_paged_prefill (sp_paged_prefill_softcap when softcap != 0). q/out [total_q, Hq, D];
+    the new tokens are already in the pools. workspace: optional device tensor for the
+    split-key partials (None: no split)."""
     ws_ptr = _ptr(workspace) if workspace is not None else None
     ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
-    check(load().sp_paged_prefill(_ptr(out), _ptr(q), _ptr(k_pool), _ptr(v_pool),
-                                  ctypes.byref(lay), _ptr(block_tables), block_tables.shape[1],
-                                  _ptr(cu_seqlens_q), _ptr(context_lens),
-                                  cu_seqlens_q.numel() - 1, max_seqlen_q, q.shape[1], scale,
-                                  window_left, sp_dtype(q), ws_ptr, ws_bytes, _stream(stream)))
+    head = (_ptr(out), _ptr(q), _ptr(k_pool), _ptr(v_pool), ctypes.byref(lay),
+            _ptr(block_tables), block_tables.shape[1], _ptr(cu_seqlens_q), _ptr(context_lens),
+            cu_seqlens_q.numel() - 1, max_seqlen_q, q.shape[1], scale)
+    tail = (window_left, sp_dtype(q), ws_ptr, ws_bytes, _stream(stream))
+    if softcap:
+        check(load().sp_paged_prefill_softcap(*head, softcap, *tail))
+    else:
+        check(load().sp_paged_prefill(*head, *tail))
 
 
 def flash_attention_masked(out, q, k, v, mask, scale: float, *, causal: bool = False,

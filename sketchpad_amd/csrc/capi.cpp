@@ -296,35 +296,63 @@ static int decode_setup(const char* fn, void* out, const void* q, const void* k_
   return SP_OK;
 }
 
-int sp_paged_decode(void* out, const void* q, const void* k_pool, const void* v_pool,
-                    const sp_cache_layout* layout, const int32_t* block_tables,
-                    int32_t max_blocks_per_seq, const int32_t* context_lens,
-                    int32_t max_context_len, int32_t num_seqs, int32_t num_q_heads, float scale,
-                    int32_t window_left, sp_dtype dtype, void* workspace, size_t workspace_bytes,
-                    void* stream) {
+}  // extern "C"
+
+// The logit soft cap of the *_softcap entry points (Gemma-4's attn_logit_softcap: logits =
+// cap * tanh(logits / cap) on the scaled product, before the mask, gemma4.rs:366-377). 0: none;
+// > 0 runs on the head-dim-256 bf16 / f16 kernels, which take it as cap_in = 2 log2(e) scale /
+// cap and cap_out = cap log2(e) (softcap_log2: the softmax's exponent units).
+static int softcap_args(const char* fn, float softcap, float scale, int head_dim, sp_dtype dtype,
+                        float* cap_in, float* cap_out) {
+  *cap_in = *cap_out = 0.f;
+  if (softcap == 0.f) return SP_OK;
+  if (!(softcap > 0.f) || !isfinite(softcap))
+    return fail(SP_EINVAL, "%s: logit_softcap must be finite and >= 0 (got %g)", fn,
+                (double)softcap);
+  if (head_dim != 256 || dtype == SP_F32)
+    return fail(SP_EUNSUPPORTED,
+                "%s: the logit soft cap runs at head_dim 256 on bf16 / f16 tensors (got head_dim "
+                "%d, %s)",
+                fn, head_dim, dtype_name(dtype));
+  *cap_in = (float)(2.0 * 1.4426950408889634 * (double)scale / (double)softcap);
+  *cap_out = (float)((double)softcap * 1.4426950408889634);
+  return SP_OK;
+}
+
+static int paged_decode_impl(const char* fn, void* out, const void* q, const void* k_pool,
+                             const void* v_pool, const sp_cache_layout* layout,
+                             const int32_t* block_tables, int32_t max_blocks_per_seq,
+                             const int32_t* context_lens, int32_t max_context_len,
+                             int32_t num_seqs, int32_t num_q_heads, float scale,
+                             int32_t window_left, sp_dtype dtype, void* workspace,
+                             size_t workspace_bytes, float softcap, void* stream) {
   DecodeArgs a{};
-  if (int rc = decode_setup("sp_paged_decode", out, q, k_pool, v_pool, layout, block_tables,
-                            max_blocks_per_seq, context_lens, max_context_len, num_seqs,
-                            num_q_heads, scale, window_left, dtype, workspace, workspace_bytes,
-                            &a))
+  if (int rc = decode_setup(fn, out, q, k_pool, v_pool, layout, block_tables, max_blocks_per_seq,
+                            context_lens, max_context_len, num_seqs, num_q_heads, scale,
+                            window_left, dtype, workspace, workspace_bytes, &a))
+    return rc;
+  if (int rc = softcap_args(fn, softcap, scale, layout->head_dim, dtype, &a.cap_in, &a.cap_out))
     return rc;
   if (num_seqs == 0) return SP_OK;
   pool_strides(layout, dtype_size(dtype), &a.block_stride_b, &a.layer_off_b);
   return launch_paged_decode(a, dtype, layout->head_dim, (hipStream_t)stream);
 }
 
-int sp_paged_append_decode(void* out, const void* q, void* k_pool, void* v_pool,
-                           const sp_cache_layout* layout, const void* k_new, const void* v_new,
-                           int64_t token_stride, int64_t head_stride, const int32_t* block_tables,
-                           int32_t max_blocks_per_seq, const int32_t* context_lens,
-                           int32_t max_context_len, int32_t num_seqs, int32_t num_q_heads,
-                           float scale, int32_t window_left, sp_dtype dtype, void* workspace,
-                           size_t workspace_bytes, void* stream) {
-  const char* fn = "sp_paged_append_decode";
+static int paged_append_decode_impl(const char* fn, void* out, const void* q, void* k_pool,
+                                    void* v_pool, const sp_cache_layout* layout,
+                                    const void* k_new, const void* v_new, int64_t token_stride,
+                                    int64_t head_stride, const int32_t* block_tables,
+                                    int32_t max_blocks_per_seq, const int32_t* context_lens,
+                                    int32_t max_context_len, int32_t num_seqs,
+                                    int32_t num_q_heads, float scale, int32_t window_left,
+                                    sp_dtype dtype, void* workspace, size_t workspace_bytes,
+                                    float softcap, void* stream) {
   DecodeArgs a{};
   if (int rc = decode_setup(fn, out, q, k_pool, v_pool, layout, block_tables, max_blocks_per_seq,
                             context_lens, max_context_len, num_seqs, num_q_heads, scale,
                             window_left, dtype, workspace, workspace_bytes, &a))
+    return rc;
+  if (int rc = softcap_args(fn, softcap, scale, layout->head_dim, dtype, &a.cap_in, &a.cap_out))
     return rc;
   if (num_seqs == 0) return SP_OK;
   if (!k_new || !v_new) return fail(SP_EINVAL, "%s: NULL pointer argument", fn);
@@ -339,6 +367,62 @@ int sp_paged_append_decode(void* out, const void* q, void* k_pool, void* v_pool,
   a.new_tok_stride_b = token_stride * es;
   a.new_head_stride_b = head_stride * es;
   return launch_paged_decode(a, dtype, layout->head_dim, (hipStream_t)stream);
+}
+
+extern "C" {
+
+int sp_paged_decode(void* out, const void* q, const void* k_pool, const void* v_pool,
+                    const sp_cache_layout* layout, const int32_t* block_tables,
+                    int32_t max_blocks_per_seq, const int32_t* context_lens,
+                    int32_t max_context_len, int32_t num_seqs, int32_t num_q_heads, float scale,
+                    int32_t window_left, sp_dtype dtype, void* workspace, size_t workspace_bytes,
+                    void* stream) {
+  return paged_decode_impl("sp_paged_decode", out, q, k_pool, v_pool, layout, block_tables,
+                           max_blocks_per_seq, context_lens, max_context_len, num_seqs,
+                           num_q_heads, scale, window_left, dtype, workspace, workspace_bytes,
+                           0.f, stream);
+}
+
+int sp_paged_decode_softcap(void* out, const void* q, const void* k_pool, const void* v_pool,
+                            const sp_cache_layout* layout, const int32_t* block_tables,
+                            int32_t max_blocks_per_seq, const int32_t* context_lens,
+                            int32_t max_context_len, int32_t num_seqs, int32_t num_q_heads,
+                            float scale, float logit_softcap, int32_t window_left,
+                            sp_dtype dtype, void* workspace, size_t workspace_bytes,
+                            void* stream) {
+  return paged_decode_impl("sp_paged_decode_softcap", out, q, k_pool, v_pool, layout,
+                           block_tables, max_blocks_per_seq, context_lens, max_context_len,
+                           num_seqs, num_q_heads, scale, window_left, dtype, workspace,
+                           workspace_bytes, logit_softcap, stream);
+}
+
+int sp_paged_append_decode(void* out, const void* q, void* k_pool, void* v_pool,
+                           const sp_cache_layout* layout, const void* k_new, const void* v_new,
+                           int64_t token_stride, int64_t head_stride, const int32_t* block_tables,
+                           int32_t max_blocks_per_seq, const int32_t* context_lens,
+                           int32_t max_context_len, int32_t num_seqs, int32_t num_q_heads,
+                           float scale, int32_t window_left, sp_dtype dtype, void* workspace,
+                           size_t workspace_bytes, void* stream) {
+  return paged_append_decode_impl("sp_paged_append_decode", out, q, k_pool, v_pool, layout,
+                                  k_new, v_new, token_stride, head_stride, block_tables,
+                                  max_blocks_per_seq, context_lens, max_context_len, num_seqs,
+                                  num_q_heads, scale, window_left, dtype, workspace,
+                                  workspace_bytes, 0.f, stream);
+}
+
+int sp_paged_append_decode_softcap(void* out, const void* q, void* k_pool, void* v_pool,
+                                   const sp_cache_layout* layout, const void* k_new,
+                                   const void* v_new, int64_t token_stride, int64_t head_stride,
+                                   const int32_t* block_tables, int32_t max_blocks_per_seq,
+                                   const int32_t* context_lens, int32_t max_context_len,
+                                   int32_t num_seqs, int32_t num_q_heads, float scale,
+                                   float logit_softcap, int32_t window_left, sp_dtype dtype,
+                                   void* workspace, size_t workspace_bytes, void* stream) {
+  return paged_append_decode_impl("sp_paged_append_decode_softcap", out, q, k_pool, v_pool,
+                                  layout, k_new, v_new, token_stride, head_stride, block_tables,
+                                  max_blocks_per_seq, context_lens, max_context_len, num_seqs,
+                                  num_q_heads, scale, window_left, dtype, workspace,
+                                  workspace_bytes, logit_softcap, stream);
 }
 
 int sp_paged_decode_noalloc(void* out, const void* q, const void* k_pool, const void* v_pool,
@@ -407,12 +491,13 @@ static int check_prefill_common(const char* fn, int32_t num_seqs, int32_t max_se
 
 static bool misaligned16(const void* p) { return ((uintptr_t)p & 15) != 0; }
 
-int sp_varlen_prefill(void* out, const void* q, const void* k, const void* v,
-                      const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k, int32_t num_seqs,
-                      int32_t max_seqlen_q, int32_t num_q_heads, int32_t num_kv_heads,
-                      int32_t head_dim, float scale, int32_t causal, int32_t window_left,
-                      sp_dtype dtype, void* stream) {
-  const char* fn = "sp_varlen_prefill";
+static int varlen_prefill_impl(const char* fn, void* out, const void* q, const void* k,
+                               const void* v, const int32_t* cu_seqlens_q,
+                               const int32_t* cu_seqlens_k, int32_t num_seqs,
+                               int32_t max_seqlen_q, int32_t num_q_heads, int32_t num_kv_heads,
+                               int32_t head_dim, float scale, int32_t causal,
+                               int32_t window_left, sp_dtype dtype, float softcap,
+                               void* stream) {
   if (int rc = check_prefill_common(fn, num_seqs, max_seqlen_q, num_q_heads, num_kv_heads,
                                     head_dim, scale, causal, window_left, dtype))
     return rc;
@@ -442,7 +527,30 @@ int sp_varlen_prefill(void* out, const void* q, const void* k, const void* v,
   a.causal = causal;
   a.window_left = window_left;
   a.scale_log2 = scale * 1.4426950408889634f;
+  if (int rc = softcap_args(fn, softcap, scale, head_dim, dtype, &a.cap_in, &a.cap_out))
+    return rc;
   return launch_prefill(a, dtype, head_dim, false, (hipStream_t)stream);
+}
+
+int sp_varlen_prefill(void* out, const void* q, const void* k, const void* v,
+                      const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k, int32_t num_seqs,
+                      int32_t max_seqlen_q, int32_t num_q_heads, int32_t num_kv_heads,
+                      int32_t head_dim, float scale, int32_t causal, int32_t window_left,
+                      sp_dtype dtype, void* stream) {
+  return varlen_prefill_impl("sp_varlen_prefill", out, q, k, v, cu_seqlens_q, cu_seqlens_k,
+                             num_seqs, max_seqlen_q, num_q_heads, num_kv_heads, head_dim, scale,
+                             causal, window_left, dtype, 0.f, stream);
+}
+
+int sp_varlen_prefill_softcap(void* out, const void* q, const void* k, const void* v,
+                              const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+                              int32_t num_seqs, int32_t max_seqlen_q, int32_t num_q_heads,
+                              int32_t num_kv_heads, int32_t head_dim, float scale,
+                              float logit_softcap, int32_t causal, int32_t window_left,
+                              sp_dtype dtype, void* stream) {
+  return varlen_prefill_impl("sp_varlen_prefill_softcap", out, q, k, v, cu_seqlens_q,
+                             cu_seqlens_k, num_seqs, max_seqlen_q, num_q_heads, num_kv_heads,
+                             head_dim, scale, causal, window_left, dtype, logit_softcap, stream);
 }
 
 // Key-range splits of a chunked prefill: the planner's count for the batch shape (the context
@@ -472,17 +580,20 @@ size_t sp_paged_prefill_workspace_size(int32_t num_seqs, int32_t max_seqlen_q,
   return prefill_partials_bytes(num_seqs, max_seqlen_q, num_q_heads, layout->head_dim, s);
 }
 
-int sp_paged_prefill(void* out, const void* q, const void* k_pool, const void* v_pool,
-                     const sp_cache_layout* layout, const int32_t* block_tables,
-                     int32_t max_blocks_per_seq, const int32_t* cu_seqlens_q,
-                     const int32_t* context_lens, int32_t num_seqs, int32_t max_seqlen_q,
-                     int32_t num_q_heads, float scale, int32_t window_left, sp_dtype dtype,
-                     void* workspace, size_t workspace_bytes, void* stream) {
-  const char* fn = "sp_paged_prefill";
+static int paged_prefill_impl(const char* fn, void* out, const void* q, const void* k_pool,
+                              const void* v_pool, const sp_cache_layout* layout,
+                              const int32_t* block_tables, int32_t max_blocks_per_seq,
+                              const int32_t* cu_seqlens_q, const int32_t* context_lens,
+                              int32_t num_seqs, int32_t max_seqlen_q, int32_t num_q_heads,
+                              float scale, int32_t window_left, sp_dtype dtype, void* workspace,
+                              size_t workspace_bytes, float softcap, void* stream) {
   if (int rc = check_layout(layout, fn)) return rc;
   if (int rc = check_prefill_common(fn, num_seqs, max_seqlen_q, num_q_heads,
                                     layout->num_kv_heads, layout->head_dim, scale,
                                     SP_CAUSAL_BOTTOM_RIGHT, window_left, dtype))
+    return rc;
+  float cap_in = 0.f, cap_out = 0.f;
+  if (int rc = softcap_args(fn, softcap, scale, layout->head_dim, dtype, &cap_in, &cap_out))
     return rc;
   if (num_seqs == 0 || max_seqlen_q == 0) return SP_OK;
   if (!out || !q || !k_pool || !v_pool || !block_tables || !cu_seqlens_q || !context_lens)
@@ -523,7 +634,34 @@ int sp_paged_prefill(void* out, const void* q, const void* k_pool, const void* v
                        : 1;
   a.partials = a.nsplit > 1 ? (float*)workspace : nullptr;
   a.max_q = max_seqlen_q;
+  a.cap_in = cap_in;
+  a.cap_out = cap_out;
   return launch_prefill(a, dtype, D, true, (hipStream_t)stream);
+}
+
+int sp_paged_prefill(void* out, const void* q, const void* k_pool, const void* v_pool,
+                     const sp_cache_layout* layout, const int32_t* block_tables,
+                     int32_t max_blocks_per_seq, const int32_t* cu_seqlens_q,
+                     const int32_t* context_lens, int32_t num_seqs, int32_t max_seqlen_q,
+                     int32_t num_q_heads, float scale, int32_t window_left, sp_dtype dtype,
+                     void* workspace, size_t workspace_bytes, void* stream) {
+  return paged_prefill_impl("sp_paged_prefill", out, q, k_pool, v_pool, layout, block_tables,
+                            max_blocks_per_seq, cu_seqlens_q, context_lens, num_seqs,
+                            max_seqlen_q, num_q_heads, scale, window_left, dtype, workspace,
+                            workspace_bytes, 0.f, stream);
+}
+
+int sp_paged_prefill_softcap(void* out, const void* q, const void* k_pool, const void* v_pool,
+                             const sp_cache_layout* layout, const int32_t* block_tables,
+                             int32_t max_blocks_per_seq, const int32_t* cu_seqlens_q,
+                             const int32_t* context_lens, int32_t num_seqs,
+                             int32_t max_seqlen_q, int32_t num_q_heads, float scale,
+                             float logit_softcap, int32_t window_left, sp_dtype dtype,
+                             void* workspace, size_t workspace_bytes, void* stream) {
+  return paged_prefill_impl("sp_paged_prefill_softcap", out, q, k_pool, v_pool, layout,
+                            block_tables, max_blocks_per_seq, cu_seqlens_q, context_lens,
+                            num_seqs, max_seqlen_q, num_q_heads, scale, window_left, dtype,
+                            workspace, workspace_bytes, logit_softcap, stream);
 }
 
 // Byte offset of the prefill's region in a mixed batch's workspace: the decode's partials come
@@ -600,18 +738,18 @@ static int fork_join_for(hipStream_t caller, ForkJoin** out) {
   return SP_OK;
 }
 
-int sp_ragged_paged_attention(void* out, const void* q, const void* k_pool, const void* v_pool,
-                              const sp_cache_layout* layout, const int32_t* block_tables,
-                              int32_t max_blocks_per_seq, const int32_t* cu_seqlens_q,
-                              const int32_t* context_lens, int32_t num_seqs,
-                              int32_t num_prefill_seqs, int32_t num_prefill_tokens,
-                              int32_t prefill_max_seqlen_q, int32_t decode_max_context_len,
-                              int32_t num_q_heads, float scale, int32_t window_left,
-                              sp_dtype dtype, void* workspace, size_t workspace_bytes,
-                              void* stream) {
-  const char* fn = "sp_ragged_paged_attention";
+static int ragged_paged_attention_impl(
+    const char* fn, void* out, const void* q, const void* k_pool, const void* v_pool,
+    const sp_cache_layout* layout, const int32_t* block_tables, int32_t max_blocks_per_seq,
+    const int32_t* cu_seqlens_q, const int32_t* context_lens, int32_t num_seqs,
+    int32_t num_prefill_seqs, int32_t num_prefill_tokens, int32_t prefill_max_seqlen_q,
+    int32_t decode_max_context_len, int32_t num_q_heads, float scale, int32_t window_left,
+    sp_dtype dtype, void* workspace, size_t workspace_bytes, float softcap, void* stream) {
   if (int rc = check_layout(layout, fn)) return rc;
   if (int rc = check_dtype(dtype, fn)) return rc;
+  float cap_in = 0.f, cap_out = 0.f;
+  if (int rc = softcap_args(fn, softcap, scale, layout->head_dim, dtype, &cap_in, &cap_out))
+    return rc;
   if (num_seqs < 0 || num_prefill_seqs < 0 || num_prefill_seqs > num_seqs ||
       num_prefill_tokens < 0 || num_q_heads <= 0 || max_blocks_per_seq < 0)
     return fail(SP_EINVAL,
@@ -625,17 +763,18 @@ int sp_ragged_paged_attention(void* out, const void* q, const void* k_pool, cons
   const int nd = num_seqs - num_prefill_seqs;
   const int64_t row = (int64_t)num_q_heads * layout->head_dim * dtype_size(dtype);
   auto decode_half = [&](void* ws, size_t ws_bytes, void* st) {
-    return sp_paged_decode((char*)out + num_prefill_tokens * row,
-                           (const char*)q + num_prefill_tokens * row, k_pool, v_pool, layout,
-                           block_tables + (int64_t)num_prefill_seqs * max_blocks_per_seq,
-                           max_blocks_per_seq, context_lens + num_prefill_seqs,
-                           decode_max_context_len, nd, num_q_heads, scale, window_left, dtype, ws,
-                           ws_bytes, st);
+    return paged_decode_impl(fn, (char*)out + num_prefill_tokens * row,
+                             (const char*)q + num_prefill_tokens * row, k_pool, v_pool, layout,
+                             block_tables + (int64_t)num_prefill_seqs * max_blocks_per_seq,
+                             max_blocks_per_seq, context_lens + num_prefill_seqs,
+                             decode_max_context_len, nd, num_q_heads, scale, window_left, dtype,
+                             ws, ws_bytes, softcap, st);
   };
   auto prefill_half = [&](void* ws, size_t ws_bytes, void* st) {
-    return sp_paged_prefill(out, q, k_pool, v_pool, layout, block_tables, max_blocks_per_seq,
-                            cu_seqlens_q, context_lens, num_prefill_seqs, prefill_max_seqlen_q,
-                            num_q_heads, scale, window_left, dtype, ws, ws_bytes, st);
+    return paged_prefill_impl(fn, out, q, k_pool, v_pool, layout, block_tables,
+                              max_blocks_per_seq, cu_seqlens_q, context_lens, num_prefill_seqs,
+                              prefill_max_seqlen_q, num_q_heads, scale, window_left, dtype, ws,
+                              ws_bytes, softcap, st);
   };
   if (nd == 0) return prefill_half(workspace, workspace_bytes, stream);
   if (num_prefill_seqs == 0) return decode_half(workspace, workspace_bytes, stream);
@@ -658,6 +797,8 @@ int sp_ragged_paged_attention(void* out, const void* q, const void* k_pool, cons
                             decode_max_context_len, nd, num_q_heads, scale, window_left, dtype,
                             workspace, workspace_bytes < d_bytes ? workspace_bytes : d_bytes, &da))
     return rc;
+  da.cap_in = cap_in;
+  da.cap_out = cap_out;
   pool_strides(layout, dtype_size(dtype), &da.block_stride_b, &da.layer_off_b);
   const hipStream_t caller = (hipStream_t)stream;
   std::lock_guard<std::mutex> lock(g_fork_mu);
@@ -678,6 +819,36 @@ int sp_ragged_paged_attention(void* out, const void* q, const void* k_pool, cons
   if (e == hipSuccess) e = hipStreamWaitEvent(caller, fj->join, 0);
   if (e != hipSuccess) return fail(SP_EHIP, "%s: join: %s", fn, hipGetErrorString(e));
   return rc;
+}
+
+int sp_ragged_paged_attention(void* out, const void* q, const void* k_pool, const void* v_pool,
+                              const sp_cache_layout* layout, const int32_t* block_tables,
+                              int32_t max_blocks_per_seq, const int32_t* cu_seqlens_q,
+                              const int32_t* context_lens, int32_t num_seqs,
+                              int32_t num_prefill_seqs, int32_t num_prefill_tokens,
+                              int32_t prefill_max_seqlen_q, int32_t decode_max_context_len,
+                              int32_t num_q_heads, float scale, int32_t window_left,
+                              sp_dtype dtype, void* workspace, size_t workspace_bytes,
+                              void* stream) {
+  return ragged_paged_attention_impl(
+      "sp_ragged_paged_attention", out, q, k_pool, v_pool, layout, block_tables,
+      max_blocks_per_seq, cu_seqlens_q, context_lens, num_seqs, num_prefill_seqs,
+      num_prefill_tokens, prefill_max_seqlen_q, decode_max_context_len, num_q_heads, scale,
+      window_left, dtype, workspace, workspace_bytes, 0.f, stream);
+}
+
+int sp_ragged_paged_attention_softcap(
+    void* out, const void* q, const void* k_pool, const void* v_pool,
+    const sp_cache_layout* layout, const int32_t* block_tables, int32_t max_blocks_per_seq,
+    const int32_t* cu_seqlens_q, const int32_t* context_lens, int32_t num_seqs,
+    int32_t num_prefill_seqs, int32_t num_prefill_tokens, int32_t prefill_max_seqlen_q,
+    int32_t decode_max_context_len, int32_t num_q_heads, float scale, float logit_softcap,
+    int32_t window_left, sp_dtype dtype, void* workspace, size_t workspace_bytes, void* stream) {
+  return ragged_paged_attention_impl(
+      "sp_ragged_paged_attention_softcap", out, q, k_pool, v_pool, layout, block_tables,
+      max_blocks_per_seq, cu_seqlens_q, context_lens, num_seqs, num_prefill_seqs,
+      num_prefill_tokens, prefill_max_seqlen_q, decode_max_context_len, num_q_heads, scale,
+      window_left, dtype, workspace, workspace_bytes, logit_softcap, stream);
 }
 
 static int flash_attention_impl(const char* fn, void* out, const void* q, const void* k,

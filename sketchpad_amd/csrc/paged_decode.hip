@@ -161,7 +161,8 @@ constexpr int decode_min_waves() {
 
 // SUB: block sizes below the 16-token tile (1, 2, 4 or 8, dividing it), so that a tile spans
 // several blocks; every row of a tile then takes the block its position maps to.
-template <typename T, int D, bool SUB>
+// CAP: the logit soft cap (a.cap_in / a.cap_out), instantiated for head_dim 256.
+template <typename T, int D, bool SUB, bool CAP = false>
 __global__ void __launch_bounds__(64 * kDecodeWaves, (decode_min_waves<T, D, SUB>()))
     paged_decode_kernel(DecodeArgs a) {
   using C = DecodeCfg<T, D>;
@@ -413,7 +414,10 @@ __global__ void __launch_bounds__(64 * kDecodeWaves, (decode_min_waves<T, D, SUB
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const bool valid = ((tile_ok >> (4 * g + j)) & 1) && pos + j >= start_tok && pos + j < L;
-      sv[j] = valid ? s[j] * a.scale_log2 : -INFINITY;
+      if constexpr (CAP)
+        sv[j] = valid ? softcap_log2(s[j], a.cap_in, a.cap_out) : -INFINITY;
+      else
+        sv[j] = valid ? s[j] * a.scale_log2 : -INFINITY;
     }
     float mt = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
     mt = fmaxf(mt, xor16(mt));
@@ -621,10 +625,22 @@ DecodePlan plan_decode(int num_seqs, int hq, int hkv, int head_dim, int max_cont
 template <typename T, int D>
 static int launch_typed(const DecodeArgs& a, hipStream_t stream) {
   const dim3 grid(a.num_seqs * a.hkv, a.max_splits);
-  if (a.block_size < kTile)
-    hipLaunchKernelGGL((paged_decode_kernel<T, D, true>), grid, dim3(64 * kDecodeWaves), 0, stream, a);
-  else
-    hipLaunchKernelGGL((paged_decode_kernel<T, D, false>), grid, dim3(64 * kDecodeWaves), 0, stream, a);
+  const dim3 block(64 * kDecodeWaves);
+  const bool sub = a.block_size < kTile;
+  if (a.cap_out > 0.f) {  // the host admits the soft cap at head_dim 256 only
+    if constexpr (D == 256) {
+      if (sub)
+        hipLaunchKernelGGL((paged_decode_kernel<T, D, true, true>), grid, block, 0, stream, a);
+      else
+        hipLaunchKernelGGL((paged_decode_kernel<T, D, false, true>), grid, block, 0, stream, a);
+    } else {
+      return fail(SP_EUNSUPPORTED, "paged decode: logit soft cap at head_dim %d", D);
+    }
+  } else if (sub) {
+    hipLaunchKernelGGL((paged_decode_kernel<T, D, true>), grid, block, 0, stream, a);
+  } else {
+    hipLaunchKernelGGL((paged_decode_kernel<T, D, false>), grid, block, 0, stream, a);
+  }
   if (a.max_splits > 1)
     hipLaunchKernelGGL((decode_combine_kernel<T, D>), dim3(a.hq, a.num_seqs), dim3(64), 0, stream,
                        a);

@@ -1069,8 +1069,9 @@ __global__ void __launch_bounds__(256, 3) prefill_k32_kernel(PrefillArgs a) {
 // per-wave state does not fit at this width (O^T alone is 128 VGPRs per lane), so 32-key tiles
 // (one 32 x 32 score block, 16 VGPRs) with the softmax between the two products, two workgroups
 // per CU and the tiles loaded one ahead through two buffers (64 KiB of LDS). Contiguous and
-// paged K/V, the same masks and arguments as prefill_kernel; no key split.
-template <typename T, int D, bool PAGED>
+// paged K/V, the same masks and arguments as prefill_kernel; no key split. CAP: the logit soft
+// cap (a.cap_in / a.cap_out) applied to each tile's raw products before the masks.
+template <typename T, int D, bool PAGED, bool CAP = false>
 __global__ void __launch_bounds__(256, 2) prefill_wide_kernel(PrefillArgs a) {
   using C = PrefillCfg<D>;  // the row swizzle
   using M = PrefillMfma<T>;
@@ -1162,7 +1163,8 @@ __global__ void __launch_bounds__(256, 2) prefill_wide_kernel(PrefillArgs a) {
   // ---- Q^T operand (B of the S^T MFMA): query wq0 + l32, dims 16c + 8hh .. +7, unscaled.
   const int wq0 = qs + 32 * wave;
   const int my_q = wq0 + l32;
-  const float c2 = a.scale_log2;  // > 0 (checked on the host)
+  // > 0 (checked on the host); with the soft cap the scores already are exponents
+  const float c2 = CAP ? 1.f : a.scale_log2;
   uint4 qreg[KC];
   {
     const char* qp = qbase + (int64_t)min(my_q, qe - 1) * a.q_tok * 2;
@@ -1498,6 +1500,10 @@ __global__ void __launch_bounds__(256, 2) prefill_wide_kernel(PrefillArgs a) {
     }
     if (visits(t0)) {
       qk(kcur, sc, [](int) {});
+      if constexpr (CAP) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) sc[r] = softcap_log2(sc[r], a.cap_in, a.cap_out);
+      }
       apply_mask(t0, sc);
       float off = m_used;
       asm volatile("" : "+v"(off));
@@ -1674,15 +1680,24 @@ static int launch_wide(const PrefillArgs& a, bool paged, hipStream_t stream) {
   const int64_t blocks = (int64_t)a.num_qblocks * a.num_seqs * a.hq;
   if (blocks <= 0) return SP_OK;
   if (blocks > 0x7fffffff) return fail(SP_EINVAL, "prefill: grid of %lld workgroups", (long long)blocks);
-  if (paged)
-    hipLaunchKernelGGL((prefill_wide_kernel<T, 256, true>), dim3((unsigned)blocks), dim3(256), 0, stream, a);
-  else
-    hipLaunchKernelGGL((prefill_wide_kernel<T, 256, false>), dim3((unsigned)blocks), dim3(256), 0, stream, a);
+  const dim3 grid((unsigned)blocks), block(256);
+  if (a.cap_out > 0.f) {
+    if (paged)
+      hipLaunchKernelGGL((prefill_wide_kernel<T, 256, true, true>), grid, block, 0, stream, a);
+    else
+      hipLaunchKernelGGL((prefill_wide_kernel<T, 256, false, true>), grid, block, 0, stream, a);
+  } else if (paged) {
+    hipLaunchKernelGGL((prefill_wide_kernel<T, 256, true>), grid, block, 0, stream, a);
+  } else {
+    hipLaunchKernelGGL((prefill_wide_kernel<T, 256, false>), grid, block, 0, stream, a);
+  }
   return check_launch("prefill_wide_kernel");
 }
 
 template <typename T>
 static int launch_t(const PrefillArgs& a, int head_dim, bool paged, hipStream_t stream) {
+  if (a.cap_out > 0.f && head_dim != 256)
+    return fail(SP_EUNSUPPORTED, "prefill: logit soft cap at head_dim %d", head_dim);
   switch (head_dim) {
     case 64: return launch_td<T, 64>(a, paged, stream);
     case 128: return launch_td<T, 128>(a, paged, stream);
@@ -1696,6 +1711,7 @@ int launch_prefill(const PrefillArgs& args, sp_dtype dtype, int head_dim, bool p
   PrefillArgs a = args;
   if (a.nsplit < 1 || !a.partials) a.nsplit = 1;
   if (dtype == SP_F32) {
+    if (a.cap_out > 0.f) return fail(SP_EUNSUPPORTED, "prefill: logit soft cap on f32 tensors");
     a.nsplit = 1;  // the fp32 kernel walks every key tile itself (no split partials)
     return launch_prefill_f32(a, head_dim, paged, stream);
   }

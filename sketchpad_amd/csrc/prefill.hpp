@@ -49,7 +49,11 @@ struct PrefillArgs {
   // offset b mask_b + h mask_h + i mask_q + j, added to score * scale; nullptr: none
   const float* mask;
   int64_t mask_b, mask_h, mask_q;
-  float inv_scale;  // 1 / scale
+  float inv_scale;  // 1 / scale (log2(e) with the soft cap: the mask then adds to the exponent)
+  // Logit soft cap (head_dim 256 only): cap_out > 0 turns each raw product s into the exponent
+  // softcap_log2(s, cap_in, cap_out) = cap log2(e) tanh(s scale / cap) instead of
+  // s * scale_log2; 0: none.
+  float cap_in, cap_out;
 };
 
 // Split count for a chunked prefill of base_wgs workgroups whose sequences span up to

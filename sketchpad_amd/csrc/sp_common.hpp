@@ -103,6 +103,19 @@ template <> struct Dot2<f16_t> {
 };
 
 // ---------------------------------------------------------------------------------------------
+// Logit soft cap (Gemma-4's attn_logit_softcap, gemma4.rs:366-369: logits = cap * tanh(logits /
+// cap) on the scaled product, before the mask), in the softmax's base-2 exponent units: for a raw
+// product s, with cap_in = 2 log2(e) scale / cap and cap_out = cap log2(e),
+//   cap_out * tanh(s scale / cap) = cap_out - 2 cap_out / (1 + 2^(s cap_in)),
+// since tanh(y) = 1 - 2 / (1 + e^(2y)). The exponential saturates cleanly: 2^(s cap_in) = inf
+// gives cap_out and 0 gives -cap_out. One exponential, one reciprocal, three other ops.
+// ---------------------------------------------------------------------------------------------
+__device__ __forceinline__ float softcap_log2(float s, float cap_in, float cap_out) {
+  const float r = __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(s * cap_in));
+  return __builtin_fmaf(-2.f * cap_out, r, cap_out);
+}
+
+// ---------------------------------------------------------------------------------------------
 // Wavefront helpers (wave64).
 // ---------------------------------------------------------------------------------------------
 // Make LDS writes by any lane of this wave visible to later LDS reads by the same wave.

@@ -24,12 +24,16 @@ def _slots(w: W.DecodeWorkload) -> np.ndarray:
     return np.where(ok, blk * w.block_size + pos % w.block_size, -1).astype(np.int32)
 
 
-def fused_vs_separate(w: W.DecodeWorkload, k_new=None, v_new=None, oracle=True, max_ctx=None):
+def fused_vs_separate(w: W.DecodeWorkload, k_new=None, v_new=None, oracle=True, max_ctx=None,
+                      softcap=0.0, qscale=1.0):
     """max_ctx: the max_context_len both calls get (default: the longest context); contexts past
-    it are attended up to it, and their new token is still appended at position L - 1."""
+    it are attended up to it, and their new token is still appended at position L - 1.
+    softcap: the logit soft cap of both calls; qscale multiplies q."""
     announce(f"append+decode {w.name} B={w.num_seqs} Hq={w.hq} Hkv={w.hkv} D={w.head_dim} "
              f"BS={w.block_size} {w.dtype} window={w.window_left} maxL={w.max_context_len}")
     t = W.make_decode_tensors(w)
+    if qscale != 1.0:
+        t["q"].mul_(qscale)
     lay = w.layout()
     kn = t["k_new"] if k_new is None else k_new
     vn = t["v_new"] if v_new is None else v_new
@@ -44,11 +48,12 @@ def fused_vs_separate(w: W.DecodeWorkload, k_new=None, v_new=None, oracle=True, 
     sp.kv_append(t["k_pool"], t["v_pool"], lay, kn, vn, slots,
                  token_stride=kn.stride(0), head_stride=kn.stride(1))
     sp.paged_decode(t["out"], t["q"], t["k_pool"], t["v_pool"], lay, t["block_tables"],
-                    t["context_lens"], max_ctx, scale, window_left=w.window_left, workspace=ws)
+                    t["context_lens"], max_ctx, scale, window_left=w.window_left, workspace=ws,
+                    softcap=softcap)
     # fused
     sp.paged_append_decode(out2, t["q"], kp2, vp2, lay, kn, vn, t["block_tables"],
                            t["context_lens"], max_ctx, scale, window_left=w.window_left,
-                           workspace=ws2)
+                           workspace=ws2, softcap=softcap)
     torch.cuda.synchronize()
     assert torch.equal(t["k_pool"], kp2), "K pool differs"
     assert torch.equal(t["v_pool"], vp2), "V pool differs"
@@ -58,7 +63,8 @@ def fused_vs_separate(w: W.DecodeWorkload, k_new=None, v_new=None, oracle=True, 
     olay = O.make_layout(w.num_blocks, w.num_layers, w.layer, w.hkv, w.block_size, w.head_dim)
     ref = O.paged_decode_f64(host_array(t["q"]), host_array(kp2), host_array(vp2), olay,
                              w.block_tables, np.minimum(w.context_lens, max_ctx), scale=scale,
-                             window_left=w.window_left, dtype=oracle_dtype(t["q"]))
+                             window_left=w.window_left, dtype=oracle_dtype(t["q"]),
+                             softcap=softcap)
     assert_attention_close(as_f64(out2), ref, w.dtype, w.name)
     return t, out2
 

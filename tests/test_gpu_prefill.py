@@ -20,7 +20,7 @@ def _rand(g, *shape, dt):
     return torch.randn(*shape, generator=g, device="cuda", dtype=torch.float32).to(dt)
 
 
-def _oracle_varlen(q, k, v, cu_q, cu_k, scale, causal_mode, window):
+def _oracle_varlen(q, k, v, cu_q, cu_k, scale, causal_mode, window, softcap=0.0):
     """Per-sequence f64 oracle over packed q [Tq, Hq, D], k/v [Tk, Hkv, D] (host arrays)."""
     out = np.zeros(q.shape, dtype=np.float64)
     dt = O.BF16 if q.dtype == np.uint16 else O.F32
@@ -32,7 +32,7 @@ def _oracle_varlen(q, k, v, cu_q, cu_k, scale, causal_mode, window):
         causal = causal_mode != sp.SP_CAUSAL_NONE
         pos0 = 0 if causal_mode == sp.SP_CAUSAL_TOP_LEFT else lk - lq
         out[qa:qb] = O.attention_f64(q[qa:qb], k[ka:kb], v[ka:kb], scale=scale, causal=causal,
-                                     q_pos0=pos0, window_left=window, dtype=dt)
+                                     q_pos0=pos0, window_left=window, dtype=dt, softcap=softcap)
     return out
 
 
@@ -41,10 +41,12 @@ def _as_f64(t):
 
 
 def run_varlen(lens_q, lens_k, hq, hkv, d, dtype, causal, window, seed, inputs=None,
-               f32_bar="abs"):
+               f32_bar="abs", softcap=0.0, qscale=1.0):
     """f32_bar: "abs" checks f32 outputs at 1e-5 per row against the f64 oracle; "refops" (for
     inputs whose scores are so large that fp32 rounding of the scores alone exceeds that) bounds
-    the worst and mean row error by twice those of the reference's own f32 op order."""
+    the worst and mean row error by twice those of the reference's own f32 op order.
+    softcap: the logit soft cap (sp_varlen_prefill_softcap); qscale multiplies q (in its dtype)
+    so that the logits reach the cap. Returns the oracle's output."""
     g = torch.Generator(device="cuda").manual_seed(seed)
     dt = DT[dtype]
     cu_q = np.concatenate([[0], np.cumsum(lens_q)]).astype(np.int32)
@@ -55,15 +57,19 @@ def run_varlen(lens_q, lens_k, hq, hkv, d, dtype, causal, window, seed, inputs=N
         v = _rand(g, int(cu_k[-1]), hkv, d, dt=dt)
     else:
         q, k, v = (x.to(device="cuda", dtype=dt) for x in inputs(cu_q, cu_k))
+    if qscale != 1.0:
+        q.mul_(qscale)
     out = torch.full_like(q, float("nan"))
     announce(f"varlen prefill lens_q={list(lens_q)} lens_k={list(lens_k)} hq={hq} hkv={hkv} "
-             f"d={d} {dtype} causal={causal} window={window}")
+             f"d={d} {dtype} causal={causal} window={window} softcap={softcap}")
     sp.varlen_prefill(out, q, k, v, torch.from_numpy(cu_q).cuda(), torch.from_numpy(cu_k).cuda(),
-                      int(max(lens_q)), d ** -0.5, causal=causal, window_left=window)
+                      int(max(lens_q)), d ** -0.5, causal=causal, window_left=window,
+                      softcap=softcap)
     torch.cuda.synchronize()
     # the oracle reads 16-bit tensors as bf16 bits; f16 inputs are handed over as float32
     to_host = host_array if dtype == "bf16" else (lambda t: t.float().cpu().numpy())
-    ref = _oracle_varlen(to_host(q), to_host(k), to_host(v), cu_q, cu_k, d ** -0.5, causal, window)
+    ref = _oracle_varlen(to_host(q), to_host(k), to_host(v), cu_q, cu_k, d ** -0.5, causal, window,
+                         softcap)
     if dtype == "f32" and f32_bar == "refops":
         got = _as_f64(out)
         r32 = np.zeros_like(ref)
@@ -87,6 +93,7 @@ def run_varlen(lens_q, lens_k, hq, hkv, d, dtype, causal, window, seed, inputs=N
             f"f32 mean row {ours.mean():.3e} vs reference op order {theirs.mean():.3e}")
         return
     assert_attention_close(_as_f64(out), ref, dtype, "varlen prefill")
+    return ref
 
 
 @pytest.mark.parametrize("dtype", ["bf16", "f16"])
@@ -267,12 +274,16 @@ def test_flash_attention_dense(causal, sq, sk):
     assert_attention_close(_as_f64(out), ref, "bf16", "flash_attention")
 
 
-def run_chunked(w: W.ChunkedPrefillWorkload, sample_rows=None, split=False, shift=None):
+def run_chunked(w: W.ChunkedPrefillWorkload, sample_rows=None, split=False, shift=None,
+                softcap=0.0, qscale=1.0):
     """split: hand sp_paged_prefill the workspace it asks for, so long contexts are split over
     several workgroups per query block (the test asserts that a split is planned).
     shift: (q_mean, k_mean) moves q and every cached / new key off N(0,1) (q = q_mean + x/2,
-    k = k_mean + x/2), so the scores sit far from zero."""
+    k = k_mean + x/2), so the scores sit far from zero.
+    softcap: the logit soft cap (sp_paged_prefill_softcap); qscale multiplies q."""
     t = W.make_chunked_tensors(w)
+    if qscale != 1.0:
+        t["q"].mul_(qscale)
     if shift is not None:
         qm, km = shift
         for name, m in (("q", qm), ("k_pool", km), ("k_new", km)):
@@ -284,11 +295,11 @@ def run_chunked(w: W.ChunkedPrefillWorkload, sample_rows=None, split=False, shif
                                               t["block_tables"].shape[1])
         assert ws is not None, "no key split planned for this shape"
     announce(f"chunked prefill {w.name} chunks={list(w.chunk_lens)} ctx={list(w.ctx_before)} "
-             f"workspace={0 if ws is None else ws.numel()}")
+             f"workspace={0 if ws is None else ws.numel()} softcap={softcap}")
     sp.kv_append(t["k_pool"], t["v_pool"], lay, t["k_new"], t["v_new"], t["slot_mapping"])
     sp.paged_prefill(t["out"], t["q"], t["k_pool"], t["v_pool"], lay, t["block_tables"],
                      t["cu_seqlens_q"], t["context_lens"], w.max_seqlen_q, w.head_dim ** -0.5,
-                     window_left=w.window_left, workspace=ws)
+                     window_left=w.window_left, workspace=ws, softcap=softcap)
     torch.cuda.synchronize()
     olay = O.make_layout(t["num_blocks"], 1, 0, w.hkv, w.block_size, w.head_dim)
     kp, vp, q = host_array(t["k_pool"]), host_array(t["v_pool"]), host_array(t["q"])
@@ -307,7 +318,7 @@ def run_chunked(w: W.ChunkedPrefillWorkload, sample_rows=None, split=False, shif
         # the chunk's queries sit at positions L - lq .. L - 1 (prefill_causal_mask)
         ref = O.attention_f64(q[cu[s]:cu[s] + lq], kt[:L], vt[:L], scale=w.head_dim ** -0.5,
                               causal=True, q_pos0=L - lq, window_left=w.window_left,
-                              dtype=oracle_dtype(t["q"]))
+                              dtype=oracle_dtype(t["q"]), softcap=softcap)
         assert_attention_close(got[cu[s] + rows], ref[rows], w.dtype, f"{w.name} seq {s}")
     return t
 

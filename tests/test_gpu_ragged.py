@@ -17,8 +17,11 @@ from tests.helpers import announce, as_f64, assert_attention_close, host_array, 
 pytestmark = pytest.mark.gpu
 
 
-def _run(w: W.MixedWorkload, window_left: int = -1, repeats: int = 1):
+def _run(w: W.MixedWorkload, window_left: int = -1, repeats: int = 1, softcap: float = 0.0,
+         qscale: float = 1.0):
     t = W.make_mixed_tensors(w)
+    if qscale != 1.0:
+        t["q"].mul_(qscale)
     lay = sp.layout(t["num_blocks"], 1, 0, w.hkv, w.block_size, w.head_dim)
     P, T0 = w.num_prefill_seqs, w.num_prefill_tokens
     pmax = int(w.chunk_lens.max()) if P else 0
@@ -26,7 +29,7 @@ def _run(w: W.MixedWorkload, window_left: int = -1, repeats: int = 1):
     mb = t["block_tables"].shape[1]
     ws = sp.alloc_ragged_workspace(w.num_seqs, P, pmax, dmax, w.hq, lay, mb, window_left)
     announce(f"ragged {w.name}: {P} chunks {list(w.chunk_lens)} on {list(w.ctx_before)}, "
-             f"{w.num_decode_seqs} decode seqs, window {window_left}")
+             f"{w.num_decode_seqs} decode seqs, window {window_left}, softcap {softcap}")
     sp.kv_append(t["k_pool"], t["v_pool"], lay, t["k_new"], t["v_new"], t["slot_mapping"])
     scale = w.head_dim ** -0.5
     first = None
@@ -36,7 +39,8 @@ def _run(w: W.MixedWorkload, window_left: int = -1, repeats: int = 1):
                                   t["block_tables"], t["cu_seqlens_q"], t["context_lens"],
                                   num_prefill_seqs=P, num_prefill_tokens=T0,
                                   prefill_max_seqlen_q=pmax, decode_max_context_len=dmax,
-                                  scale=scale, window_left=window_left, workspace=ws)
+                                  scale=scale, window_left=window_left, workspace=ws,
+                                  softcap=softcap)
         if r == 0:
             first = t["out"].clone()
         else:
@@ -47,13 +51,13 @@ def _run(w: W.MixedWorkload, window_left: int = -1, repeats: int = 1):
         pws = sp.alloc_paged_prefill_workspace(P, pmax, w.hq, lay, mb)
         sp.paged_prefill(pre, t["q"][:T0], t["k_pool"], t["v_pool"], lay, t["block_tables"][:P],
                          t["cu_seqlens_q"], t["context_lens"][:P], pmax, scale,
-                         window_left=window_left, workspace=pws)
+                         window_left=window_left, workspace=pws, softcap=softcap)
     if w.num_decode_seqs:
         dec = torch.full_like(t["q"][T0:], float("nan"))
         dws = sp.alloc_decode_workspace(w.num_decode_seqs, w.hq, dmax, window_left, lay)
         sp.paged_decode(dec, t["q"][T0:], t["k_pool"], t["v_pool"], lay, t["block_tables"][P:],
                         t["context_lens"][P:], dmax, scale, window_left=window_left,
-                        workspace=dws)
+                        workspace=dws, softcap=softcap)
     torch.cuda.synchronize()
     if P:
         assert torch.equal(t["out"][:T0], pre), "chunk rows differ from sp_paged_prefill"
@@ -69,7 +73,7 @@ def _run(w: W.MixedWorkload, window_left: int = -1, repeats: int = 1):
     # decode rows: every sequence, every head
     if w.num_decode_seqs:
         ref = O.paged_decode_f64(q[T0:], kp, vp, olay, tables[P:], lens[P:], scale=scale,
-                                 window_left=window_left, dtype=odt)
+                                 window_left=window_left, dtype=odt, softcap=softcap)
         assert_attention_close(got[T0:], ref, w.dtype, f"{w.name} decode rows")
     # chunk rows: every row of every chunk (queries at positions L - lq .. L - 1)
     cu = w.cu_seqlens_q
@@ -79,7 +83,7 @@ def _run(w: W.MixedWorkload, window_left: int = -1, repeats: int = 1):
         kt = np.ascontiguousarray(kg.transpose(1, 0, 2))
         vt = np.ascontiguousarray(vg.transpose(1, 0, 2))
         r = O.attention_f64(q[cu[s]:cu[s] + lq], kt, vt, scale=scale, causal=True,
-                            q_pos0=L - lq, window_left=window_left, dtype=odt)
+                            q_pos0=L - lq, window_left=window_left, dtype=odt, softcap=softcap)
         assert_attention_close(got[cu[s]:cu[s] + lq], r, w.dtype, f"{w.name} chunk {s}")
 
 
