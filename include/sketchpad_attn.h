@@ -397,7 +397,8 @@ int sp_ragged_paged_attention_softcap(void* out, const void* q,
  * f32 tensors (the element type the reference's flash_attention runs, attention.rs:21-25):
  * head_dim 40, 64, 80, 128, 160 or 256 (so the SD-1.x UNet's head dims 40 / 80 / 160 run
  * without padding, sketchpad-unet/src/cubecl.rs:256-316), v_head_dim a multiple of 4 up to
- * 256. bf16 / f16 tensors: head_dim == v_head_dim, 64 or 128. out_dtype any of f32 / bf16 / f16.
+ * 256. bf16 / f16 tensors: head_dim == v_head_dim, 64, 128 or 256. out_dtype any of f32 / bf16 /
+ * f16.
  * The reference scales by head_dim^-0.5.
  */
 int sp_flash_attention_ex(void* out, const void* q, const void* k, const void* v,
