@@ -11,14 +11,18 @@
 // GQA group (up to 16) ride in the N = 16 columns of the MFMA tiles, so each K/V byte is read
 // from HBM once. Per tile, per wave:
 //   S^T[16 tok, 16 heads]  = K[16 tok, D] . Q^T[D, 16 heads]     MFMA 16x16x32 (16-bit) / 16x16x4 (f32)
-//     K is the A operand loaded straight from the pool: lane (g, n) loads 16 bytes of token n,
-//     so no LDS trip for K. Lane (g, n) then holds scores of tokens 4g..4g+3 for head n.
+//     16-bit: the tile's K and V rows are loaded lane-linear (coalesced 16-byte chunks) and
+//     staged in the wave's LDS with an XOR chunk swizzle; the K operand of lane (g, n) is read
+//     back as 16 bytes of token n. f32: K is the A operand loaded straight from the pool (lane
+//     (g, n) loads 16 bytes of token n). Lane (g, n) then holds scores of tokens 4g..4g+3 for
+//     head n.
 //   online softmax per head column (two cross-row shuffles per tile), fp32.
 //   O^T[D, 16 heads]     += V^T[D, 16 tok] . P^T[16 tok, 16 heads] MFMA 16x16x16 / 16x16x4
-//     The score registers are already the B-operand layout of P^T; V is staged in LDS with
-//     coalesced 16-byte stores and read back column-wise (padded pitch, conflict-free).
-// The next tile's loads are issued as soon as the current K has entered the MFMAs and V is in
-// LDS, so they stay in flight through the softmax and PV of the current tile.
+//     The score registers are already the B-operand layout of P^T; V^T comes from the stage by
+//     transpose reads (ds_read_b64_tr_b16; f32: a padded pitch read column-wise).
+// The next tile's loads are issued as soon as the current tile is in LDS (f32: as soon as K has
+// entered the MFMAs and V is in LDS), so they stay in flight through the MFMAs and softmax of
+// the current tile.
 // sp_paged_append_decode runs the step's append in the same launch: the last split of each
 // (sequence, KV head) unit stores the new token's rows (store_kv, paged_attention.rs:230-310)
 // and reads them from the input rather than the pool.
