@@ -1,13 +1,13 @@
-"""Build the gfx950 attention library and its checkers, in-tree.
+"""Build the gfx950 attention library and the C++ host mirror, in-tree.
 
-    python -m sketchpad_amd.build            # everything
+    python -m sketchpad_amd.build            # both
     python -m sketchpad_amd.build --lib      # only libsketchpad_attn.so
 
 Outputs (git-ignored, but shipped with the tree to the GPU box):
     sketchpad_amd/lib/libsketchpad_attn.so   C-ABI kernels (include/sketchpad_attn.h)
     sketchpad_amd/lib/libsketchpad_host.so   C++ mirror of the reference's paged-cache API
-    tests/cpp/build/test_paged_attention     C++ tests of the mirror
-    oracle/build/libsp_oracle.so             CPU oracle (built by oracle/build.sh)
+The checkers (the CPU oracle and the C++ tests of the mirror) are built by
+tests/build_checkers.py; __graft_entry__.build() builds everything.
 """
 from __future__ import annotations
 
@@ -87,29 +87,12 @@ def build_host(jobs: int = 8) -> Path | None:
     _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs),
           f"-L{LIBDIR}", "-lsketchpad_attn", "-Wl,-rpath,$ORIGIN", "-o", str(tmp)])
     tmp.replace(out)
-    test_srcs = [ROOT / "tests" / "cpp" / s for s in ("test_paged_attention.cpp",
-                                                       "test_batching.cpp")]
-    if all(p.exists() for p in test_srcs):
-        exe = ROOT / "tests" / "cpp" / "build" / "test_paged_attention"
-        exe.parent.mkdir(parents=True, exist_ok=True)
-        _run([HIPCC, *DEVICE_FLAGS, f"-I{HOST}", "-x", "hip", *map(str, test_srcs), "-o", str(exe),
-              f"-L{LIBDIR}", "-lsketchpad_host", "-lsketchpad_attn",
-              "-Wl,-rpath,$ORIGIN/../../../sketchpad_amd/lib"])
     return out
-
-
-def build_oracle() -> Path | None:
-    script = ROOT / "oracle" / "build.sh"
-    if not script.exists():
-        return None
-    _run(["bash", str(script)])
-    return ROOT / "oracle" / "build" / "libsp_oracle.so"
 
 
 def build_all(jobs: int = 8) -> None:
     build_lib(jobs)
     build_host(jobs)
-    build_oracle()
 
 
 def main() -> None:

@@ -6,8 +6,8 @@
 //     mixed batches that run chunked prefill and decode side by side), and
 //   - a multi-layer step through one interleaved-layer pool (run_batched_step: every layer
 //     appends at the same positions, the lengths advance once per step),
-// whose every attention output is compared with a float64 host computation over the sequence's
-// own history.
+// whose every attention output is compared with the f64 oracle's attention (test infrastructure,
+// oracle/) over the sequence's own history.
 #include <math.h>
 #include <string.h>
 
@@ -17,6 +17,7 @@
 #include <random>
 
 #include "ragged_batch.hpp"
+#include "sp_oracle.h"
 #include "test_harness.hpp"
 
 using namespace sketchpad;
@@ -143,11 +144,15 @@ struct LayerInputs {
 };
 
 // Appends the batch's new rows to each sequence's history, then checks every output row against
-// float64 attention over the history up to the row's position (no mask for one new token, the
-// causal rule inside a chunk), GQA head h -> KV head h / (hq / hkv). Returns the worst |error|.
+// the f64 oracle's attention (spo_attention_f64, oracle/sp_oracle.c, pinned by tests/test_oracle*.py)
+// over the history up to the row's position: no mask for one new token, the causal rule inside a
+// chunk (the row sees keys 0 .. pos), GQA head h -> KV head h / (hq / hkv). Returns the worst
+// |error|.
 double check_layer(const RaggedBatch& b, const LayerInputs& in, const std::vector<uint16_t>& oh,
                    std::map<size_t, History>& hist, int hq, int hkv, int d, float scale) {
   double worst = 0.0;
+  std::vector<float> q1((size_t)hq * d);
+  std::vector<double> o1((size_t)hq * d);
   for (size_t s = 0; s < b.num_seqs(); ++s) {
     History& H = hist[b.seq_ids[s]];
     for (int t = b.cu_seqlens_q[s]; t < b.cu_seqlens_q[s + 1]; ++t)
@@ -156,27 +161,13 @@ double check_layer(const RaggedBatch& b, const LayerInputs& in, const std::vecto
         H.v.push_back(bf16_value(in.vh[(size_t)t * hkv * d + x]));
       }
     for (int t = b.cu_seqlens_q[s]; t < b.cu_seqlens_q[s + 1]; ++t) {
-      const size_t pos = (size_t)b.positions[t];
-      for (int h = 0; h < hq; ++h) {
-        const int g = h / (hq / hkv);
-        std::vector<double> sc(pos + 1);
-        double mx = -1e300;
-        for (size_t j = 0; j <= pos; ++j) {
-          double acc = 0;
-          for (int e = 0; e < d; ++e)
-            acc += (double)bf16_value(in.qh[((size_t)t * hq + h) * d + e]) *
-                   H.k[(j * hkv + g) * d + e];
-          sc[j] = acc * scale;
-          mx = std::max(mx, sc[j]);
-        }
-        double den = 0;
-        for (auto& x : sc) den += (x = exp(x - mx));
-        for (int e = 0; e < d; ++e) {
-          double num = 0;
-          for (size_t j = 0; j <= pos; ++j) num += sc[j] * H.v[(j * hkv + g) * d + e];
-          worst = std::max(worst, fabs(num / den - bf16_value(oh[((size_t)t * hq + h) * d + e])));
-        }
-      }
+      const int64_t pos = b.positions[t];
+      for (int x = 0; x < hq * d; ++x) q1[x] = bf16_value(in.qh[(size_t)t * hq * d + x]);
+      // one query row [1, hq, d] against keys [pos + 1, hkv, d], all visible
+      spo_attention_f64(q1.data(), (int64_t)hq * d, d, H.k.data(), H.v.data(), (int64_t)hkv * d,
+                        d, 1, pos + 1, hq, hkv, d, scale, nullptr, 0, 0, -1, SPO_F32, o1.data());
+      for (int x = 0; x < hq * d; ++x)
+        worst = std::max(worst, fabs(o1[x] - bf16_value(oh[(size_t)t * hq * d + x])));
     }
   }
   return worst;
