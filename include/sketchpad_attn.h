@@ -180,9 +180,9 @@ size_t sp_paged_decode_workspace_size(int32_t num_seqs, int32_t num_q_heads,
  *   workspace      : device scratch of at least sp_paged_decode_workspace_size() bytes (no
  *                    initialisation needed). Calls that share a workspace must not overlap.
  * Softmax and accumulation are fp32 for every dtype. GQA groups (Hq / Hkv) up to 16, head_dim
- * 64 or 128 (and 256 for bf16 / f16: Gemma-4's sliding layers, gemma4.rs:94-102), block_size a
- * multiple of 16 or one of 1, 2, 4, 8 (a 16-token tile then spans several blocks, each row read
- * from the block its position maps to).
+ * 64 or 128 (and 256 for bf16 / f16: Gemma-4's sliding layers, gemma4.rs:94-102), any block_size
+ * (BlockTable takes any, paged_attention.rs:89-148; one that is not a multiple of 16 makes a
+ * 16-token tile span several blocks, each row read from the block its position maps to).
  */
 int sp_paged_decode(void* out, const void* q,
                     const void* k_pool, const void* v_pool, const sp_cache_layout* layout,

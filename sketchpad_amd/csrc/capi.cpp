@@ -261,13 +261,11 @@ static int decode_setup(const char* fn, void* out, const void* q, const void* k_
   const DecodePlan p =
       plan_decode(num_seqs, num_q_heads, hkv, D, max_context_len < 1 ? 1 : max_context_len,
                   window_left, kind);
-  // dense pools: block sizes that are multiples of the tile or divide it (a tile then spans
-  // several blocks); PolarQuant pools: multiples of the tile
-  const bool sub_tile = kind == DecodeKind::Dense && layout->block_size < p.tt &&
-                        p.tt % layout->block_size == 0;
-  if (layout->block_size % p.tt != 0 && !sub_tile)
+  // dense pools: any block size (one that is not a multiple of the tile takes the per-row path,
+  // where a tile spans several blocks); PolarQuant pools: multiples of the tile
+  if (kind != DecodeKind::Dense && layout->block_size % p.tt != 0)
     return fail(SP_EUNSUPPORTED,
-                "%s: block_size %d neither divides nor is a multiple of the %d-token tile", fn,
+                "%s: block_size %d is not a multiple of the %d-token tile of PolarQuant pools", fn,
                 layout->block_size, p.tt);
   if (p.ws_bytes > 0 && (!workspace || workspace_bytes < p.ws_bytes))
     return fail(SP_ENOSPACE, "%s: workspace of %zu bytes, %zu required", fn, workspace_bytes,

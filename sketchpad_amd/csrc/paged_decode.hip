@@ -163,8 +163,9 @@ constexpr int decode_min_waves() {
   return Elem<T>::bytes == 4 ? 1 : (D == 256 ? 2 : (SUB ? 3 : 4));
 }
 
-// SUB: block sizes below the 16-token tile (1, 2, 4 or 8, dividing it), so that a tile spans
-// several blocks; every row of a tile then takes the block its position maps to.
+// SUB: block sizes that are not multiples of the 16-token tile (1-15, 24, 40, ...), so that a
+// tile spans several blocks or straddles a block edge; every row of a tile then takes the block
+// its position maps to.
 // CAP: the logit soft cap (a.cap_in / a.cap_out), instantiated for head_dim 256.
 template <typename T, int D, bool SUB, bool CAP = false>
 __global__ void __launch_bounds__(64 * kDecodeWaves, (decode_min_waves<T, D, SUB>()))
@@ -261,8 +262,6 @@ __global__ void __launch_bounds__(64 * kDecodeWaves, (decode_min_waves<T, D, SUB
     if (lane < n_tiles) blk0 = table[((t_begin + lane) * kTile) / a.block_size];
     if (lane + 64 < n_tiles) blk1 = table[((t_begin + 64 + lane) * kTile) / a.block_size];
   }
-  // SUB: the tile's rows lie in kTile / block_size blocks (block_size a power of two)
-  const int bs_shift = SUB ? 31 - __builtin_clz(a.block_size) : 0;
 
   // Tile loads. K in MFMA A-operand order (token n, 16 bytes at c*64 + g*16); V coalesced
   // (lane-linear 16-byte chunks of the contiguous 16 x RB tile). Rows outside [start_tok, L)
@@ -318,21 +317,26 @@ __global__ void __launch_bounds__(64 * kDecodeWaves, (decode_min_waves<T, D, SUB
       vr[i] = ldnt(a.vpool + base + o);
     }
   };
-  // SUB: the rows of one tile lie in kTile / block_size blocks. Lane r < 16 reads the block id
-  // of row r (ok: bit r set when that block lies in the pool), and each load takes its row's
-  // block through a lane shuffle (every lane takes part in it).
+  // SUB: the rows of one tile lie in several blocks. Lane r < 16 reads the block id of row r
+  // (ok: bit r set when that block lies in the pool) and works out the row's byte offset in the
+  // pool once; each load takes its row's offset through a lane shuffle (every lane takes part).
+  const unsigned bsz = (unsigned)a.block_size;
   auto load_tile_sub = [&](int t, uint4* kr, uint4* vr, uint32_t& okm) {
     const int pos0 = t * kTile;
     const int rlo = max(start_tok - pos0, 0), rhi = min(L - pos0, kTile) - 1;  // valid rows
+    const unsigned p = (unsigned)min(pos0 + (lane & (kTile - 1)), L - 1);
+    const unsigned bi = p / bsz;
     int rblk = 0;
-    if (lane < kTile) rblk = table[min(pos0 + lane, L - 1) >> bs_shift];
+    if (lane < kTile) rblk = table[bi];
     const bool okr = rblk >= 0 && rblk < a.num_blocks;
     okm = (uint32_t)__builtin_amdgcn_ballot_w64(okr) & 0xFFFFu;
     rblk = okr ? rblk : 0;
+    const int64_t roff =
+        (int64_t)rblk * a.block_stride_b + head_off + (int64_t)(p - bi * bsz) * RB;
     auto row_off = [&](int r) -> int64_t {
-      const int b = __shfl(rblk, r, 64);
-      return (int64_t)b * a.block_stride_b + head_off +
-             (int64_t)((pos0 + r) & (a.block_size - 1)) * RB;
+      const int lo = __shfl((int)(uint32_t)roff, r, 64);
+      const int hi = __shfl((int)(roff >> 32), r, 64);
+      return (int64_t)(((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo);
     };
     const bool has_new = knew_row && pos0 + kTile > L - 1;  // the fused append's token (row rhi)
     if constexpr (kF32) {
@@ -630,7 +634,7 @@ template <typename T, int D>
 static int launch_typed(const DecodeArgs& a, hipStream_t stream) {
   const dim3 grid(a.num_seqs * a.hkv, a.max_splits);
   const dim3 block(64 * kDecodeWaves);
-  const bool sub = a.block_size < kTile;
+  const bool sub = a.block_size % kTile != 0;
   if (a.cap_out > 0.f) {  // the host admits the soft cap at head_dim 256 only
     if constexpr (D == 256) {
       if (sub)

@@ -91,9 +91,8 @@ def test_decode_validation(sp_lib):
     _expect(_lib.SP_EOOB, call(_lay(), max_ctx=33), "exceeds the block tables")
     _expect(_lib.SP_EINVAL, call(_lay(), window=-2), "window_left")
     _expect(_lib.SP_EINVAL, call(_lay(), scale=float("inf")), "scale")
-    # block sizes must divide the 16-token tile or be multiples of it (8 and 32 run, 12 and 24 not)
-    _expect(_lib.SP_EUNSUPPORTED, call(_lay(block_size=12), mbs=4), "block_size 12")
-    _expect(_lib.SP_EUNSUPPORTED, call(_lay(block_size=24), mbs=4), "block_size 24")
+    # dense pools take any block size (the GPU tests run 1-8, 12, 16, 24, 32, 48); the PolarQuant
+    # pools' multiple-of-16 rule is checked in test_polar_pool_bytes_and_validation
     # a batch needing split-K partials refuses a missing workspace
     lay = _lay(num_blocks=4096)
     need = sp_lib.sp_paged_decode_workspace_size(3, 4, 4096, -1, ctypes.byref(lay))
@@ -179,6 +178,7 @@ def test_polar_pool_bytes_and_validation(sp_lib):
     _expect(_lib.SP_EUNSUPPORTED, call(_lay(), dtype=0), "bf16, f16")
     _expect(_lib.SP_EUNSUPPORTED, call(_lay(head_dim=96)), "head_dim 96")
     _expect(_lib.SP_EUNSUPPORTED, call(_lay(block_size=8), mbs=4), "block_size 8")
+    _expect(_lib.SP_EUNSUPPORTED, call(_lay(block_size=24), mbs=4), "block_size 24")
     _expect(_lib.SP_EINVAL, call(_lay(), hq=3), "multiple")
 
 

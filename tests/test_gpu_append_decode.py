@@ -131,10 +131,10 @@ def test_append_decode_context_past_max_context_len():
 
 
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
-@pytest.mark.parametrize("bs", [1, 4, 8])
-def test_append_decode_block_sizes_below_the_tile(dtype, bs):
-    """Tiles spanning several blocks: the new token's row comes from k_new / v_new whatever block
-    of its tile holds it."""
+@pytest.mark.parametrize("bs", [1, 4, 8, 12, 24])
+def test_append_decode_block_sizes_off_the_tile(dtype, bs):
+    """Tiles spanning several blocks or straddling a block edge: the new token's row comes from
+    k_new / v_new whatever block of its tile holds it."""
     fused_vs_separate(W.random_decode(seed=5500 + bs + len(dtype), num_seqs=6, hq=16, hkv=4,
                                       head_dim=128, block_size=bs, dtype=dtype, min_len=1,
                                       max_len=600))

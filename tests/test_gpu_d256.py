@@ -36,7 +36,7 @@ def test_d256_decode(dtype, window):
     check_decode(w)
 
 
-@pytest.mark.parametrize("bs", [8, 16])
+@pytest.mark.parametrize("bs", [8, 12, 16])
 def test_d256_append_decode(bs):
     fused_vs_separate(W.random_decode(seed=910 + bs, num_seqs=6, hq=HQ, hkv=HKV, head_dim=D,
                                       block_size=bs, dtype="bf16", min_len=1, max_len=2500,
@@ -52,7 +52,7 @@ def test_d256_varlen_prefill(dtype, window):
 
 
 @pytest.mark.parametrize("window", [-1, GEMMA_WINDOW - 1])
-@pytest.mark.parametrize("bs", [8, 16, 32])
+@pytest.mark.parametrize("bs", [8, 16, 24, 32])
 def test_d256_chunked_prefill(window, bs):
     w = W.ChunkedPrefillWorkload("d256-chunked", 930 + bs, np.array([1, 70, 300, 129], np.int32),
                                  np.array([0, 900, 2000, 40], np.int32), HQ, HKV, D, "bf16",

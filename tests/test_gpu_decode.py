@@ -114,32 +114,33 @@ def test_decode_block_size_32():
 
 @pytest.mark.parametrize("dtype", ["f32", "bf16", "f16"])
 @pytest.mark.parametrize("d", [64, 128])
-@pytest.mark.parametrize("bs", [1, 2, 4, 8])
-def test_decode_block_sizes_below_the_tile(dtype, d, bs):
-    """Block sizes that divide the 16-token tile (the reference's BlockTable takes any size; its
-    own test uses 4, paged_attention.rs:568-598): every tile then spans several blocks of a
-    shuffled table. Lengths cross many tile and block edges, and split the keys."""
+@pytest.mark.parametrize("bs", [1, 2, 3, 4, 8, 12, 24, 48])
+def test_decode_block_sizes_off_the_tile(dtype, d, bs):
+    """Block sizes that are not multiples of the 16-token tile (the reference's BlockTable takes
+    any size; its own test uses 4, paged_attention.rs:568-598): every tile then spans several
+    blocks of a shuffled table (1-12) or straddles a block edge (24, 48). Lengths cross many
+    tile and block edges, and split the keys."""
     w = W.random_decode(seed=600 + bs * 10 + d + len(dtype), num_seqs=6, hq=16, hkv=4,
                         head_dim=d, block_size=bs, dtype=dtype, min_len=1, max_len=1500)
     check(w)
 
 
-@pytest.mark.parametrize("bs", [4, 8])
-def test_decode_block_sizes_below_the_tile_window(bs):
+@pytest.mark.parametrize("bs", [4, 8, 12, 24])
+def test_decode_block_sizes_off_the_tile_window(bs):
     w = W.random_decode(seed=700 + bs, num_seqs=5, hq=32, hkv=8, head_dim=128, block_size=bs,
                         dtype="bf16", min_len=50, max_len=900, window_left=200)
     check(w)
 
 
-@pytest.mark.parametrize("bs", [4, 8])
-def test_decode_block_sizes_below_the_tile_out_of_pool_block(bs):
+@pytest.mark.parametrize("bs", [4, 8, 12])
+def test_decode_block_sizes_off_the_tile_out_of_pool_block(bs):
     """A block id outside the pool in the middle of a tile masks that block's rows only (the
     reference panics on such an id, "Block not allocated", paged_attention.rs:242; this build
     skips the rows): the output is attention over the sequence's other keys, computed here in
     float64 from the pool."""
     w = W.random_decode(seed=800 + bs, num_seqs=3, hq=8, hkv=2, head_dim=128, block_size=bs,
                         dtype="bf16", min_len=100, max_len=400)
-    bad = 16 // bs + 1  # the second block of the sequence's second tile
+    bad = 16 // bs + 1  # a block of the sequence's second tile (16 // bs + 1 = 2 at 12: keys 24-35)
     w.block_tables[1, bad] = -1
     announce(f"decode sub-tile blocks BS={bs} with block {bad} of sequence 1 outside the pool")
     t = run_step(w)

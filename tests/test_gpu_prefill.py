@@ -350,11 +350,12 @@ def test_paged_prefill_block_size_32():
     run_chunked(w)
 
 
-@pytest.mark.parametrize("d,bs", [(128, 4), (128, 8), (128, 64), (64, 4), (64, 8), (64, 64)])
+@pytest.mark.parametrize("d,bs", [(128, 4), (128, 8), (128, 64), (64, 4), (64, 8), (64, 64),
+                                  (128, 12), (128, 24), (64, 3), (64, 48)])
 def test_paged_prefill_block_sizes(d, bs):
     """Block sizes on every tile-load path: blocks holding whole groups of four 1 KiB loads (one
-    base per group), smaller blocks (one base per load) and blocks smaller than one load
-    (per-lane addresses)."""
+    base per group), smaller blocks (one base per load), blocks smaller than one load and block
+    sizes that do not divide the tile (per-lane addresses)."""
     w = W.ChunkedPrefillWorkload(f"chunked-d{d}-bs{bs}", 44 + bs + d, np.array([130, 61], np.int32),
                                  np.array([200, 7], np.int32), 8, 2, d, "bf16", block_size=bs)
     run_chunked(w)
