@@ -148,14 +148,18 @@ def test_ragged_decode_only_and_prefill_only():
     _run(only_pre)
 
 
-def test_ragged_mixed_graph_capture():
+@pytest.mark.parametrize("d,softcap", [(128, 0.0), (256, 50.0)])
+def test_ragged_mixed_graph_capture(d, softcap):
     """The mixed step's fork / join (decode on the library's side stream) captured into a HIP
     graph through torch: four replays, each after eager work that overwrites the output, each
-    bit-identical to the eager call."""
+    bit-identical to the eager call. Also at head dim 256 with Gemma-4's logit soft cap
+    (sp_ragged_paged_attention_softcap)."""
     w = W.MixedWorkload("mixed-graph", 81, np.array([64, 100], np.int32),
                         np.array([4000, 300], np.int32),
-                        np.array([3000, 17, 1500, 640], np.int32), 8, 2, 128, "bf16")
+                        np.array([3000, 17, 1500, 640], np.int32), 8, 2, d, "bf16")
     t = W.make_mixed_tensors(w)
+    if softcap:
+        t["q"].mul_(8.0)  # logits that reach the cap
     lay = sp.layout(t["num_blocks"], 1, 0, w.hkv, w.block_size, w.head_dim)
     P, T0 = w.num_prefill_seqs, w.num_prefill_tokens
     pmax, dmax = int(w.chunk_lens.max()), int(w.decode_lens.max())
@@ -168,9 +172,10 @@ def test_ragged_mixed_graph_capture():
                                   t["block_tables"], t["cu_seqlens_q"], t["context_lens"],
                                   num_prefill_seqs=P, num_prefill_tokens=T0,
                                   prefill_max_seqlen_q=pmax, decode_max_context_len=dmax,
-                                  scale=w.head_dim ** -0.5, workspace=ws, stream=stream)
+                                  scale=w.head_dim ** -0.5, workspace=ws, softcap=softcap,
+                                  stream=stream)
 
-    announce("ragged mixed step under graph capture")
+    announce(f"ragged mixed step under graph capture, D={d}, softcap={softcap}")
     call(torch.cuda.current_stream().cuda_stream)
     torch.cuda.synchronize()
     eager = t["out"].clone()
