@@ -249,10 +249,11 @@ static int decode_setup(const char* fn, void* out, const void* q, const void* k_
     return fail(SP_EUNSUPPORTED, "%s: GQA group %d > %d has no kernel", fn, group,
                 kDecodeMaxGroup);
   const int D = layout->head_dim;
-  const bool d256 = D == 256 && dtype != SP_F32 && kind == DecodeKind::Dense;
-  if (D != 64 && D != 128 && !d256)
+  const bool wide = (D == 256 || D == 512) && dtype != SP_F32 && kind == DecodeKind::Dense;
+  if (D != 64 && D != 128 && !wide)
     return fail(SP_EUNSUPPORTED,
-                "%s: head_dim %d has no kernel (64, 128; 256 for 16-bit dense pools)", fn, D);
+                "%s: head_dim %d has no kernel (64, 128; 256 and 512 for 16-bit dense pools)", fn,
+                D);
   if (window_left < -1) return fail(SP_EINVAL, "%s: window_left %d < -1", fn, window_left);
   if ((int64_t)max_context_len > (int64_t)max_blocks_per_seq * layout->block_size)
     return fail(SP_EOOB, "%s: max_context_len %d exceeds the block tables (%d blocks of %d)", fn,
@@ -298,8 +299,9 @@ static int decode_setup(const char* fn, void* out, const void* q, const void* k_
 
 // The logit soft cap of the *_softcap entry points (Gemma-4's attn_logit_softcap: logits =
 // cap * tanh(logits / cap) on the scaled product, before the mask, gemma4.rs:366-377). 0: none;
-// > 0 runs on the head-dim-256 bf16 / f16 kernels, which take it as cap_in = 2 log2(e) scale /
-// cap and cap_out = cap log2(e) (softcap_log2: the softmax's exponent units).
+// > 0 runs on the head-dim-256 and -512 bf16 / f16 kernels (Gemma-4's two head dims), which take
+// it as cap_in = 2 log2(e) scale / cap and cap_out = cap log2(e) (softcap_log2: the softmax's
+// exponent units).
 static int softcap_args(const char* fn, float softcap, float scale, int head_dim, sp_dtype dtype,
                         float* cap_in, float* cap_out) {
   *cap_in = *cap_out = 0.f;
@@ -307,10 +309,10 @@ static int softcap_args(const char* fn, float softcap, float scale, int head_dim
   if (!(softcap > 0.f) || !isfinite(softcap))
     return fail(SP_EINVAL, "%s: logit_softcap must be finite and >= 0 (got %g)", fn,
                 (double)softcap);
-  if (head_dim != 256 || dtype == SP_F32)
+  if ((head_dim != 256 && head_dim != 512) || dtype == SP_F32)
     return fail(SP_EUNSUPPORTED,
-                "%s: the logit soft cap runs at head_dim 256 on bf16 / f16 tensors (got head_dim "
-                "%d, %s)",
+                "%s: the logit soft cap runs at head_dims 256 and 512 on bf16 / f16 tensors (got "
+                "head_dim %d, %s)",
                 fn, head_dim, dtype_name(dtype));
   *cap_in = (float)(2.0 * 1.4426950408889634 * (double)scale / (double)softcap);
   *cap_out = (float)((double)softcap * 1.4426950408889634);

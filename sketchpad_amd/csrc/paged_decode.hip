@@ -7,9 +7,11 @@
 // over keys j in [start, L_s), start = 0 or L_s-1-window_left; fp32 softmax and accumulation.
 //
 // Work decomposition: one workgroup of four waves per (split, KV head, sequence); a split is
-// `tps` consecutive 16-token tiles and the waves take every fourth tile. All query heads of the
-// GQA group (up to 16) ride in the N = 16 columns of the MFMA tiles, so each K/V byte is read
-// from HBM once. Per tile, per wave:
+// `tps` consecutive 16-token tiles and the waves take every fourth tile (head_dim 512: the four
+// waves take every tile together, each a quarter of its dims, and add up their partial products
+// through LDS before one shared softmax). All query heads of the GQA group (up to 16) ride in
+// the N = 16 columns of the MFMA tiles, so each K/V byte is read from HBM once. Per tile, per
+// wave:
 //   S^T[16 tok, 16 heads]  = K[16 tok, D] . Q^T[D, 16 heads]     MFMA 16x16x32 (16-bit) / 16x16x4 (f32)
 //     16-bit: the tile's K and V rows are loaded lane-linear (coalesced 16-byte chunks) and
 //     staged in the wave's LDS with an XOR chunk swizzle; the K operand of lane (g, n) is read
@@ -136,15 +138,25 @@ struct DecodeCfg {
   static constexpr int ES = Elem<T>::bytes;
   static constexpr bool kF32 = (ES == 4);
   static constexpr int RB = D * ES;                    // bytes per K/V row
-  static constexpr int NL = RB / 64;                   // 16-byte loads per lane per tile (K or V)
+  // Head dim 512 (16-bit): the four waves of a workgroup share every tile, each taking a slice
+  // of D / 4 dims of its rows (one wave's registers cannot hold a whole row's Q, K, V and O);
+  // otherwise one slice, the whole row, and the waves take every fourth tile.
+  static constexpr int NSL = (D == 512) ? kDecodeWaves : 1;  // slices per row
+  static constexpr int SD = D / NSL;                   // dims of a wave's slice
+  static constexpr int SB = SD * ES;                   // bytes of a row's slice
+  static constexpr int NL = SB / 64;                   // 16-byte loads per lane per tile (K or V)
   static constexpr int VP = RB + (kF32 ? 16 : 0);      // f32: V staging pitch (new banks per row)
-  // 16-bit: K and V stages of 16 rows each, 16-byte chunks XOR-swizzled per row (swz below);
-  // f32: a padded V stage only (K is read from HBM straight into the MFMA operand).
-  static constexpr int WAVE_LDS = kF32 ? kTile * VP : 2 * kTile * RB;
-  static constexpr int CPR = RB / 16;                  // 16-byte chunks per row
-  static constexpr int ND = D / 16;                    // 16-dim output blocks
-  static constexpr int MERGE_LDS = kDecodeWaves * (2 * 16 + 16 * D) * 4;
-  static constexpr int LDS = (kDecodeWaves * WAVE_LDS > MERGE_LDS) ? kDecodeWaves * WAVE_LDS : MERGE_LDS;
+  // 16-bit: K and V stages of 16 rows (slices) each, 16-byte chunks XOR-swizzled per row (swz
+  // below); f32: a padded V stage only (K is read from HBM straight into the MFMA operand).
+  static constexpr int WAVE_LDS = kF32 ? kTile * VP : 2 * kTile * SB;
+  static constexpr int CPR = SB / 16;                  // 16-byte chunks per staged row
+  static constexpr int ND = SD / 16;                   // 16-dim output blocks of a wave
+  // the four waves' (m, l, O) merge; with slices the waves share one softmax and do not merge
+  static constexpr int MERGE_LDS = NSL > 1 ? 0 : kDecodeWaves * (2 * 16 + 16 * D) * 4;
+  // slices: each wave's partial products of a tile, [tile parity][wave][lane] x 4 floats
+  static constexpr int XCHG_LDS = NSL > 1 ? 2 * kDecodeWaves * 64 * 16 : 0;
+  static constexpr int STAGE_LDS = kDecodeWaves * WAVE_LDS + XCHG_LDS;
+  static constexpr int LDS = STAGE_LDS > MERGE_LDS ? STAGE_LDS : MERGE_LDS;
   // Chunk swizzle of the 16-bit stages: the K operand read (16 rows at one logical chunk) and
   // the V transpose read (8 consecutive rows x 32 bytes per 32 lanes) hit distinct banks.
   // (Rows of 32 chunks, D = 256, take the 16-chunk pattern: it only needs to separate the rows
@@ -157,7 +169,8 @@ struct DecodeCfg {
 typedef __attribute__((address_space(3))) s16x4_v lds_s16x4_v;
 
 // 16-bit kernels fit four waves per SIMD (<= 128 VGPRs, no spills), three for sub-tile blocks
-// and two at head_dim 256; f32 D=128 would spill.
+// and two at head_dim 256 (head_dim 512 holds a quarter row per wave, like 128); f32 D=128
+// would spill.
 template <typename T, int D, bool SUB>
 constexpr int decode_min_waves() {
   return Elem<T>::bytes == 4 ? 1 : (D == 256 ? 2 : (SUB ? 3 : 4));
@@ -166,14 +179,19 @@ constexpr int decode_min_waves() {
 // SUB: block sizes that are not multiples of the 16-token tile (1-15, 24, 40, ...), so that a
 // tile spans several blocks or straddles a block edge; every row of a tile then takes the block
 // its position maps to.
-// CAP: the logit soft cap (a.cap_in / a.cap_out), instantiated for head_dim 256.
+// CAP: the logit soft cap (a.cap_in / a.cap_out), instantiated for head_dims 256 and 512.
 template <typename T, int D, bool SUB, bool CAP = false>
 __global__ void __launch_bounds__(64 * kDecodeWaves, (decode_min_waves<T, D, SUB>()))
     paged_decode_kernel(DecodeArgs a) {
   using C = DecodeCfg<T, D>;
-  constexpr int ES = C::ES, RB = C::RB, NL = C::NL, VP = C::VP, ND = C::ND;
+  constexpr int ES = C::ES, RB = C::RB, SD = C::SD, SB = C::SB, NL = C::NL, VP = C::VP;
+  constexpr int ND = C::ND;
   constexpr bool kF32 = C::kF32;
-  static_assert(RB % 64 == 0, "row must split into 64-byte MFMA K chunks");
+  constexpr bool kSlices = C::NSL > 1;
+  static_assert(SB % 64 == 0, "a slice must split into 64-byte MFMA K chunks");
+  static_assert(!kSlices || !kF32, "dim slices are for 16-bit pools");
+  // the waves' tile order: every fourth tile each, or (slices) every tile together
+  constexpr int kStep = kSlices ? 1 : kDecodeWaves;
 
   __shared__ __attribute__((aligned(16))) char smem[C::LDS];
 
@@ -187,6 +205,7 @@ __global__ void __launch_bounds__(64 * kDecodeWaves, (decode_min_waves<T, D, SUB
   const int unit = blockIdx.x, split = blockIdx.y;
   const int seq = unit / a.hkv, kvh = unit - seq * a.hkv;
   const int G = a.group;
+  const int slice_b = kSlices ? wave * SB : 0;  // byte offset of this wave's slice in a row
 
   const int L_raw = a.context_lens[seq];
   const int L = min(L_raw, min(a.max_context_len, a.max_blocks_per_seq * a.block_size));
@@ -207,11 +226,13 @@ __global__ void __launch_bounds__(64 * kDecodeWaves, (decode_min_waves<T, D, SUB
   const int t_begin = first_tile + split * a.tps;
   const int t_end = min(t_begin + a.tps, last_tile + 1);
 
-  // Q^T operand: lane (g, n) holds head n's bytes [c*64 + g*16, +16) for every chunk c.
+  // Q^T operand: lane (g, n) holds head n's bytes [c*64 + g*16, +16) of the slice for every
+  // chunk c.
   uint4 qv[NL];
   {
     const bool real = n < G;
-    const char* qp = (const char*)a.q + ((int64_t)seq * a.hq + kvh * G + (real ? n : 0)) * RB;
+    const char* qp =
+        (const char*)a.q + ((int64_t)seq * a.hq + kvh * G + (real ? n : 0)) * RB + slice_b;
 #pragma unroll
     for (int c = 0; c < NL; ++c) {
       const uint4 x = *(const uint4*)(qp + c * 64 + g * 16);  // padding heads read head 0
@@ -295,11 +316,12 @@ __global__ void __launch_bounds__(64 * kDecodeWaves, (decode_min_waves<T, D, SUB
 #pragma unroll
       for (int i = 0; i < NL; ++i) {
         const int off = (i * 64 + lane) * 16;
-        const int row = min(max(off / RB, rlo), rhi);
+        const int row = min(max(off / SB, rlo), rhi);
         const bool nw = row == rhi;
-        const int o = row * RB + off % RB;
-        if constexpr (!kF32) kr[i] = ldnt(nw ? knew_row + off % RB : a.kpool + base + o);
-        vr[i] = ldnt(nw ? vnew_row + off % RB : a.vpool + base + o);
+        const int so = slice_b + off % SB;  // byte of the row
+        const int o = row * RB + so;
+        if constexpr (!kF32) kr[i] = ldnt(nw ? knew_row + so : a.kpool + base + o);
+        vr[i] = ldnt(nw ? vnew_row + so : a.vpool + base + o);
       }
       return;
     }
@@ -311,8 +333,8 @@ __global__ void __launch_bounds__(64 * kDecodeWaves, (decode_min_waves<T, D, SUB
 #pragma unroll
     for (int i = 0; i < NL; ++i) {
       const int off = (i * 64 + lane) * 16;
-      const int row = off / RB;
-      const int o = min(max(row, rlo), rhi) * RB + off % RB;
+      const int row = off / SB;
+      const int o = min(max(row, rlo), rhi) * RB + slice_b + off % SB;
       if constexpr (!kF32) kr[i] = ldnt(a.kpool + base + o);  // coalesced, staged through LDS
       vr[i] = ldnt(a.vpool + base + o);
     }
@@ -349,11 +371,12 @@ __global__ void __launch_bounds__(64 * kDecodeWaves, (decode_min_waves<T, D, SUB
 #pragma unroll
     for (int i = 0; i < NL; ++i) {
       const int off = (i * 64 + lane) * 16;
-      const int row = min(max(off / RB, rlo), rhi);
-      const int64_t o = row_off(row) + off % RB;
+      const int row = min(max(off / SB, rlo), rhi);
+      const int so = slice_b + off % SB;  // byte of the row
+      const int64_t o = row_off(row) + so;
       const bool nw = has_new && row == rhi;
-      if constexpr (!kF32) kr[i] = ldnt(nw ? knew_row + off % RB : a.kpool + o);
-      vr[i] = ldnt(nw ? vnew_row + off % RB : a.vpool + o);
+      if constexpr (!kF32) kr[i] = ldnt(nw ? knew_row + so : a.kpool + o);
+      vr[i] = ldnt(nw ? vnew_row + so : a.vpool + o);
     }
   };
   auto load_tile = [&](int t, uint4* kr, uint4* vr, uint32_t& okm) {
@@ -368,9 +391,9 @@ __global__ void __launch_bounds__(64 * kDecodeWaves, (decode_min_waves<T, D, SUB
 
   uint4 kc[NL], vc[NL];
   uint32_t ok_c = 0;
-  int t = t_begin + wave;
+  int t = kSlices ? t_begin : t_begin + wave;
   if (t < t_end) load_tile(t, kc, vc, ok_c);
-  for (; t < t_end; t += kDecodeWaves) {
+  for (; t < t_end; t += kStep) {
     const uint32_t tile_ok = ok_c;
 
     f32x4_v s = {0.f, 0.f, 0.f, 0.f};
@@ -393,27 +416,41 @@ __global__ void __launch_bounds__(64 * kDecodeWaves, (decode_min_waves<T, D, SUB
       }
       // K went into the MFMAs and V into LDS: the registers take the next tile's loads, which
       // stay in flight through this tile's softmax and PV.
-      if (t + kDecodeWaves < t_end) load_tile(t + kDecodeWaves, kc, vc, ok_c);
+      if (t + kStep < t_end) load_tile(t + kStep, kc, vc, ok_c);
     } else {
-      // Stage K and V rows (lane-linear 16-byte chunks at swizzled chunk positions).
-      char* kst = vst + kTile * RB;
+      // Stage K and V rows (slices): lane-linear 16-byte chunks at swizzled chunk positions.
+      char* kst = vst + kTile * SB;
 #pragma unroll
       for (int i = 0; i < NL; ++i) {
         const int off = (i * 64 + lane) * 16;
-        const int row = off / RB, lc = (off % RB) / 16;
-        const int dst = row * RB + 16 * (lc ^ C::swz(row));
+        const int row = off / SB, lc = (off % SB) / 16;
+        const int dst = row * SB + 16 * (lc ^ C::swz(row));
         *(uint4*)(kst + dst) = kc[i];
         *(uint4*)(vst + dst) = vc[i];
       }
       wave_lds_sync();
       // both tiles are in LDS: the registers take the next tile's loads, which stay in flight
       // through this tile's MFMAs and softmax
-      if (t + kDecodeWaves < t_end) load_tile(t + kDecodeWaves, kc, vc, ok_c);
+      if (t + kStep < t_end) load_tile(t + kStep, kc, vc, ok_c);
       // S^T = K Q^T: the K operand of chunk c is row n, logical chunk 4c + g
       const int ksw = C::swz(n);
 #pragma unroll
       for (int c = 0; c < NL; ++c)
-        s = DecodeMfma<T>::qk(*(const uint4*)(kst + n * RB + 16 * ((4 * c + g) ^ ksw)), qv[c], s);
+        s = DecodeMfma<T>::qk(*(const uint4*)(kst + n * SB + 16 * ((4 * c + g) ^ ksw)), qv[c], s);
+      if constexpr (kSlices) {
+        // s holds the products over this wave's dims only: add up the four waves' partials, in
+        // the same order in every wave, so that all four hold the same scores (and from them
+        // the same softmax state). Two exchange buffers by tile parity: a wave writes tile t + 2's
+        // partials only after the barrier of tile t + 1, which every wave reaches after reading
+        // tile t's.
+        f32x4_v* xs = (f32x4_v*)(smem + kDecodeWaves * C::WAVE_LDS) +
+                      ((t - t_begin) & 1) * kDecodeWaves * 64;
+        xs[wave * 64 + lane] = s;
+        lds_barrier();
+        s = xs[lane];
+#pragma unroll
+        for (int w = 1; w < kDecodeWaves; ++w) s += xs[w * 64 + lane];
+      }
     }
 
     // Online softmax for head column n over tokens 4g..4g+3 of this tile.
@@ -462,7 +499,7 @@ __global__ void __launch_bounds__(64 * kDecodeWaves, (decode_min_waves<T, D, SUB
 #pragma unroll
       for (int db = 0; db < ND; ++db) {
         const int colb = (db * 16 + 4 * (n & 3)) * ES;
-        const char* ap = vst + vrow * RB + 16 * ((colb >> 4) ^ vsw) + (colb & 15);
+        const char* ap = vst + vrow * SB + 16 * ((colb >> 4) ^ vsw) + (colb & 15);
         const s16x4_v vop = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_v*)ap);
         acc[db] = DecodeMfma<T>::pv(__builtin_bit_cast(uint2, vop), pp, acc[db]);
       }
@@ -470,53 +507,84 @@ __global__ void __launch_bounds__(64 * kDecodeWaves, (decode_min_waves<T, D, SUB
     wave_lds_sync();  // reads done before the next tile overwrites the staging area
   }
 
-  // Per-head sums over the four token groups of the wave, then merge the four waves in LDS.
+  // Per-head sums over the four token groups of the wave, then (whole rows) merge the four waves
+  // in LDS.
   l_run += xor16(l_run);
   l_run += xor32(l_run);
-  __syncthreads();
-  float* cm = (float*)smem;             // [waves][16]
-  float* cl = cm + kDecodeWaves * 16;   // [waves][16]
-  float* ca = cl + kDecodeWaves * 16;   // [waves][16][D]
-  if (g == 0) {
-    cm[wave * 16 + n] = m_run;
-    cl[wave * 16 + n] = l_run;
-  }
-#pragma unroll
-  for (int db = 0; db < ND; ++db)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) ca[(wave * 16 + n) * D + db * 16 + 4 * g + r] = acc[db][r];
-  __syncthreads();
-
-  for (int i = threadIdx.x; i < G * D; i += blockDim.x) {
-    const int h = i / D, d = i % D;
-    float M = -INFINITY;
-#pragma unroll
-    for (int w = 0; w < kDecodeWaves; ++w) M = fmaxf(M, cm[w * 16 + h]);
-    float lsum = 0.f, asum = 0.f;
-    if (M != -INFINITY) {
-#pragma unroll
-      for (int w = 0; w < kDecodeWaves; ++w) {
-        const float mw = cm[w * 16 + h];
-        const float f = (mw == -INFINITY) ? 0.f : exp2f(mw - M);
-        lsum = fmaf(cl[w * 16 + h], f, lsum);
-        asum = fmaf(ca[(w * 16 + h) * D + d], f, asum);
-      }
-    }
-    const int hq = kvh * G + h;
+  if constexpr (kSlices) {
+    // The four waves hold the same softmax state and each the output of its own dims: no merge.
+    // Lane (g, n) holds O^T[dims SD wave + 16 db + 4g .. +3][head n].
+    if (n >= G) return;
+    const int hq = kvh * G + n;
+    const int d0 = SD * wave + 4 * g;
     if (nsplit == 1) {
-      Elem<T>::store(a.out, ((int64_t)seq * a.hq + hq) * D + d, lsum > 0.f ? asum / lsum : 0.f);
+      const float inv = l_run > 0.f ? 1.f / l_run : 0.f;
+      char* op = (char*)a.out + (((int64_t)seq * a.hq + hq) * D + d0) * ES;
+#pragma unroll
+      for (int db = 0; db < ND; ++db)
+        *(uint2*)(op + db * 16 * ES) =
+            make_uint2(DecodeMfma<T>::pack(acc[db][0] * inv, acc[db][1] * inv),
+                       DecodeMfma<T>::pack(acc[db][2] * inv, acc[db][3] * inv));
     } else {
       float* pp = a.partials + (((int64_t)seq * a.hq + hq) * a.max_splits + split) * (D + 4);
-      if (d == 0) {
-        pp[0] = M;
-        pp[1] = lsum;
+      if (wave == 0 && g == 0) {
+        pp[0] = m_run;
+        pp[1] = l_run;
       }
-      pp[4 + d] = asum;
+#pragma unroll
+      for (int db = 0; db < ND; ++db)
+        *(float4*)(pp + 4 + d0 + db * 16) =
+            make_float4(acc[db][0], acc[db][1], acc[db][2], acc[db][3]);
     }
-    // word 2 of split 0's record: the split count, read by the combine in the same round trip as
-    // the partials (1: the output is final)
-    if (split == 0 && d == 0 && a.max_splits > 1)
+    // word 2 of split 0's record: the split count, read by the combine (1: the output is final)
+    if (split == 0 && wave == 0 && g == 0 && a.max_splits > 1)
       a.partials[((int64_t)seq * a.hq + hq) * a.max_splits * (D + 4) + 2] = (float)nsplit;
+  } else {
+    __syncthreads();
+    float* cm = (float*)smem;             // [waves][16]
+    float* cl = cm + kDecodeWaves * 16;   // [waves][16]
+    float* ca = cl + kDecodeWaves * 16;   // [waves][16][D]
+    if (g == 0) {
+      cm[wave * 16 + n] = m_run;
+      cl[wave * 16 + n] = l_run;
+    }
+#pragma unroll
+    for (int db = 0; db < ND; ++db)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) ca[(wave * 16 + n) * D + db * 16 + 4 * g + r] = acc[db][r];
+    __syncthreads();
+
+    for (int i = threadIdx.x; i < G * D; i += blockDim.x) {
+      const int h = i / D, d = i % D;
+      float M = -INFINITY;
+#pragma unroll
+      for (int w = 0; w < kDecodeWaves; ++w) M = fmaxf(M, cm[w * 16 + h]);
+      float lsum = 0.f, asum = 0.f;
+      if (M != -INFINITY) {
+#pragma unroll
+        for (int w = 0; w < kDecodeWaves; ++w) {
+          const float mw = cm[w * 16 + h];
+          const float f = (mw == -INFINITY) ? 0.f : exp2f(mw - M);
+          lsum = fmaf(cl[w * 16 + h], f, lsum);
+          asum = fmaf(ca[(w * 16 + h) * D + d], f, asum);
+        }
+      }
+      const int hq = kvh * G + h;
+      if (nsplit == 1) {
+        Elem<T>::store(a.out, ((int64_t)seq * a.hq + hq) * D + d, lsum > 0.f ? asum / lsum : 0.f);
+      } else {
+        float* pp = a.partials + (((int64_t)seq * a.hq + hq) * a.max_splits + split) * (D + 4);
+        if (d == 0) {
+          pp[0] = M;
+          pp[1] = lsum;
+        }
+        pp[4 + d] = asum;
+      }
+      // word 2 of split 0's record: the split count, read by the combine in the same round trip as
+      // the partials (1: the output is final)
+      if (split == 0 && d == 0 && a.max_splits > 1)
+        a.partials[((int64_t)seq * a.hq + hq) * a.max_splits * (D + 4) + 2] = (float)nsplit;
+    }
   }
 }
 
@@ -588,9 +656,13 @@ DecodePlan plan_decode(int num_seqs, int hq, int hkv, int head_dim, int max_cont
   }
   p.max_tiles = max_tiles < 1 ? 1 : max_tiles;
   // Workgroups the batch launches with splits of t tiles if every sequence spanned max_tiles
-  // (the host does not read the context lengths).
+  // (the host does not read the context lengths). At head_dim 512 the four waves of a workgroup
+  // share each tile (a quarter of its dims each), so one tile is a whole-workgroup step, as four
+  // tiles are elsewhere: the rules below run on quarter tiles (qf) and the split is converted
+  // back at the end.
   const int64_t units = (int64_t)num_seqs * (hkv > 0 ? hkv : 1);
-  auto wgs = [&](int t) { return units * ((p.max_tiles + t - 1) / t); };
+  const int qf = (head_dim == 512 && kind == DecodeKind::Dense) ? kDecodeWaves : 1;
+  auto wgs = [&](int t) { return units * (((int64_t)p.max_tiles * qf + t - 1) / t); };
   int tps;
   if (kind == DecodeKind::Dense) {
     // A rule fitted to measurements (24 batches: groups 1-16, 64-1024 units, contexts of
@@ -611,9 +683,11 @@ DecodePlan plan_decode(int num_seqs, int hq, int hkv, int head_dim, int max_cont
       while (tps > kDecodeWaves && wgs(tps) < 512) tps /= 2;
     } else if (wgs(128) >= 384 && wgs(128) <= 512) {
       tps = 128;
-    } else if (p.group <= 4 && units >= 512 && p.max_tiles > 128 && p.max_tiles <= 256) {
+    } else if (p.group <= 4 && units >= 512 && p.max_tiles * qf > 128 &&
+               p.max_tiles * qf <= 256) {
       tps = 32;
     }
+    tps = tps / qf < 1 ? 1 : tps / qf;
   } else {
     // Compressed tiles are a quarter of a dense one's bytes: start from 64-tile splits and halve
     // while the batch launches fewer than 2048 workgroups, but not below 32 tiles once it
@@ -635,8 +709,8 @@ static int launch_typed(const DecodeArgs& a, hipStream_t stream) {
   const dim3 grid(a.num_seqs * a.hkv, a.max_splits);
   const dim3 block(64 * kDecodeWaves);
   const bool sub = a.block_size % kTile != 0;
-  if (a.cap_out > 0.f) {  // the host admits the soft cap at head_dim 256 only
-    if constexpr (D == 256) {
+  if (a.cap_out > 0.f) {  // the host admits the soft cap at head_dims 256 and 512 only
+    if constexpr (D >= 256) {
       if (sub)
         hipLaunchKernelGGL((paged_decode_kernel<T, D, true, true>), grid, block, 0, stream, a);
       else
@@ -662,9 +736,13 @@ static int launch_t(const DecodeArgs& a, int head_dim, hipStream_t stream) {
     case 128: return launch_typed<T, 128>(a, stream);
     case 256:  // 16-bit pools only (Gemma-4's sliding layers, griffin)
       if constexpr (Elem<T>::bytes == 2) return launch_typed<T, 256>(a, stream);
-      [[fallthrough]];
-    default: return fail(SP_EUNSUPPORTED, "paged decode: head_dim %d has no kernel", head_dim);
+      break;
+    case 512:  // 16-bit pools only (Gemma-4's global layers)
+      if constexpr (Elem<T>::bytes == 2) return launch_typed<T, 512>(a, stream);
+      break;
+    default: break;
   }
+  return fail(SP_EUNSUPPORTED, "paged decode: head_dim %d has no kernel", head_dim);
 }
 
 template <typename T>

@@ -125,6 +125,13 @@ __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+// Workgroup barrier for data in LDS only: waits for this wave's LDS accesses, not for its global
+// loads (which stay in flight across it), then meets the other waves. The memory clobber keeps
+// the compiler from moving LDS accesses across it.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 // Butterfly max / sum over aligned groups of WIDTH lanes (WIDTH a power of two <= 64).
 template <int WIDTH>
 __device__ __forceinline__ float group_max(float v) {

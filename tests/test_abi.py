@@ -286,8 +286,8 @@ def test_ragged_paged_attention_validation(sp_lib):
 
 
 def test_softcap_validation(sp_lib):
-    """The *_softcap entry points: 0 is the namesake, > 0 runs at head_dim 256 on bf16 / f16 only,
-    a negative or non-finite cap is rejected; all before anything is enqueued."""
+    """The *_softcap entry points: 0 is the namesake, > 0 runs at head_dims 256 and 512 on bf16 /
+    f16 only, a negative or non-finite cap is rejected; all before anything is enqueued."""
     fake = ctypes.c_void_p(0x1000)
     d = sp_lib.sp_paged_decode_softcap
 
@@ -295,26 +295,28 @@ def test_softcap_validation(sp_lib):
         return d(fake, fake, fake, fake, ctypes.byref(lay), fake, 2, fake, 32, 3, 4, 0.125, cap, -1,
                  dtype, None, 0, None)
 
-    _expect(_lib.SP_EUNSUPPORTED, dec(_lay(head_dim=128), 50.0), "head_dim 256")
+    cap_dims = "head_dims 256 and 512"
+    _expect(_lib.SP_EUNSUPPORTED, dec(_lay(head_dim=128), 50.0), cap_dims)
     _expect(_lib.SP_EUNSUPPORTED, dec(_lay(head_dim=256), 50.0, dtype=0), "head_dim 256")
+    _expect(_lib.SP_EUNSUPPORTED, dec(_lay(head_dim=512), 50.0, dtype=0), "head_dim 512")
     _expect(_lib.SP_EINVAL, dec(_lay(head_dim=256), -1.0), "logit_softcap")
     _expect(_lib.SP_EINVAL, dec(_lay(head_dim=256), float("nan")), "logit_softcap")
     a = sp_lib.sp_paged_append_decode_softcap
     _expect(_lib.SP_EUNSUPPORTED,
             a(fake, fake, fake, fake, ctypes.byref(_lay()), fake, fake, 128, 64, fake, 2, fake, 32,
-              3, 4, 0.125, 50.0, -1, 1, None, 0, None), "head_dim 256")
+              3, 4, 0.125, 50.0, -1, 1, None, 0, None), cap_dims)
     v = sp_lib.sp_varlen_prefill_softcap
     _expect(_lib.SP_EUNSUPPORTED,
             v(fake, fake, fake, fake, fake, fake, 2, 16, 4, 2, 128, 0.125, 50.0, 1, -1, 1, None),
-            "head_dim 256")
+            cap_dims)
     _expect(_lib.SP_EINVAL,
             v(fake, fake, fake, fake, fake, fake, 2, 16, 4, 2, 256, 0.125, float("inf"), 1, -1, 1,
               None), "logit_softcap")
     p = sp_lib.sp_paged_prefill_softcap
     _expect(_lib.SP_EUNSUPPORTED,
             p(fake, fake, fake, fake, ctypes.byref(_lay()), fake, 2, fake, fake, 2, 16, 4, 0.125,
-              50.0, -1, 1, None, 0, None), "head_dim 256")
+              50.0, -1, 1, None, 0, None), cap_dims)
     r = sp_lib.sp_ragged_paged_attention_softcap
     _expect(_lib.SP_EUNSUPPORTED,
             r(fake, fake, fake, fake, ctypes.byref(_lay()), fake, 2, fake, fake, 3, 1, 16, 16, 32,
-              4, 0.125, 50.0, -1, 1, None, 0, None), "head_dim 256")
+              4, 0.125, 50.0, -1, 1, None, 0, None), cap_dims)
