@@ -453,7 +453,7 @@ int sp_paged_decode_noalloc(void* out, const void* q, const void* k_pool, const 
 
 // dense_f32: the dense f32 path (flash_attention), which also takes head dims 40, 80, 160 and
 // 256 and a value head dim of its own; everything else runs head_dim 64 or 128, Dv == D (and
-// 256 for 16-bit tensors).
+// 256 and 512 for 16-bit tensors).
 static int check_prefill_common(const char* fn, int32_t num_seqs, int32_t max_seqlen_q,
                                 int32_t hq, int32_t hkv, int32_t D, float scale,
                                 int32_t causal, int32_t window_left, sp_dtype dtype,
@@ -473,10 +473,10 @@ static int check_prefill_common(const char* fn, int32_t num_seqs, int32_t max_se
                   "%s: f32 head_dim %d / value head_dim %d has no kernel (head_dim 40, 64, 80, "
                   "128, 160 or 256; value head_dim a multiple of 4 up to 256)",
                   fn, D, Dv);
-  } else if ((D != 64 && D != 128 && !(D == 256 && dtype != SP_F32)) || Dv != D) {
+  } else if ((D != 64 && D != 128 && !((D == 256 || D == 512) && dtype != SP_F32)) || Dv != D) {
     return fail(SP_EUNSUPPORTED,
-                "%s: head_dim %d / value head_dim %d has no %s kernel (64 or 128, and 256 for "
-                "16-bit tensors; equal)",
+                "%s: head_dim %d / value head_dim %d has no %s kernel (64 or 128, and 256 and 512 "
+                "for 16-bit tensors; equal)",
                 fn, D, Dv, dtype_name(dtype));
   }
   if (causal < SP_CAUSAL_NONE || causal > SP_CAUSAL_TOP_LEFT)
@@ -557,7 +557,7 @@ int sp_varlen_prefill_softcap(void* out, const void* q, const void* k, const voi
 // bound is the block tables' width), lowered until the partials fit the caller's workspace.
 static int prefill_splits(int32_t num_seqs, int32_t max_seqlen_q, int32_t num_q_heads,
                           int32_t head_dim, int64_t max_context, size_t workspace_bytes) {
-  if (head_dim == 256) return 1;  // the head-dim-256 kernel walks every key tile itself
+  if (head_dim >= 256) return 1;  // the head-dim-256 / 512 kernels walk every key tile themselves
   const int64_t base = (int64_t)((max_seqlen_q + kPrefillBM - 1) / kPrefillBM) * num_seqs *
                        num_q_heads;
   int s = plan_prefill_splits(base, (max_context + kPrefillBN - 1) / kPrefillBN);

@@ -119,20 +119,6 @@ __device__ __forceinline__ f32x4_v mfma_f32(float a, float b, f32x4_v c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
-// Value held by lane ^ 16 / lane ^ 32. v_permlane16_swap(x, x) returns (x[l & ~16], x[l | 16])
-// and v_permlane32_swap(x, x) returns (x[l & ~32], x[l | 32]); the partner is the one that is not
-// the lane's own value.
-__device__ __forceinline__ float xor16(float x) {
-  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false,
-                                                  false);
-  return __uint_as_float((__lane_id() & 16) ? r[0] : r[1]);
-}
-__device__ __forceinline__ float xor32(float x) {
-  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
-                                                  false);
-  return __uint_as_float((__lane_id() & 32) ? r[0] : r[1]);
-}
-
 template <typename T, int D>
 struct DecodeCfg {
   static constexpr int ES = Elem<T>::bytes;

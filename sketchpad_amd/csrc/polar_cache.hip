@@ -301,18 +301,6 @@ __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {  // v_cvt_pk
   return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_v){lo, hi}, bf16x2_v));
 }
 
-// Xor-partner values across the 16-lane rows of a wave (see paged_decode.hip).
-__device__ __forceinline__ float pxor16(float x) {
-  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false,
-                                                  false);
-  return __uint_as_float((__lane_id() & 16) ? r[0] : r[1]);
-}
-__device__ __forceinline__ float pxor32(float x) {
-  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
-                                                  false);
-  return __uint_as_float((__lane_id() & 32) ? r[0] : r[1]);
-}
-
 template <int NW> struct CodeWords;
 template <> struct CodeWords<4> {
   using V = uint4;
@@ -413,8 +401,8 @@ __global__ void __launch_bounds__(64 * kDecodeWaves, 4) polar_decode_kernel(Deco
       }
     }
   }
-  qsum += pxor16(qsum);
-  qsum += pxor32(qsum);
+  qsum += xor16(qsum);
+  qsum += xor32(qsum);
   if (a.scale_log2 < 0.f) qsum = -qsum;
   const float s_init = -PolarQk<T>::kBias * qsum;
   const f32x4_v s0 = {s_init, s_init, s_init, s_init};
@@ -514,8 +502,8 @@ __global__ void __launch_bounds__(64 * kDecodeWaves, 4) polar_decode_kernel(Deco
     // exp2(score - m_run) stay below 2^kLazy, well inside fp32 and bf16 range. Any reference max
     // gives the same acc / l; the merge and the split combine use each wave's own m_run.
     float mt = fmaxf(fmaxf(u[0], u[1]), fmaxf(u[2], u[3]));
-    mt = fmaxf(mt, pxor16(mt));
-    mt = fmaxf(mt, pxor32(mt));
+    mt = fmaxf(mt, xor16(mt));
+    mt = fmaxf(mt, xor32(mt));
     mt *= ck;
     if (__builtin_amdgcn_ballot_w64(mt > m_run + kLazy)) {
       const float m_new = fmaxf(m_run, mt);
@@ -570,8 +558,8 @@ __global__ void __launch_bounds__(64 * kDecodeWaves, 4) polar_decode_kernel(Deco
   // of |v| / 7.
   const float cn = kVBias * __shfl(corr[0], n, 64);
   constexpr float kSeventh = 1.0f / 7.0f;
-  l_run += pxor16(l_run);
-  l_run += pxor32(l_run);
+  l_run += xor16(l_run);
+  l_run += xor32(l_run);
   __syncthreads();
   float* cm = (float*)smem;             // [waves][16]
   float* cl = cm + kDecodeWaves * 16;   // [waves][16]

@@ -46,6 +46,7 @@ typedef __bf16 pf_bf16x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 pf_f16x2 __attribute__((ext_vector_type(2)));
 typedef float pf_f32x2 __attribute__((ext_vector_type(2)));
 typedef float pf_f32x16 __attribute__((ext_vector_type(16)));
+typedef float pf_f32x4 __attribute__((ext_vector_type(4)));
 typedef short pf_s16x4 __attribute__((ext_vector_type(4)));
 typedef short pf_s16x8 __attribute__((ext_vector_type(8)));
 typedef __attribute__((address_space(3))) pf_s16x4 lds_s16x4;
@@ -58,6 +59,16 @@ template <> struct PrefillMfma<bf16_t> {
   }
   __device__ __forceinline__ static pf_f32x16 mma(pf_s16x8 a, uint4 b, pf_f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(pf_bf16x8, a),
+                                                   __builtin_bit_cast(pf_bf16x8, b), c, 0, 0, 0);
+  }
+  // v_mfma_f32_16x16x32: A 16 x 32 (lane l: row l % 16, k 8(l / 16) .. +7), B 32 x 16 (lane l:
+  // column l % 16, the same k), D 16 x 16 (lane l: column l % 16, rows 4(l / 16) .. +3)
+  __device__ __forceinline__ static pf_f32x4 mma16(uint4 a, uint4 b, pf_f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(pf_bf16x8, a),
+                                                   __builtin_bit_cast(pf_bf16x8, b), c, 0, 0, 0);
+  }
+  __device__ __forceinline__ static pf_f32x4 mma16(pf_s16x8 a, uint4 b, pf_f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(pf_bf16x8, a),
                                                    __builtin_bit_cast(pf_bf16x8, b), c, 0, 0, 0);
   }
   __device__ __forceinline__ static uint32_t pack(float lo, float hi) {  // v_cvt_pk_bf16_f32 (RNE)
@@ -76,6 +87,14 @@ template <> struct PrefillMfma<f16_t> {
   }
   __device__ __forceinline__ static pf_f32x16 mma(pf_s16x8 a, uint4 b, pf_f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(pf_f16x8, a),
+                                                  __builtin_bit_cast(pf_f16x8, b), c, 0, 0, 0);
+  }
+  __device__ __forceinline__ static pf_f32x4 mma16(uint4 a, uint4 b, pf_f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(pf_f16x8, a),
+                                                  __builtin_bit_cast(pf_f16x8, b), c, 0, 0, 0);
+  }
+  __device__ __forceinline__ static pf_f32x4 mma16(pf_s16x8 a, uint4 b, pf_f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(pf_f16x8, a),
                                                   __builtin_bit_cast(pf_f16x8, b), c, 0, 0, 0);
   }
   __device__ __forceinline__ static uint32_t pack(float lo, float hi) {
@@ -1575,6 +1594,404 @@ __global__ void __launch_bounds__(256, 2) prefill_wide_kernel(PrefillArgs a) {
     }
 }
 
+// Head dim 512 (Gemma-4's global-attention layers, gemma4.rs:82-107): a wave of 32 queries would
+// hold 128 VGPRs of Q and 256 of O at this width, so each wave takes 16 queries on
+// v_mfma_f32_16x16x32 (S^T blocks of 16 keys x 16 queries, O^T blocks of 16 dims x 16 queries)
+// and eight waves cover the 128-query block. The K / V tiles (32 keys, 32 KiB each) go HBM -> LDS
+// one ahead through two buffers (128 KiB: one workgroup of two waves per SIMD on each CU); waves
+// 0-3 load K, 4-7 V, one 1 KiB row per load. Lane (g, n) (g = lane / 16, n = lane % 16) holds
+// query n's scores of the tile's keys 4g .. 4g+3 and 16 + 4g .. +3, which are also the k slots
+// 8g .. 8g+7 of its P^T operand; the V^T operand takes the same keys through two transpose reads.
+// Contiguous and paged K/V, the masks and arguments of prefill_kernel; no key split. CAP: the
+// logit soft cap (a.cap_in / a.cap_out) on each tile's raw products before the masks.
+template <typename T, bool PAGED, bool CAP = false>
+__global__ void __launch_bounds__(512, 1) prefill_d512_kernel(PrefillArgs a) {
+  using C = PrefillCfg<512>;  // the row swizzle
+  using M = PrefillMfma<T>;
+  constexpr int D = 512, BN = 32, RB = C::RB, TILE = BN * RB;
+  constexpr int KC = D / 32;  // QK k-steps (32 dims each)
+  constexpr int DB = D / 16;  // PV output blocks (16 dims each)
+  constexpr int NLD = 8;      // one-row loads per wave and tile
+  static_assert(RB == 1024 && NLD * 4 == BN, "four waves fill one tile, a row per load");
+  __shared__ __attribute__((aligned(1024))) char kl[2][TILE];
+  __shared__ __attribute__((aligned(1024))) char vl[2][TILE];
+
+  // ---- workgroup -> (kv head, group member, sequence, query block), heavy query blocks first;
+  // wave w takes queries 16w .. 16w + 15 of the block
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = wave_uniform(tid >> 6);
+  const int32_t* const cu_q_p = a.cu_q;
+  const int32_t* const cu_k_p = PAGED ? a.context_lens : a.cu_k;
+  int id = blockIdx.x;
+  const int kvh = id % a.hkv;
+  id /= a.hkv;
+  const int gm = id % a.group;
+  id /= a.group;
+  const int seq = id % a.num_seqs;
+  const int qblk = a.num_qblocks - 1 - id / a.num_seqs;
+  const int h = kvh * a.group + gm;
+
+  const kconst_i32 cq = cu_q_p ? as_const(cu_q_p) + seq : as_const(kPrefillZeroPair);
+  const kconst_i32 ck = PAGED || cu_k_p ? as_const(cu_k_p) + seq : as_const(kPrefillZeroPair);
+  const int cq0 = cq[0], cq1 = cq[1], ck0 = ck[0], ck1 = PAGED ? 0 : ck[1];
+  asm volatile("" ::"s"(ck0), "s"(ck1));  // keep the key-length loads ahead of the early exit
+  const int q_begin = cq0;
+  const int Lq = cu_q_p ? cq1 - cq0 : a.lq;
+  int Lk, k_begin = 0;
+  if constexpr (PAGED) {
+    Lk = min(ck0, a.max_blocks_per_seq * a.block_size);
+  } else {
+    k_begin = ck0;
+    Lk = cu_k_p ? ck1 - ck0 : a.lk;
+  }
+  const int qs = qblk * kPrefillBM;
+  if (qs >= Lq) return;
+  const int qe = min(qs + kPrefillBM, Lq);
+  const int pos_off = (a.causal == SP_CAUSAL_TOP_LEFT) ? 0 : Lk - Lq;
+  // keys any query of this workgroup can see: [kv_lo, kv_hi)
+  int kv_lo = 0, kv_hi = Lk;
+  if (a.causal != SP_CAUSAL_NONE) kv_hi = min(Lk, qe - 1 + pos_off + 1);
+  if (a.window_left >= 0) kv_lo = max(0, qs + pos_off - a.window_left);
+  const int t_first = (kv_lo / BN) * BN, kv_end = kv_hi;
+
+  const int n = lane & 15, g = lane >> 4;  // MFMA column (query) and row group
+
+  // ---- per-sequence base addresses
+  const char* qbase = (const char*)a.q +
+      ((a.cu_q ? (int64_t)q_begin * a.q_tok : (int64_t)seq * a.q_batch) + (int64_t)h * a.q_head) * 2;
+  char* obase = (char*)a.out +
+      ((a.cu_q ? (int64_t)q_begin * a.o_tok : (int64_t)seq * a.o_batch) + (int64_t)h * a.o_head) *
+          dtype_size((sp_dtype)a.out_dtype);
+  const char* kbase = nullptr;
+  const char* vbase = nullptr;
+  const int32_t* table = nullptr;
+  int64_t head_off = 0;
+  if constexpr (PAGED) {
+    table = a.block_tables + (int64_t)seq * a.max_blocks_per_seq;
+    head_off = a.layer_off_b + (int64_t)kvh * a.block_size * RB;
+  } else {
+    const int64_t kv0 = (a.cu_k ? (int64_t)k_begin * a.kv_tok : (int64_t)seq * a.kv_batch) +
+                        (int64_t)kvh * a.kv_head;
+    kbase = (const char*)a.k + kv0 * 2;
+    vbase = (const char*)a.v + kv0 * 2;
+  }
+
+  // ---- HBM -> LDS tile loads. Wave w (w & 3 = j) loads rows 8j .. 8j + 7 of each tile (K for
+  // waves 0-3, V for 4-7), one row per load; lane `lane` takes physical chunk `lane` of the row
+  // and fetches the logical chunk the swizzle puts there. Interior tiles go out in two groups of
+  // four loads that share one M0 write (instruction offsets 0-3 KiB): contiguous K/V from one
+  // scalar base per tile, paged K/V from one base per block (block_size divides the tile) or per
+  // group (block_size a multiple of four). Edge tiles clamp rows outside [kv_lo, kv_hi) to a
+  // valid row (their scores are masked) and compute per-lane addresses.
+  const bool v_wave = wave >= 4;
+  const int wrow0 = (wave & 3) * NLD;
+  const int64_t row_pitch = PAGED ? (int64_t)RB : (int64_t)a.kv_tok * 2;
+  const char* src_base = PAGED ? (v_wave ? a.vpool : a.kpool) : (v_wave ? vbase : kbase);
+  const bool paged_fast = PAGED && BN % a.block_size == 0;
+  const bool group_blk = wave_uniform(PAGED && a.block_size % 4 == 0);
+  // lane part of load u's source offset less its instruction offset (u % 4) KiB; >= 0: load u's
+  // row lies u rows of at least RB = 1 KiB past the group's base (contiguous), or its group
+  // starts a block's rows (paged, whole groups)
+  int voff_g[NLD];
+#pragma unroll
+  for (int u = 0; u < NLD; ++u) {
+    const int r = wrow0 + u;
+    const int chunk = 16 * (lane ^ C::swz(r));
+    if constexpr (PAGED)
+      voff_g[u] = (r % max(a.block_size, 1)) * RB + chunk - (group_blk ? (u & 3) * 1024 : 0);
+    else
+      voff_g[u] = (int)((int64_t)(u & 4) * row_pitch) + (u & 3) * (int)(row_pitch - 1024) + chunk;
+  }
+  auto tile_interior = [&](int t0) __attribute__((always_inline)) {
+    return t0 >= kv_lo && t0 + BN <= kv_hi;
+  };
+  // paged: block ids of this wave's rows of the next tile, fetched a tile ahead in lanes 0-7
+  int nblk = 0;
+  const int bs_shift = paged_fast ? wave_uniform(31 - __builtin_clz(max(a.block_size, 1))) : 0;
+  const int lane_blk = (wrow0 + min(lane, NLD - 1)) >> bs_shift;
+  auto fetch_blocks = [&](int t0) __attribute__((always_inline)) {
+    if constexpr (PAGED) {
+      if (paged_fast && t0 < kv_end && tile_interior(t0)) nblk = table[(t0 >> bs_shift) + lane_blk];
+    }
+  };
+  auto issue_tile = [&](int t0, char* buf) __attribute__((always_inline)) {
+    char* dst = buf + wrow0 * RB;
+    if (tile_interior(t0) && (!PAGED || paged_fast)) {
+      if constexpr (PAGED) {
+        const int bl = (nblk >= 0 && nblk < a.num_blocks) ? nblk : 0;  // never outside the pool
+        const uint64_t vb = (uint64_t)(uintptr_t)(src_base + head_off) +
+                            (uint64_t)bl * (uint64_t)a.block_stride_b -
+                            (group_blk ? 0ull : (uint64_t)((lane & 3) * 1024));
+        const int vb_lo = (int)(uint32_t)vb, vb_hi = (int)(uint32_t)(vb >> 32);
+        auto base_of = [&](int u) __attribute__((always_inline)) {
+          const uint64_t lo = (uint32_t)__builtin_amdgcn_readlane(vb_lo, u);
+          const uint64_t hi = (uint32_t)__builtin_amdgcn_readlane(vb_hi, u);
+          return (const char*)(uintptr_t)((hi << 32) | lo);
+        };
+#pragma unroll
+        for (int gq = 0; gq < NLD; gq += 4) {
+          if (group_blk) {
+            const char* b = base_of(gq);
+            lds_dma16x4(b, b, b, b, voff_g[gq], voff_g[gq + 1], voff_g[gq + 2], voff_g[gq + 3],
+                        dst + gq * 1024);
+          } else {
+            lds_dma16x4(base_of(gq), base_of(gq + 1), base_of(gq + 2), base_of(gq + 3),
+                        voff_g[gq], voff_g[gq + 1], voff_g[gq + 2], voff_g[gq + 3],
+                        dst + gq * 1024);
+          }
+        }
+      } else {
+        const char* sb = src_base + (int64_t)(t0 + wrow0) * row_pitch;
+#pragma unroll
+        for (int gq = 0; gq < NLD; gq += 4)
+          lds_dma16x4(sb, sb, sb, sb, voff_g[gq], voff_g[gq + 1], voff_g[gq + 2], voff_g[gq + 3],
+                      dst + gq * 1024);
+      }
+      return;
+    }
+    int ln = lane;
+    asm volatile("" : "+v"(ln));
+#pragma unroll
+    for (int u = 0; u < NLD; ++u) {
+      const int R = wrow0 + u;
+      const int c = ln ^ C::swz(R);
+      const int j = min(max(t0 + R, kv_lo), kv_hi - 1);
+      const char* src;
+      if constexpr (PAGED) {
+        int blk = table[j / a.block_size];
+        blk = (blk >= 0 && blk < a.num_blocks) ? blk : 0;  // never dereference outside the pool
+        src = src_base + (int64_t)blk * a.block_stride_b + head_off +
+              (int64_t)(j % a.block_size) * RB + c * 16;
+      } else {
+        src = src_base + (int64_t)j * row_pitch + c * 16;
+      }
+      lds_dma16(src, dst + u * 1024);
+    }
+  };
+
+  // First tile's loads ahead of the Q loads.
+  int t0 = t_first;
+  if (t0 < kv_end) {
+    fetch_blocks(t0);
+    issue_tile(t0, v_wave ? vl[0] : kl[0]);
+    fetch_blocks(t0 + BN);
+  }
+
+  // ---- Q^T operand (B of the S^T MFMA): query wq0 + n, dims 32c + 8g .. +7, unscaled.
+  const int wq0 = qs + 16 * wave;
+  const int my_q = wq0 + n;
+  const float c2 = CAP ? 1.f : a.scale_log2;  // with the cap the scores already are exponents
+  uint4 qreg[KC];
+  {
+    const char* qp = qbase + (int64_t)min(my_q, qe - 1) * a.q_tok * 2;
+#pragma unroll
+    for (int c = 0; c < KC; ++c)
+      qreg[c] = my_q < qe ? *(const uint4*)(qp + (32 * c + 8 * g) * 2) : make_uint4(0, 0, 0, 0);
+  }
+
+  float m_run = -INFINITY, m_used = 0.f, l_run = 0.f;
+  pf_f32x4 acc[DB];
+#pragma unroll
+  for (int db = 0; db < DB; ++db) acc[db] = pf_f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int wq_lo = wq0, wq_hi = min(wq0 + 16, qe) - 1;  // this wave's queries (inclusive)
+  const bool wave_active = wq_lo < qe;
+  const int qpos = my_q + pos_off;
+  int mask_below = kv_lo, mask_above = Lk - BN;
+  if (a.causal != SP_CAUSAL_NONE) mask_above = min(mask_above, wq_lo + pos_off - BN + 1);
+  if (a.window_left >= 0) mask_below = max(mask_below, wq_hi + pos_off - a.window_left);
+  mask_below = wave_uniform(mask_below);
+  mask_above = wave_uniform(mask_above);
+
+  // LDS operand addresses: K operand (half b, k-step c) is row 16b + n, logical chunk 4c + g:
+  // b 16 RB + (k_lane ^ 64c). V^T operand (keys 16b + 4g .., dims 16db ..) by transpose read: lane
+  // n addresses row 16b + 4g + n / 4, dims 16db + 4(n % 4) .. +3: b 16 RB + (v_lane ^ 32db).
+  const int k_lane = (n * RB) | (16 * (g ^ C::swz(n)));
+  const int vr = 4 * g + (n >> 2);
+  const int v_lane = (vr * RB) | (16 * (((n & 3) >> 1) ^ C::swz(vr))) | (8 * (n & 1));
+
+  // score i of this lane is key t0 + koff(i), koff(i) = 16(i / 4) + 4g + i % 4
+  float sc[8];
+  auto qk = [&](const char* kb) __attribute__((always_inline)) {
+    int kbl = k_lane;
+    asm volatile("" : "+v"(kbl));
+    auto read_k = [&](int i) __attribute__((always_inline)) {  // operand i: half i & 1, step i / 2
+      return *(const uint4*)(kb + (i & 1) * 16 * RB + (kbl ^ (64 * (i >> 1))));
+    };
+    constexpr int AHK = 2;
+    uint4 kop[AHK];
+#pragma unroll
+    for (int i = 0; i < AHK; ++i) kop[i] = read_k(i);
+    __builtin_amdgcn_sched_barrier(0);
+    pf_f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < 2 * KC; ++i) {
+      const uint4 cur = kop[i % AHK];
+      if (i + AHK < 2 * KC) kop[i % AHK] = read_k(i + AHK);
+      if (i & 1) s1 = M::mma16(cur, qreg[i >> 1], s1);
+      else s0 = M::mma16(cur, qreg[i >> 1], s0);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      sc[r] = s0[r];
+      sc[4 + r] = s1[r];
+    }
+  };
+
+  const float* mrow = a.mask ? a.mask + (int64_t)seq * a.mask_b + (int64_t)h * a.mask_h +
+                                   (int64_t)min(my_q, qe - 1) * a.mask_q
+                             : nullptr;
+  auto apply_mask = [&](int t0) __attribute__((always_inline)) {
+    const int jb = t0 + 4 * g;
+    if (mrow) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        sc[i] += mrow[min(jb + 16 * (i >> 2) + (i & 3), Lk - 1)] * a.inv_scale;
+    }
+    if (t0 < mask_below || t0 > mask_above) {
+      int lo = kv_lo, hi = Lk - 1;
+      if (a.causal != SP_CAUSAL_NONE) hi = min(hi, qpos);
+      if (a.window_left >= 0) lo = max(lo, qpos - a.window_left);
+      const int olo = lo - jb, ohi = hi - jb;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int off = 16 * (i >> 2) + (i & 3);
+        sc[i] = (off >= olo && off <= ohi) ? sc[i] : -INFINITY;
+      }
+    }
+  };
+
+  // Softmax weights (FlashAttention-2 online softmax, Dao 2023) with the lazily raised maximum
+  // of prefill_kernel: p = 2^(s c2 - m_used), packed to 16 bits in k-slot order (pb word e holds
+  // scores 2e, 2e + 1); the row sum adds the 16-bit values the PV product uses.
+  uint4 pb;
+  float la = 0.f;
+  auto weights_all = [&](float off) __attribute__((always_inline)) {
+    uint32_t w[4];
+    la = 0.f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[2 * e], c2, -off));
+      const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[2 * e + 1], c2, -off));
+      w[e] = M::pack(p0, p1);
+      la = M::sum2(w[e], la);
+    }
+    pb = make_uint4(w[0], w[1], w[2], w[3]);
+  };
+  constexpr float kLazyBound = 4096.f;  // 2^12
+  auto finish_weights = [&]() __attribute__((always_inline)) {
+    float lsum = la;
+    if (__any(lsum > kLazyBound || m_run == -INFINITY)) {
+      float x = max3f(sc[0], sc[1], sc[2]);
+      x = max3f(x, sc[3], sc[4]);
+      x = max3f(x, sc[5], sc[6]);
+      x = __builtin_fmaxf(x, sc[7]);
+      x = __builtin_fmaxf(x, xor16(x));  // the query's four lanes: n, n + 16, n + 32, n + 48
+      x = __builtin_fmaxf(x, xor32(x));
+      const float m_new = __builtin_fmaxf(m_run, x * c2);
+      const float used_new = (m_new == -INFINITY) ? 0.f : m_new;
+      const float alpha = __builtin_amdgcn_exp2f(m_run - used_new);  // 0 while m_run = -inf
+      weights_all(used_new);
+      lsum = la;
+      m_run = m_new;
+      m_used = used_new;
+      l_run *= alpha;
+#pragma unroll
+      for (int db = 0; db < DB; ++db) acc[db] *= alpha;
+    }
+    l_run += lsum;
+  };
+
+  // PV product O^T += V^T P^T: output block db (dims 16db ..) takes the V^T operand of keys
+  // 4g .. 4g+3 (first transpose read) and 16 + 4g .. +3 (second), k slots 8g .. 8g+7.
+  auto pv = [&](const char* vb) __attribute__((always_inline)) {
+    int vbl = v_lane;
+    asm volatile("" : "+v"(vbl));
+    auto read_v = [&](int db) __attribute__((always_inline)) {
+      const char* a0 = vb + (vbl ^ (32 * db));
+      const pf_s16x4 v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(a0));
+      const pf_s16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(a0 + 16 * RB));
+      return __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7);
+    };
+    constexpr int AH = 2;
+    pf_s16x8 vop[AH];
+#pragma unroll
+    for (int i = 0; i < AH; ++i) vop[i] = read_v(i);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int db = 0; db < DB; ++db) {
+      const pf_s16x8 cur = vop[db % AH];
+      if (db + AH < DB) vop[db % AH] = read_v(db + AH);
+      acc[db] = M::mma16(cur, pb, acc[db]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+
+  int vis_lo = -(1 << 30), vis_hi = wave_active ? kv_end : -(1 << 30);
+  if (a.causal != SP_CAUSAL_NONE) vis_hi = min(vis_hi, wq_hi + pos_off + 1);
+  if (a.window_left >= 0) vis_lo = wq_lo + pos_off - a.window_left - BN + 1;
+  vis_lo = wave_uniform(vis_lo);
+  vis_hi = wave_uniform(vis_hi);
+
+  // One step on tile t0: wait for its tiles (own loads, then everyone's; the barrier also frees
+  // the other buffers), start the next tile's loads, then QK product, softmax, PV product.
+  auto step = [&](int t0, const char* kcur, const char* vcur, char* kload, char* vload)
+      __attribute__((always_inline)) {
+    __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+    __syncthreads();
+    if (t0 + BN < kv_end) {
+      issue_tile(t0 + BN, v_wave ? vload : kload);
+      fetch_blocks(t0 + 2 * BN);
+    }
+    if (t0 >= vis_lo && t0 < vis_hi) {
+      qk(kcur);
+      if constexpr (CAP) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) sc[i] = softcap_log2(sc[i], a.cap_in, a.cap_out);
+      }
+      apply_mask(t0);
+      float off = m_used;
+      asm volatile("" : "+v"(off));
+      weights_all(off);
+      finish_weights();
+      pv(vcur);
+    }
+  };
+  while (t0 < kv_end) {
+    step(t0, kl[0], vl[0], kl[1], vl[1]);
+    t0 += BN;
+    if (t0 >= kv_end) break;
+    step(t0, kl[1], vl[1], kl[0], vl[0]);
+    t0 += BN;
+  }
+
+  // ---- normalise and store: lane holds O^T[dims 16db + 4g .. +3][query n]
+  float l = l_run;
+  l += xor16(l);
+  l += xor32(l);
+  if (my_q >= qe) return;
+  const float inv = l > 0.f ? 1.f / l : 0.f;
+  constexpr int kSelf = std::is_same<T, bf16_t>::value ? SP_BF16 : SP_F16;  // out = in type
+  const int oes = dtype_size((sp_dtype)a.out_dtype);
+  char* op = obase + (int64_t)my_q * a.o_tok * oes;
+#pragma unroll
+  for (int db = 0; db < DB; ++db) {
+    const int d0 = db * 16 + 4 * g;
+    const float o0 = acc[db][0] * inv, o1 = acc[db][1] * inv;
+    const float o2 = acc[db][2] * inv, o3 = acc[db][3] * inv;
+    if (a.out_dtype == SP_F32) {
+      *(float4*)(op + d0 * 4) = make_float4(o0, o1, o2, o3);
+    } else if (a.out_dtype == kSelf) {
+      *(uint2*)(op + d0 * 2) = make_uint2(M::pack(o0, o1), M::pack(o2, o3));
+    } else {  // the other 16-bit type
+      using O = PrefillMfma<typename std::conditional<kSelf == SP_BF16, f16_t, bf16_t>::type>;
+      *(uint2*)(op + d0 * 2) = make_uint2(O::pack(o0, o1), O::pack(o2, o3));
+    }
+  }
+}
+
 // Merge the split partials of one (sequence, head, group of kCombineRows query rows):
 // out = sum_s 2^(m_s - M) acc_s / sum_s 2^(m_s - M) l_s, M = max_s m_s (zeros when no split saw
 // a key). D/4 lanes per row, four output elements each, one row per lane group, so every row's
@@ -1695,14 +2112,37 @@ static int launch_wide(const PrefillArgs& a, bool paged, hipStream_t stream) {
 }
 
 template <typename T>
+static int launch_d512(const PrefillArgs& a, bool paged, hipStream_t stream) {
+  if (a.nsplit > 1) return fail(SP_EUNSUPPORTED, "prefill: head_dim 512 takes no key split");
+  const int64_t blocks = (int64_t)a.num_qblocks * a.num_seqs * a.hq;
+  if (blocks <= 0) return SP_OK;
+  if (blocks > 0x7fffffff) return fail(SP_EINVAL, "prefill: grid of %lld workgroups", (long long)blocks);
+  const dim3 grid((unsigned)blocks), block(512);
+  if (a.cap_out > 0.f) {
+    if (paged)
+      hipLaunchKernelGGL((prefill_d512_kernel<T, true, true>), grid, block, 0, stream, a);
+    else
+      hipLaunchKernelGGL((prefill_d512_kernel<T, false, true>), grid, block, 0, stream, a);
+  } else if (paged) {
+    hipLaunchKernelGGL((prefill_d512_kernel<T, true>), grid, block, 0, stream, a);
+  } else {
+    hipLaunchKernelGGL((prefill_d512_kernel<T, false>), grid, block, 0, stream, a);
+  }
+  return check_launch("prefill_d512_kernel");
+}
+
+template <typename T>
 static int launch_t(const PrefillArgs& a, int head_dim, bool paged, hipStream_t stream) {
-  if (a.cap_out > 0.f && head_dim != 256)
+  if (a.cap_out > 0.f && head_dim != 256 && head_dim != 512)
     return fail(SP_EUNSUPPORTED, "prefill: logit soft cap at head_dim %d", head_dim);
   switch (head_dim) {
     case 64: return launch_td<T, 64>(a, paged, stream);
     case 128: return launch_td<T, 128>(a, paged, stream);
     case 256: return launch_wide<T>(a, paged, stream);
-    default: return fail(SP_EUNSUPPORTED, "prefill: head_dim %d has no kernel (64, 128, 256)", head_dim);
+    case 512: return launch_d512<T>(a, paged, stream);
+    default:
+      return fail(SP_EUNSUPPORTED, "prefill: head_dim %d has no kernel (64, 128, 256, 512)",
+                  head_dim);
   }
 }
 

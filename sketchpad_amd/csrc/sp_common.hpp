@@ -125,6 +125,20 @@ __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+// Value held by lane ^ 16 / lane ^ 32. v_permlane16_swap(x, x) returns (x[l & ~16], x[l | 16])
+// and v_permlane32_swap(x, x) returns (x[l & ~32], x[l | 32]); the partner is the one that is not
+// the lane's own value.
+__device__ __forceinline__ float xor16(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return __uint_as_float((__lane_id() & 16) ? r[0] : r[1]);
+}
+__device__ __forceinline__ float xor32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return __uint_as_float((__lane_id() & 32) ? r[0] : r[1]);
+}
+
 // Workgroup barrier for data in LDS only: waits for this wave's LDS accesses, not for its global
 // loads (which stay in flight across it), then meets the other waves. The memory clobber keeps
 // the compiler from moving LDS accesses across it.
