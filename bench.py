@@ -29,6 +29,8 @@ line:
              the serial bound) and the C5 / C1 decode calls' fractions of HBM
   gemma4_d256  head dim 256 (Gemma-4's sliding layers, 16 / 8 heads, 1024-key window): a paged
              decode batch and a windowed varlen prefill, with their roofline fractions
+  gemma4_d512  head dim 512 (Gemma-4's global layers, 16 / 8 heads, causal, no window): the same
+             two legs
 Decode legs whose working set is below 512 MB (C5's window, the PolarQuant pools, C1) rotate
 their timed calls over copies of the pools, so that more than 512 MB (twice the 256 MB MALL) of
 K/V is read between two reads of the same byte; each reports its working set, the rotation and
@@ -88,7 +90,8 @@ def parse_args():
                     help="only that config's decode leg, timed as in the default line (pool "
                          "copies rotated past the MALL), for profiling; prints its JSON object")
     ap.add_argument("--gemma-only", action="store_true",
-                    help="only the head-dim-256 Gemma-4 decode and prefill legs (profiling)")
+                    help="only the Gemma-4 decode and prefill legs, head dims 256 and 512 "
+                         "(profiling)")
     ap.add_argument("--layer", action="store_true",
                     help="also time a whole attention layer (projections + RoPE append + "
                          "attention) on the C2 decode step and the C3 prefill")
@@ -475,19 +478,26 @@ def time_prefill_c3(steps: int, warmup: int):
 GEMMA4_LOGIT_SOFTCAP = 50.0  # attn_logit_softcap (crates/sketchpad-llm/src/gemma4.rs:96)
 
 
-def time_gemma4_d256(steps: int):
-    """Head dim 256 (Gemma-4's sliding-window layers, 16 query / 8 KV heads, a 1024-key window):
-    the paged decode of decode_gemma4_d256 timed past the MALL, and the windowed causal varlen
-    prefill of prefill_gemma4_d256 (TFLOP/s over the visible pairs), each as Gemma-4 runs it
-    (logit soft cap 50, the *_softcap entry points) and without the cap."""
+def time_gemma4(steps: int, head_dim: int):
+    """Gemma-4's two attention shapes, 16 query / 8 KV heads (gemma4.rs:82-107): head dim 256
+    (the sliding-window layers, a 1024-key window) and 512 (the global layers, causal with no
+    window). The paged decode (decode_gemma4_d256 / _d512, timed past the MALL) and the causal
+    varlen prefill (prefill_gemma4_d256 / _d512, TFLOP/s over the visible pairs), each as Gemma-4
+    runs it (logit soft cap 50, the *_softcap entry points) and without the cap."""
     import torch
     import sketchpad_amd as sp
     from sketchpad_amd import workloads as W
 
     cap = GEMMA4_LOGIT_SOFTCAP
-    dec = time_decode_leg("gemma4-d256", steps, W.decode_gemma4_d256())
-    dec_cap = time_decode_leg("gemma4-d256", steps, W.decode_gemma4_d256(), softcap=cap)
-    w = W.prefill_gemma4_d256()
+    if head_dim == 256:
+        dw, w = W.decode_gemma4_d256(), W.prefill_gemma4_d256()
+        kernel = "prefill_wide_kernel<bf16,256,false{}>"
+    else:
+        dw, w = W.decode_gemma4_d512(), W.prefill_gemma4_d512()
+        kernel = "prefill_d512_kernel<bf16,false{}>"
+    name = f"gemma4-d{head_dim}"
+    dec = time_decode_leg(name, steps, dw)
+    dec_cap = time_decode_leg(name, steps, dw, softcap=cap)
     t = W.make_prefill_tensors(w, with_pool=False)
     stream = torch.cuda.current_stream()
 
@@ -497,6 +507,7 @@ def time_gemma4_d256(steps: int):
                                          window_left=w.window_left, softcap=softcap,
                                          stream=stream.cuda_stream)
 
+    window = f"window_left {w.window_left}" if w.window_left >= 0 else "no window"
     res = {}
     for key, c in (("prefill", 0.0), ("prefill_softcap", cap)):
         fn = prefill(c)
@@ -505,11 +516,11 @@ def time_gemma4_d256(steps: int):
         ms, _ = _event_times(stream, fn, max(10, steps))
         tflops = w.flops() / (ms * 1e-3) / 1e12
         res[key] = {"workload": f"{w.name}: B={w.num_seqs}, lens={[int(x) for x in w.lens]}, "
-                                f"Hq={w.hq}, Hkv={w.hkv}, D={w.head_dim}, causal, "
-                                f"window_left {w.window_left}, logit softcap {c:g}",
+                                f"Hq={w.hq}, Hkv={w.hkv}, D={w.head_dim}, causal, {window}, "
+                                f"logit softcap {c:g}",
                     "ms": round(ms, 5), "flops": w.flops(), "tflops": round(tflops, 2),
                     "frac_mfma": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
-                    "kernel": f"prefill_wide_kernel<bf16,256,false{',true' if c else ''}>"}
+                    "kernel": kernel.format(",true" if c else "")}
     dec_cap["logit_softcap"] = cap
     return {"decode": dec, "decode_softcap": dec_cap, **res}
 
@@ -863,7 +874,8 @@ def main():
               flush=True)
         return
     if args.gemma_only:
-        print(json.dumps({"gemma4_d256": time_gemma4_d256(args.steps)}), flush=True)
+        print(json.dumps({"gemma4_d256": time_gemma4(args.steps, 256),
+                          "gemma4_d512": time_gemma4(args.steps, 512)}), flush=True)
         return
     w = W.DECODE_CONFIGS[args.config]()
     if args.polar_only:
@@ -928,7 +940,8 @@ def main():
             if name != args.config:
                 cfg[name] = time_decode_leg(name, max(10, args.steps // 2))
         line["configs"] = cfg
-        line["gemma4_d256"] = time_gemma4_d256(max(10, args.steps // 2))
+        line["gemma4_d256"] = time_gemma4(max(10, args.steps // 2), 256)
+        line["gemma4_d512"] = time_gemma4(max(10, args.steps // 2), 512)
     if args.secondary:
         sec = line.setdefault("secondary", {})
         sec["C4-chunked-prefill"] = time_chunked_c4(10, 2)

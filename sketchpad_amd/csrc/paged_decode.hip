@@ -642,15 +642,19 @@ DecodePlan plan_decode(int num_seqs, int hq, int hkv, int head_dim, int max_cont
   }
   p.max_tiles = max_tiles < 1 ? 1 : max_tiles;
   // Workgroups the batch launches with splits of t tiles if every sequence spanned max_tiles
-  // (the host does not read the context lengths). At head_dim 512 the four waves of a workgroup
-  // share each tile (a quarter of its dims each), so one tile is a whole-workgroup step, as four
-  // tiles are elsewhere: the rules below run on quarter tiles (qf) and the split is converted
-  // back at the end.
+  // (the host does not read the context lengths).
   const int64_t units = (int64_t)num_seqs * (hkv > 0 ? hkv : 1);
-  const int qf = (head_dim == 512 && kind == DecodeKind::Dense) ? kDecodeWaves : 1;
-  auto wgs = [&](int t) { return units * (((int64_t)p.max_tiles * qf + t - 1) / t); };
+  auto wgs = [&](int t) { return units * ((p.max_tiles + t - 1) / t); };
   int tps;
-  if (kind == DecodeKind::Dense) {
+  if (kind == DecodeKind::Dense && head_dim == 512) {
+    // The four waves of a workgroup share each tile (a quarter of its dims each), so a tile is a
+    // whole-workgroup step. 32 tiles, halved while the batch launches fewer than 512 workgroups:
+    // measured on Gemma-4's global shape (16 / 8 heads) at 8-128 sequences of 0.3k-32k tokens,
+    // 32-tile splits were 0.5-7 % faster than 16 and 8-15 % faster than 8; 64 was 1 % faster on
+    // 16 contexts of 8k-32k tokens and 0.5-7 % slower on the others.
+    tps = 32;
+    while (tps > 4 && wgs(tps) < 512) tps /= 2;
+  } else if (kind == DecodeKind::Dense) {
     // A rule fitted to measurements (24 batches: groups 1-16, 64-1024 units, contexts of
     // 256-16k tokens, windowed and not; it is within 2 % of the best of 32 / 64 / 128 tiles on
     // each, where one fixed length loses up to 20 %):
@@ -669,11 +673,9 @@ DecodePlan plan_decode(int num_seqs, int hq, int hkv, int head_dim, int max_cont
       while (tps > kDecodeWaves && wgs(tps) < 512) tps /= 2;
     } else if (wgs(128) >= 384 && wgs(128) <= 512) {
       tps = 128;
-    } else if (p.group <= 4 && units >= 512 && p.max_tiles * qf > 128 &&
-               p.max_tiles * qf <= 256) {
+    } else if (p.group <= 4 && units >= 512 && p.max_tiles > 128 && p.max_tiles <= 256) {
       tps = 32;
     }
-    tps = tps / qf < 1 ? 1 : tps / qf;
   } else {
     // Compressed tiles are a quarter of a dense one's bytes: start from 64-tile splits and halve
     // while the batch launches fewer than 2048 workgroups, but not below 32 tiles once it

@@ -119,9 +119,12 @@ struct PrefillCfg {
   // low four bits). Chosen so that 16 consecutive rows at one logical chunk, and 4 consecutive
   // rows x 64 logical bytes, land on distinct LDS banks.
   // (Rows of 32 chunks, D = 256, take the 16-chunk permutation: it only has to separate rows
-  // within 256 bytes of banks.)
+  // within 256 bytes of banks.) Rows of 64 chunks, D = 512, are read by transposes of 8 rows x
+  // 32 bytes per 32 lanes (prefill_d512_kernel), which need the row's permutation to move the
+  // chunk pair by a different even offset for each of 8 consecutive rows: 2(row % 8) + row / 8 % 2.
   __device__ __forceinline__ static int swz(int row) {
-    if constexpr (CPR >= 16) return ((row & 3) << 2) | ((row >> 2) & 3);
+    if constexpr (CPR >= 64) return ((row & 7) << 1) | ((row >> 3) & 1);
+    else if constexpr (CPR >= 16) return ((row & 3) << 2) | ((row >> 2) & 3);
     else return (((row >> 1) & 1) << 2) | ((row >> 2) & 3);
   }
 };

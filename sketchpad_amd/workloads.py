@@ -171,6 +171,19 @@ def decode_gemma4_d256() -> DecodeWorkload:
                           tables, nblk, window_left=1023)
 
 
+def decode_gemma4_d512() -> DecodeWorkload:
+    """Gemma-4's global-attention layers (head_dim 512, 16 query / 8 KV heads, no window;
+    gemma4.rs:82-107) at C2's batch: 64 sequences with contexts U[512, 4096], bf16, block size
+    16. Not one of the five benchmark configurations."""
+    seed = seed_for(8)
+    rng = np.random.default_rng(seed)
+    lens = rng.integers(512, 4096, size=64, endpoint=True).astype(np.int32)
+    nblk = int(((lens + 15) // 16).sum())
+    tables = _tables_from_pool(rng, lens, 16, nblk)
+    return DecodeWorkload("gemma4-d512-global-decode", seed, 64, 16, 8, 512, 16, "bf16", lens,
+                          tables, nblk)
+
+
 DECODE_CONFIGS = {"C1": decode_c1, "C2": decode_c2, "C4": decode_c4, "C5": decode_c5}
 
 
@@ -298,6 +311,15 @@ def prefill_gemma4_d256() -> PrefillWorkload:
     lens = rng.integers(256, 2048, size=8, endpoint=True).astype(np.int32)
     return PrefillWorkload("gemma4-d256-window-prefill", seed, lens, 16, 8, 256, "bf16",
                            window_left=1023)
+
+
+def prefill_gemma4_d512() -> PrefillWorkload:
+    """Gemma-4 global-layer prefill: C3's lengths drawn again (8 sequences U[256, 2048]) at
+    head_dim 512, 16 query / 8 KV heads, causal, bf16."""
+    seed = seed_for(9)
+    rng = np.random.default_rng(seed)
+    lens = rng.integers(256, 2048, size=8, endpoint=True).astype(np.int32)
+    return PrefillWorkload("gemma4-d512-global-prefill", seed, lens, 16, 8, 512, "bf16")
 
 
 def make_prefill_tensors(w: PrefillWorkload, device="cuda", with_pool: bool = True) -> dict:
