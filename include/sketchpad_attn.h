@@ -180,7 +180,8 @@ size_t sp_paged_decode_workspace_size(int32_t num_seqs, int32_t num_q_heads,
  *   workspace      : device scratch of at least sp_paged_decode_workspace_size() bytes (no
  *                    initialisation needed). Calls that share a workspace must not overlap.
  * Softmax and accumulation are fp32 for every dtype. GQA groups (Hq / Hkv) up to 16, head_dim
- * 64 or 128 (and 256 for bf16 / f16: Gemma-4's sliding layers, gemma4.rs:94-102), any block_size
+ * 64 or 128 (and 256 and 512 for bf16 / f16: Gemma-4's sliding and global layers,
+ * gemma4.rs:82-107), any block_size
  * (BlockTable takes any, paged_attention.rs:89-148; one that is not a multiple of 16 makes a
  * 16-token tile span several blocks, each row read from the block its position maps to).
  */
@@ -197,9 +198,10 @@ int sp_paged_decode(void* out, const void* q,
  * attn_logit_softcap = 50, :96): every logit becomes logit_softcap * tanh(logit / logit_softcap),
  * logit = (q . k) * scale, before the mask and the softmax. Each *_softcap entry point below is
  * its namesake with that one argument added after `scale`; logit_softcap == 0 is the namesake
- * itself, > 0 runs at head_dim 256 on bf16 / f16 tensors (the sliding-window layers the cap and
- * the W-key window of gemma4.rs:1086-1108 come with; window_left = W - 1) and returns
- * SP_EUNSUPPORTED elsewhere; a negative or non-finite cap is SP_EINVAL.
+ * itself, > 0 runs at head_dims 256 and 512 on bf16 / f16 tensors (Gemma-4's sliding-window
+ * layers, which come with the W-key window of gemma4.rs:1086-1108, window_left = W - 1, and its
+ * global layers, causal without a window) and returns SP_EUNSUPPORTED elsewhere; a negative or
+ * non-finite cap is SP_EINVAL.
  */
 int sp_paged_decode_softcap(void* out, const void* q,
                             const void* k_pool, const void* v_pool, const sp_cache_layout* layout,
@@ -276,7 +278,7 @@ int sp_paged_decode_noalloc(void* out, const void* q,
  *   causal : sp_causal; window_left >= 0 adds the sliding window (see above).
  * Softmax and accumulation are fp32; a query that sees no key gets zeros. f32 (fp32 MFMA, fp32
  * weights: the reference flash_attention's element type), bf16 and f16 (16-bit weights on the
- * bf16/f16 MFMA), head_dim 64 or 128 (and 256 for bf16 / f16), GQA groups of any size.
+ * bf16/f16 MFMA), head_dim 64 or 128 (and 256 and 512 for bf16 / f16), GQA groups of any size.
  */
 int sp_varlen_prefill(void* out, const void* q, const void* k, const void* v,
                       const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
@@ -304,7 +306,9 @@ int sp_varlen_prefill_softcap(void* out, const void* q, const void* k, const voi
  *               holds their fp32 partials, sp_paged_prefill_workspace_size() bytes for the full
  *               split; a smaller (or NULL) workspace lowers the split (NULL: none). The result
  *               does not depend on whether the keys were split beyond fp32 rounding of the
- *               merge. Calls sharing one workspace must not overlap.
+ *               merge. Calls sharing one workspace must not overlap. Head dims 256 and 512
+ *               take no split (their workspace size is 0).
+ * Dtypes, head dims and GQA groups as sp_varlen_prefill.
  */
 size_t sp_paged_prefill_workspace_size(int32_t num_seqs, int32_t max_seqlen_q,
                                        int32_t num_q_heads, const sp_cache_layout* layout,
@@ -397,8 +401,8 @@ int sp_ragged_paged_attention_softcap(void* out, const void* q,
  * f32 tensors (the element type the reference's flash_attention runs, attention.rs:21-25):
  * head_dim 40, 64, 80, 128, 160 or 256 (so the SD-1.x UNet's head dims 40 / 80 / 160 run
  * without padding, sketchpad-unet/src/cubecl.rs:256-316), v_head_dim a multiple of 4 up to
- * 256. bf16 / f16 tensors: head_dim == v_head_dim, 64, 128 or 256. out_dtype any of f32 / bf16 /
- * f16.
+ * 256. bf16 / f16 tensors: head_dim == v_head_dim, 64, 128, 256 or 512. out_dtype any of
+ * f32 / bf16 / f16.
  * The reference scales by head_dim^-0.5.
  */
 int sp_flash_attention_ex(void* out, const void* q, const void* k, const void* v,
