@@ -50,6 +50,13 @@ typedef float pf_f32x4 __attribute__((ext_vector_type(4)));
 typedef short pf_s16x4 __attribute__((ext_vector_type(4)));
 typedef short pf_s16x8 __attribute__((ext_vector_type(8)));
 typedef __attribute__((address_space(3))) pf_s16x4 lds_s16x4;
+typedef unsigned pf_u32x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) pf_u32x4 lds_u32x4;
+
+// LDS byte address of a pointer into a __shared__ array.
+__device__ __forceinline__ unsigned lds_addr(const char* p) {
+  return (unsigned)(uintptr_t)(lds_void*)p;
+}
 
 template <typename T> struct PrefillMfma;
 template <> struct PrefillMfma<bf16_t> {
@@ -1814,13 +1821,18 @@ __global__ void __launch_bounds__(512, 1) prefill_d512_kernel(PrefillArgs a) {
   const int vr = 4 * g + (n >> 2);
   const int v_lane = (vr * RB) | (16 * (((n & 3) >> 1) ^ C::swz(vr))) | (8 * (n & 1));
 
+  // The operand reads take LDS byte addresses: the buffer base (1 KiB aligned, so its low ten
+  // bits are zero) plus the lane part, then an XOR of bits 5-9 per operand and the half's
+  // 16 KiB as the instruction offset. One VALU op per read address, where pointer arithmetic
+  // from the buffer's pointer cost an add more (a base past 64 KiB does not fit the offset).
   // score i of this lane is key t0 + koff(i), koff(i) = 16(i / 4) + 4g + i % 4
   float sc[8];
   auto qk = [&](const char* kb) __attribute__((always_inline)) {
-    int kbl = k_lane;
+    unsigned kbl = lds_addr(kb) + k_lane;
     asm volatile("" : "+v"(kbl));
     auto read_k = [&](int i) __attribute__((always_inline)) {  // operand i: half i & 1, step i / 2
-      return *(const uint4*)(kb + (i & 1) * 16 * RB + (kbl ^ (64 * (i >> 1))));
+      return __builtin_bit_cast(
+          uint4, *(const lds_u32x4*)(uintptr_t)((kbl ^ (64u * (i >> 1))) + (i & 1) * 16 * RB));
     };
     constexpr int AHK = 2;
     uint4 kop[AHK];
@@ -1910,12 +1922,13 @@ __global__ void __launch_bounds__(512, 1) prefill_d512_kernel(PrefillArgs a) {
   // PV product O^T += V^T P^T: output block db (dims 16db ..) takes the V^T operand of keys
   // 4g .. 4g+3 (first transpose read) and 16 + 4g .. +3 (second), k slots 8g .. 8g+7.
   auto pv = [&](const char* vb) __attribute__((always_inline)) {
-    int vbl = v_lane;
+    unsigned vbl = lds_addr(vb) + v_lane;
     asm volatile("" : "+v"(vbl));
     auto read_v = [&](int db) __attribute__((always_inline)) {
-      const char* a0 = vb + (vbl ^ (32 * db));
-      const pf_s16x4 v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(a0));
-      const pf_s16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(a0 + 16 * RB));
+      const unsigned a0 = vbl ^ (32u * db);
+      const pf_s16x4 v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(uintptr_t)a0);
+      const pf_s16x4 v1 =
+          __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(uintptr_t)(a0 + 16 * RB));
       return __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7);
     };
     constexpr int AH = 2;
