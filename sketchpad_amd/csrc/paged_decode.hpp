@@ -47,8 +47,8 @@ struct DecodeArgs {
   int tps;
   int max_splits;
   float scale_log2;  // softmax scale * log2(e)
-  // Logit soft cap (head_dim 256 only): cap_out > 0 turns each raw product s into the exponent
-  // softcap_log2(s, cap_in, cap_out) = cap log2(e) tanh(s scale / cap) instead of
+  // Logit soft cap (head_dims 256 and 512 only): cap_out > 0 turns each raw product s into the
+  // exponent softcap_log2(s, cap_in, cap_out) = cap log2(e) tanh(s scale / cap) instead of
   // s * scale_log2; 0: none.
   float cap_in, cap_out;
   // Fused append (sp_paged_append_decode), or null: the step's new token of sequence s, for KV

@@ -50,8 +50,8 @@ struct PrefillArgs {
   const float* mask;
   int64_t mask_b, mask_h, mask_q;
   float inv_scale;  // 1 / scale (log2(e) with the soft cap: the mask then adds to the exponent)
-  // Logit soft cap (head_dim 256 only): cap_out > 0 turns each raw product s into the exponent
-  // softcap_log2(s, cap_in, cap_out) = cap log2(e) tanh(s scale / cap) instead of
+  // Logit soft cap (head_dims 256 and 512 only): cap_out > 0 turns each raw product s into the
+  // exponent softcap_log2(s, cap_in, cap_out) = cap log2(e) tanh(s scale / cap) instead of
   // s * scale_log2; 0: none.
   float cap_in, cap_out;
 };
