@@ -148,11 +148,11 @@ def test_ragged_decode_only_and_prefill_only():
     _run(only_pre)
 
 
-@pytest.mark.parametrize("d,softcap", [(128, 0.0), (256, 50.0)])
+@pytest.mark.parametrize("d,softcap", [(128, 0.0), (256, 50.0), (512, 50.0)])
 def test_ragged_mixed_graph_capture(d, softcap):
     """The mixed step's fork / join (decode on the library's side stream) captured into a HIP
     graph through torch: four replays, each after eager work that overwrites the output, each
-    bit-identical to the eager call. Also at head dim 256 with Gemma-4's logit soft cap
+    bit-identical to the eager call. Also at head dims 256 and 512 with Gemma-4's logit soft cap
     (sp_ragged_paged_attention_softcap)."""
     w = W.MixedWorkload("mixed-graph", 81, np.array([64, 100], np.int32),
                         np.array([4000, 300], np.int32),
