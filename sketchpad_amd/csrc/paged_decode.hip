@@ -666,7 +666,12 @@ DecodePlan plan_decode(int num_seqs, int hq, int hkv, int head_dim, int max_cont
     //    Mistral batch, 16-head groups, 256 units of 4k-token contexts);
     //  - 32 for groups of at most 4 query heads over contexts of 129-256 tiles with 512 or
     //    more units, where the short per-tile work leaves the merge cheap and finer splits
-    //    balance the ragged lengths better (Llama-3-8B at 64 sequences: 104 against 106 us).
+    //    balance the ragged lengths better (Llama-3-8B at 64 sequences: 104 against 106 us);
+    //  - 96 for the other batches of at least 256 units: fewer, longer splits whose busy
+    //    workgroups come closer to whole rounds of resident slots (measured against 64 on seven
+    //    batches of groups 1-16: 2-7 % faster on all five with 256-2,048 units, e.g. the
+    //    Qwen2.5-7B batch 111.8 -> 108.5 us; 1 % and 11 % slower on the two with 128 and 64
+    //    units, which keep 64).
     tps = 64;
     if (wgs(64) < 512) {
       tps = 32;
@@ -675,6 +680,8 @@ DecodePlan plan_decode(int num_seqs, int hq, int hkv, int head_dim, int max_cont
       tps = 128;
     } else if (p.group <= 4 && units >= 512 && p.max_tiles > 128 && p.max_tiles <= 256) {
       tps = 32;
+    } else if (units >= 256) {
+      tps = 96;
     }
   } else {
     // Compressed tiles are a quarter of a dense one's bytes: start from 64-tile splits and halve
