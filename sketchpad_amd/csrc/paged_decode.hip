@@ -664,14 +664,17 @@ DecodePlan plan_decode(int num_seqs, int hq, int hkv, int head_dim, int max_cont
     //  - 128 when that plan launches 384-512 workgroups: its longest splits then fill the GPU
     //    about once and a half to twice, with the fewest partials to merge (the windowed
     //    Mistral batch, 16-head groups, 256 units of 4k-token contexts);
-    //  - 32 for groups of at most 4 query heads over contexts of 129-256 tiles with 512 or
-    //    more units, where the short per-tile work leaves the merge cheap and finer splits
-    //    balance the ragged lengths better (Llama-3-8B at 64 sequences: 104 against 106 us);
+    //  - 80 for groups of at most 4 query heads over contexts of 129-256 tiles with 512 or
+    //    more units (measured on six such batches against 32, the earlier choice for them, and
+    //    96: 80 was 0.5-5 % faster than 32 on all six, e.g. Llama-3-8B at 64 sequences
+    //    105.0 -> 102.1 us, and level with 96 on average);
     //  - 96 for the other batches of at least 256 units: fewer, longer splits whose busy
     //    workgroups come closer to whole rounds of resident slots (measured against 64 on seven
     //    batches of groups 1-16: 2-7 % faster on all five with 256-2,048 units, e.g. the
     //    Qwen2.5-7B batch 111.8 -> 108.5 us; 1 % and 11 % slower on the two with 128 and 64
     //    units, which keep 64).
+    // (Splitting each sequence's tiles into near-equal parts instead of full splits plus a
+    // remainder measured slower on most of these batches.)
     tps = 64;
     if (wgs(64) < 512) {
       tps = 32;
@@ -679,7 +682,7 @@ DecodePlan plan_decode(int num_seqs, int hq, int hkv, int head_dim, int max_cont
     } else if (wgs(128) >= 384 && wgs(128) <= 512) {
       tps = 128;
     } else if (p.group <= 4 && units >= 512 && p.max_tiles > 128 && p.max_tiles <= 256) {
-      tps = 32;
+      tps = 80;
     } else if (units >= 256) {
       tps = 96;
     }
