@@ -98,7 +98,9 @@ def test_decode_validation(sp_lib):
     need = sp_lib.sp_paged_decode_workspace_size(3, 4, 4096, -1, ctypes.byref(lay))
     assert need > 0
     _expect(_lib.SP_ENOSPACE, call(lay, max_ctx=4096, mbs=256), "workspace")
-    _expect(_lib.SP_ENOSPACE, call(lay, max_ctx=4096, mbs=256, ws=fake, ws_bytes=need - 1),
+    # (the size is the larger of the dense and the PolarQuant plans' partials, so the dense
+    # plan's own boundary is not visible here: a workspace far below it)
+    _expect(_lib.SP_ENOSPACE, call(lay, max_ctx=4096, mbs=256, ws=fake, ws_bytes=need // 8),
             "workspace")
 
 

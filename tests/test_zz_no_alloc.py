@@ -74,13 +74,14 @@ def test_noalloc_decode_rejects_batches_past_the_scratch():
 
 def test_noalloc_decode_runs_where_only_the_polar_plan_passes_the_scratch():
     """sp_paged_decode_workspace_size covers both pool kinds, so it can exceed the 32 MiB scratch
-    for a batch whose dense split plan fits it: 89 sequences x 16 query heads over one KV head
-    with max_context_len 23,552 plan 23 dense splits (17.3 MB of partials) against 46 PolarQuant
-    ones (34.6 MB). The no-allocation call runs such a batch (the scratch check is the dense
-    plan's), bit-identical to sp_paged_decode with the workspace it asks for."""
-    w = W.random_decode(seed=779, num_seqs=89, hq=16, hkv=1, head_dim=128, block_size=16,
+    for a batch whose dense split plan fits it: 256 sequences x 16 query heads over one KV head
+    with max_context_len 19,200 (1,200 tiles) plan 13 dense splits of 96 tiles (28.1 MB of
+    partials) against 22 PolarQuant ones of 56 (47.6 MB). The no-allocation call runs such a
+    batch (the scratch check is the dense plan's), bit-identical to sp_paged_decode with the
+    workspace it asks for."""
+    w = W.random_decode(seed=779, num_seqs=256, hq=16, hkv=1, head_dim=128, block_size=16,
                         dtype="bf16", min_len=1, max_len=300)
-    max_ctx = 23552
+    max_ctx = 19200
     t = W.make_decode_tensors(w)
     lay = w.layout()
     need = sp.paged_decode_workspace_size(w.num_seqs, w.hq, max_ctx, -1, lay)
