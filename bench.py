@@ -19,8 +19,9 @@ line:
              over 10 back-to-back launches (and over 50: sustained MFMA load lowers the clock),
              TFLOP/s over the unmasked (query, key) pairs and the fraction of the 2.5 PFLOP/s
              dense bf16 peak, the C3 append, the C3 RoPE-fused append (sp_rope_kv_append: K
-             rotated into the pool, V copied, Q rotated in place) and the oracle's prefill port
-             on a bounded sample
+             rotated into the pool, V copied, Q rotated in place), the oracle's prefill port
+             on a bounded sample, and (long_sequence) the same kernel on one causal
+             8,192-token sequence at C3's heads
   polar_decode  the same decode step on PolarQuant-compressed pools (sp_polar_kv_append +
              sp_polar_paged_decode): launch time, algorithmic bytes (2 + D/2 per cached
              vector), GB/s, fraction of HBM peak, and the speed-up over the dense decode
@@ -473,6 +474,34 @@ def time_prefill_c3(steps: int, warmup: int):
         "rope_append": {"ms": round(ra_ms, 5), "bytes": rope_bytes,
                         "GBs": round(rope_bytes / (ra_ms * 1e-3) / 1e9, 2)},
     }
+
+
+def time_prefill_long(steps: int):
+    """C3's heads and head dim on one long sequence: a causal 8,192-token prefill (32 / 8 heads,
+    D 128, bf16) through sp_varlen_prefill, for the kernel's MFMA fraction on long key walks
+    beside C3's short ones (same warm-up and 10-launch region as the C3 leg)."""
+    import torch
+    import sketchpad_amd as sp
+    from sketchpad_amd import workloads as W
+
+    c3 = W.prefill_c3()
+    w = W.PrefillWorkload("causal-8192-llama3-8b-heads", c3.seed + 100, np.array([8192], np.int32),
+                          c3.hq, c3.hkv, c3.head_dim, c3.dtype)
+    t = W.make_prefill_tensors(w, with_pool=False)
+    stream = torch.cuda.current_stream()
+
+    def prefill():
+        sp.varlen_prefill(t["out"], t["q"], t["k"], t["v"], t["cu_seqlens"], t["cu_seqlens"],
+                          w.max_seqlen, w.head_dim ** -0.5, stream=stream.cuda_stream)
+
+    _warm(prefill, 3)
+    torch.cuda.synchronize()
+    ms, ms_min = _event_times(stream, prefill, max(10, steps))
+    tflops = w.flops() / (ms * 1e-3) / 1e12
+    return {"workload": f"{w.name}: B=1, L=8192, Hq={w.hq}, Hkv={w.hkv}, D={w.head_dim}, causal",
+            "ms": round(ms, 5), "ms_min": round(ms_min, 5), "tflops": round(tflops, 2),
+            "frac_mfma": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
+            "kernel": "prefill_k32_kernel<bf16,128> (one sp_varlen_prefill call)"}
 
 
 GEMMA4_LOGIT_SOFTCAP = 50.0  # attn_logit_softcap (crates/sketchpad-llm/src/gemma4.rs:96)
@@ -932,6 +961,7 @@ def main():
         wp, pf = time_prefill_c3(max(10, args.steps // 2), 3)
         if not args.no_cpu_baseline:
             pf["cpu_baseline"] = cpu_prefill_baseline(wp, args.cpu_seconds)
+        pf["long_sequence"] = time_prefill_long(10)
         line["prefill"] = pf
     if not args.no_configs:
         # the other benchmark configurations: C4 (one mixed iteration), C5, C1
