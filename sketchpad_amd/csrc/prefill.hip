@@ -1071,9 +1071,42 @@ __global__ void __launch_bounds__(256, 3) prefill_k32_kernel(PrefillArgs a) {
   float x0, x1;
   swap_halves(l_run, x0, x1);
   const float l = x0 + x1;
-  if (my_q >= qe) return;
   const float inv = l > 0.f ? 1.f / l : 0.f;
   constexpr int kSelf = std::is_same<T, bf16_t>::value ? SP_BF16 : SP_F16;  // out = in type
+  if (a.out_dtype == kSelf) {
+    // Straight from the MFMA layout, each store of a wave would put 16 bytes into each of 32
+    // rows. Instead the wave stages its 32 x D block in 8 KiB of LDS and stores whole rows, 16
+    // lanes x 16 bytes per row. The stage is a ring buffer the last step's barrier freed: not
+    // the last tile's (other waves may still read it), and no load is pending into it (the last
+    // step waited for all). With n steps, the last used buffer (n - 1) % 3; the free ones are
+    // n % 3 (waves 0-1) and (n + 1) % 3 (waves 2-3), K half or V half by wave parity. Chunk c
+    // of row r sits at chunk c ^ (r % 16), so the row writes and the 16-lane row reads hit
+    // distinct banks.
+    static_assert(RB == 256 && TILE >= 32 * RB, "a 32-row stage of 16 chunks per row");
+    const int nsteps = kv_end > t_first ? (kv_end - t_first + BN - 1) / BN : 0;
+    const int fb = wave_uniform((nsteps + (wave >> 1)) % 3);
+    char* stage = (wave & 1) ? vl[fb] : kl[fb];
+    const int rsw = l32 & 15;
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int rg = 0; rg < 4; ++rg) {
+        const float o0 = acc[db][rg * 4 + 0] * inv, o1 = acc[db][rg * 4 + 1] * inv;
+        const float o2 = acc[db][rg * 4 + 2] * inv, o3 = acc[db][rg * 4 + 3] * inv;
+        *(uint2*)(stage + l32 * RB + 16 * ((db * 4 + rg) ^ rsw) + 8 * hh) =
+            make_uint2(M::pack(o0, o1), M::pack(o2, o3));
+      }
+    const int cc = lane & 15;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int row = 4 * j + (lane >> 4);
+      const uint4 v = *(const uint4*)(stage + row * RB + 16 * (cc ^ (row & 15)));
+      const int q = wq0 + row;
+      if (q < qe) *(uint4*)(obase + (int64_t)q * a.o_tok * 2 + 16 * cc) = v;
+    }
+    return;
+  }
+  if (my_q >= qe) return;
   const int oes = dtype_size((sp_dtype)a.out_dtype);
   char* op = obase + (int64_t)my_q * a.o_tok * oes;
 #pragma unroll
