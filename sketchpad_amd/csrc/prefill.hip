@@ -692,6 +692,39 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PrefillArgs a) {
   float x0, x1;
   swap_halves(l_run, x0, x1);
   const float l = x0 + x1;
+  constexpr int kSelf = std::is_same<T, bf16_t>::value ? SP_BF16 : SP_F16;  // out = in type
+  if (a.nsplit <= 1 && a.out_dtype == kSelf) {
+    // Straight from the MFMA layout, each store of a wave would put 16 bytes into each of 32
+    // rows. Instead the wave stages its 32 x D block in LDS and stores whole rows, CPR lanes x
+    // 16 bytes per row. The stage is half of a K buffer: after the last step's barrier no wave
+    // reads K (the last step has no next tile) and no load is pending (every wave waited for
+    // all before that barrier); only the V buffer of the last tile may still be read. Waves
+    // 0-1 take kl[0], waves 2-3 kl[1]. Chunk c of row r sits at chunk c ^ (r % CPR), so the
+    // row writes and the row reads spread over the banks.
+    static_assert(TILE >= 64 * RB, "two 32-row stages per K buffer");
+    const float inv = l > 0.f ? 1.f / l : 0.f;
+    char* stage = kl[wave >> 1] + (wave & 1) * 32 * RB;
+    const int rsw = l32 & (CPR - 1);
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int rg = 0; rg < 4; ++rg) {
+        const float o0 = acc[db][rg * 4 + 0] * inv, o1 = acc[db][rg * 4 + 1] * inv;
+        const float o2 = acc[db][rg * 4 + 2] * inv, o3 = acc[db][rg * 4 + 3] * inv;
+        *(uint2*)(stage + l32 * RB + 16 * ((db * 4 + rg) ^ rsw) + 8 * hh) =
+            make_uint2(M::pack(o0, o1), M::pack(o2, o3));
+      }
+    constexpr int RPI_O = 64 / CPR;  // rows per store instruction
+    const int cc = lane % CPR;
+#pragma unroll
+    for (int j = 0; j < 32 / RPI_O; ++j) {
+      const int row = RPI_O * j + lane / CPR;
+      const uint4 v = *(const uint4*)(stage + row * RB + 16 * (cc ^ (row & (CPR - 1))));
+      const int q = wq0 + row;
+      if (q < qe) *(uint4*)(obase + (int64_t)q * a.o_tok * 2 + 16 * cc) = v;
+    }
+    return;
+  }
   if (my_q >= qe) return;
   if (a.nsplit > 1) {
     // partial record (m, l, -, -, acc[D]) of this split; m is the offset the weights are
@@ -712,7 +745,6 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PrefillArgs a) {
     return;
   }
   const float inv = l > 0.f ? 1.f / l : 0.f;
-  constexpr int kSelf = std::is_same<T, bf16_t>::value ? SP_BF16 : SP_F16;  // out = in type
   const int oes = dtype_size((sp_dtype)a.out_dtype);
   char* op = obase + (int64_t)my_q * a.o_tok * oes;
 #pragma unroll
