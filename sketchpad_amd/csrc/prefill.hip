@@ -166,6 +166,43 @@ __device__ __forceinline__ void lds_dma16x4(const char* b0, const char* b1, cons
       : "memory");
 }
 
+// A wave's normalised 32 x D output block, stored as whole rows in the input's 16-bit type. In
+// the O^T MFMA layout lane (l32, hh) holds dims 32db + 8rg + 4hh .. +3 of query l32, so a store
+// straight from there would put 16 bytes into each of 32 rows. The block goes instead through
+// `stage`, 32 rows x SD dims (SD = min(D, 128)) of LDS that no other wave touches meanwhile, in
+// D / SD passes: the lanes write their values there (chunk c of row r at chunk c ^ (r % CPS), so
+// that the writes and the row reads spread over the banks), then read it back row-wise and
+// store CPS lanes x 16 bytes per row. A wave's LDS accesses run in order, so a pass's writes do
+// not overtake the previous pass's reads. Rows at or past qe are not stored.
+template <typename M, int D>
+__device__ __forceinline__ void store_rows_staged(const pf_f32x16* acc, float inv, char* stage,
+                                                  char* obase, int64_t o_tok, int wq0, int qe,
+                                                  int lane) {
+  constexpr int SD = D < 128 ? D : 128, SRB = SD * 2, CPS = SRB / 16, DBS = SD / 32;
+  constexpr int RPS = 64 / CPS;  // rows per store instruction
+  static_assert(D % SD == 0 && CPS * 16 == SRB, "whole passes of 16-byte chunks");
+  const int l32 = lane & 31, hh = lane >> 5, rsw = l32 & (CPS - 1), cc = lane % CPS;
+#pragma unroll
+  for (int p = 0; p < D / SD; ++p) {
+#pragma unroll
+    for (int db = 0; db < DBS; ++db)
+#pragma unroll
+      for (int rg = 0; rg < 4; ++rg) {
+        const pf_f32x16& A = acc[p * DBS + db];
+        *(uint2*)(stage + l32 * SRB + 16 * ((db * 4 + rg) ^ rsw) + 8 * hh) =
+            make_uint2(M::pack(A[rg * 4 + 0] * inv, A[rg * 4 + 1] * inv),
+                       M::pack(A[rg * 4 + 2] * inv, A[rg * 4 + 3] * inv));
+      }
+#pragma unroll
+    for (int j = 0; j < 32 / RPS; ++j) {
+      const int row = RPS * j + lane / CPS;
+      const uint4 v = *(const uint4*)(stage + row * SRB + 16 * (cc ^ (row & (CPS - 1))));
+      const int q = wq0 + row;
+      if (q < qe) *(uint4*)(obase + (int64_t)q * o_tok * 2 + p * SRB + 16 * cc) = v;
+    }
+  }
+}
+
 // Stands in for cu_seqlens when a batch has none, so the kernel's length loads need no branch.
 __constant__ int32_t kPrefillZeroPair[2] = {0, 0};
 
@@ -694,35 +731,13 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PrefillArgs a) {
   const float l = x0 + x1;
   constexpr int kSelf = std::is_same<T, bf16_t>::value ? SP_BF16 : SP_F16;  // out = in type
   if (a.nsplit <= 1 && a.out_dtype == kSelf) {
-    // Straight from the MFMA layout, each store of a wave would put 16 bytes into each of 32
-    // rows. Instead the wave stages its 32 x D block in LDS and stores whole rows, CPR lanes x
-    // 16 bytes per row. The stage is half of a K buffer: after the last step's barrier no wave
-    // reads K (the last step has no next tile) and no load is pending (every wave waited for
-    // all before that barrier); only the V buffer of the last tile may still be read. Waves
-    // 0-1 take kl[0], waves 2-3 kl[1]. Chunk c of row r sits at chunk c ^ (r % CPR), so the
-    // row writes and the row reads spread over the banks.
+    // Whole output rows through an LDS stage (store_rows_staged). The stage is half of a K
+    // buffer: after the last step's barrier no wave reads K (the last step has no next tile) and
+    // no load is pending (every wave waited for all before that barrier); only the V buffer of
+    // the last tile may still be read. Waves 0-1 take kl[0], waves 2-3 kl[1].
     static_assert(TILE >= 64 * RB, "two 32-row stages per K buffer");
-    const float inv = l > 0.f ? 1.f / l : 0.f;
-    char* stage = kl[wave >> 1] + (wave & 1) * 32 * RB;
-    const int rsw = l32 & (CPR - 1);
-#pragma unroll
-    for (int db = 0; db < DB; ++db)
-#pragma unroll
-      for (int rg = 0; rg < 4; ++rg) {
-        const float o0 = acc[db][rg * 4 + 0] * inv, o1 = acc[db][rg * 4 + 1] * inv;
-        const float o2 = acc[db][rg * 4 + 2] * inv, o3 = acc[db][rg * 4 + 3] * inv;
-        *(uint2*)(stage + l32 * RB + 16 * ((db * 4 + rg) ^ rsw) + 8 * hh) =
-            make_uint2(M::pack(o0, o1), M::pack(o2, o3));
-      }
-    constexpr int RPI_O = 64 / CPR;  // rows per store instruction
-    const int cc = lane % CPR;
-#pragma unroll
-    for (int j = 0; j < 32 / RPI_O; ++j) {
-      const int row = RPI_O * j + lane / CPR;
-      const uint4 v = *(const uint4*)(stage + row * RB + 16 * (cc ^ (row & (CPR - 1))));
-      const int q = wq0 + row;
-      if (q < qe) *(uint4*)(obase + (int64_t)q * a.o_tok * 2 + 16 * cc) = v;
-    }
+    store_rows_staged<M, D>(acc, l > 0.f ? 1.f / l : 0.f, kl[wave >> 1] + (wave & 1) * 32 * RB,
+                            obase, a.o_tok, wq0, qe, lane);
     return;
   }
   if (my_q >= qe) return;
@@ -1106,36 +1121,16 @@ __global__ void __launch_bounds__(256, 3) prefill_k32_kernel(PrefillArgs a) {
   const float inv = l > 0.f ? 1.f / l : 0.f;
   constexpr int kSelf = std::is_same<T, bf16_t>::value ? SP_BF16 : SP_F16;  // out = in type
   if (a.out_dtype == kSelf) {
-    // Straight from the MFMA layout, each store of a wave would put 16 bytes into each of 32
-    // rows. Instead the wave stages its 32 x D block in 8 KiB of LDS and stores whole rows, 16
-    // lanes x 16 bytes per row. The stage is a ring buffer the last step's barrier freed: not
-    // the last tile's (other waves may still read it), and no load is pending into it (the last
-    // step waited for all). With n steps, the last used buffer (n - 1) % 3; the free ones are
-    // n % 3 (waves 0-1) and (n + 1) % 3 (waves 2-3), K half or V half by wave parity. Chunk c
-    // of row r sits at chunk c ^ (r % 16), so the row writes and the 16-lane row reads hit
-    // distinct banks.
-    static_assert(RB == 256 && TILE >= 32 * RB, "a 32-row stage of 16 chunks per row");
+    // Whole output rows through an LDS stage (store_rows_staged). The stage is a ring buffer the
+    // last step's barrier freed: not the last tile's (other waves may still read it), and no
+    // load is pending into it (the last step waited for all). With n steps, the last used
+    // buffer is (n - 1) % 3; the free ones are n % 3 (waves 0-1) and (n + 1) % 3 (waves 2-3),
+    // K half or V half by wave parity.
+    static_assert(TILE >= 32 * RB, "a 32-row stage per K or V buffer");
     const int nsteps = kv_end > t_first ? (kv_end - t_first + BN - 1) / BN : 0;
     const int fb = wave_uniform((nsteps + (wave >> 1)) % 3);
-    char* stage = (wave & 1) ? vl[fb] : kl[fb];
-    const int rsw = l32 & 15;
-#pragma unroll
-    for (int db = 0; db < DB; ++db)
-#pragma unroll
-      for (int rg = 0; rg < 4; ++rg) {
-        const float o0 = acc[db][rg * 4 + 0] * inv, o1 = acc[db][rg * 4 + 1] * inv;
-        const float o2 = acc[db][rg * 4 + 2] * inv, o3 = acc[db][rg * 4 + 3] * inv;
-        *(uint2*)(stage + l32 * RB + 16 * ((db * 4 + rg) ^ rsw) + 8 * hh) =
-            make_uint2(M::pack(o0, o1), M::pack(o2, o3));
-      }
-    const int cc = lane & 15;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int row = 4 * j + (lane >> 4);
-      const uint4 v = *(const uint4*)(stage + row * RB + 16 * (cc ^ (row & 15)));
-      const int q = wq0 + row;
-      if (q < qe) *(uint4*)(obase + (int64_t)q * a.o_tok * 2 + 16 * cc) = v;
-    }
+    store_rows_staged<M, D>(acc, inv, (wave & 1) ? vl[fb] : kl[fb], obase, a.o_tok, wq0, qe,
+                            lane);
     return;
   }
   if (my_q >= qe) return;
@@ -1628,6 +1623,21 @@ __global__ void __launch_bounds__(256, 2) prefill_wide_kernel(PrefillArgs a) {
   float x0, x1;
   swap_halves(l_run, x0, x1);
   const float l = x0 + x1;
+  constexpr int kSelf = std::is_same<T, bf16_t>::value ? SP_BF16 : SP_F16;  // out = in type
+  if (a.nsplit <= 1 && a.out_dtype == kSelf) {
+    // Whole output rows through an LDS stage (store_rows_staged, two passes of 128 dims). The
+    // stage is a quarter of the buffer pair the last step did not read: with n steps the last
+    // read pair n - 1 (mod 2), and no load is pending into pair n % 2 (the last step issued
+    // none and waited for all before its barrier, which also ended every read of that pair).
+    // Waves 0-1 take kl, waves 2-3 vl, 8 KiB each.
+    static_assert(TILE >= 2 * 32 * 256, "two 32-row x 128-dim stages per buffer");
+    const int nsteps = kv_end > t_first ? (kv_end - t_first + BN - 1) / BN : 0;
+    const int fb = wave_uniform(nsteps % 2);
+    store_rows_staged<M, D>(acc, l > 0.f ? 1.f / l : 0.f,
+                            ((wave >> 1) ? vl[fb] : kl[fb]) + (wave & 1) * 32 * 256, obase,
+                            a.o_tok, wq0, qe, lane);
+    return;
+  }
   if (my_q >= qe) return;
   if (a.nsplit > 1) {
     // partial record (m, l, -, -, acc[D]) of this split; m is the offset the weights are
@@ -1648,7 +1658,6 @@ __global__ void __launch_bounds__(256, 2) prefill_wide_kernel(PrefillArgs a) {
     return;
   }
   const float inv = l > 0.f ? 1.f / l : 0.f;
-  constexpr int kSelf = std::is_same<T, bf16_t>::value ? SP_BF16 : SP_F16;  // out = in type
   const int oes = dtype_size((sp_dtype)a.out_dtype);
   char* op = obase + (int64_t)my_q * a.o_tok * oes;
 #pragma unroll
