@@ -203,6 +203,34 @@ __device__ __forceinline__ void store_rows_staged(const pf_f32x16* acc, float in
   }
 }
 
+// The same for a wave of 16 queries on v_mfma_f32_16x16x32 (head dim 512): lane (n, g) holds
+// dims 16db + 4g .. +3 of query n, so a direct store puts 32 bytes into each of 16 rows. The
+// 16 x 512 block goes through a 16-row x 256-dim stage (8 KiB) in two passes; chunk c of row r
+// sits at chunk c ^ (r % 16), and every store writes 32 lanes x 16 bytes of a row.
+template <typename M>
+__device__ __forceinline__ void store_rows_staged16(const pf_f32x4* acc, float inv, char* stage,
+                                                    char* obase, int64_t o_tok, int wq0, int qe,
+                                                    int lane) {
+  constexpr int D = 512, SD = 256, SRB = SD * 2, CPS = SRB / 16, DBS = SD / 16;
+  const int n = lane & 15, g = lane >> 4, cc = lane & 31;
+#pragma unroll
+  for (int p = 0; p < D / SD; ++p) {
+#pragma unroll
+    for (int db = 0; db < DBS; ++db) {
+      const pf_f32x4& A = acc[p * DBS + db];
+      *(uint2*)(stage + n * SRB + 16 * ((2 * db + (g >> 1)) ^ n) + 8 * (g & 1)) =
+          make_uint2(M::pack(A[0] * inv, A[1] * inv), M::pack(A[2] * inv, A[3] * inv));
+    }
+#pragma unroll
+    for (int j = 0; j < 16 / (64 / CPS); ++j) {
+      const int row = 2 * j + (lane >> 5);
+      const uint4 v = *(const uint4*)(stage + row * SRB + 16 * (cc ^ row));
+      const int q = wq0 + row;
+      if (q < qe) *(uint4*)(obase + (int64_t)q * o_tok * 2 + p * SRB + 16 * cc) = v;
+    }
+  }
+}
+
 // Stands in for cu_seqlens when a batch has none, so the kernel's length loads need no branch.
 __constant__ int32_t kPrefillZeroPair[2] = {0, 0};
 
@@ -2061,9 +2089,22 @@ __global__ void __launch_bounds__(512, 1) prefill_d512_kernel(PrefillArgs a) {
   float l = l_run;
   l += xor16(l);
   l += xor32(l);
-  if (my_q >= qe) return;
   const float inv = l > 0.f ? 1.f / l : 0.f;
   constexpr int kSelf = std::is_same<T, bf16_t>::value ? SP_BF16 : SP_F16;  // out = in type
+  if (a.out_dtype == kSelf) {
+    // Whole output rows through an LDS stage (store_rows_staged16). The stage is an eighth of
+    // the buffer pair the last step did not read: with n steps the last read pair n - 1 (mod 2),
+    // and no load is pending into pair n % 2 (the last step issued none and waited for all
+    // before its barrier, which also ended every read of that pair). Waves 0-3 take kl, waves
+    // 4-7 vl, 8 KiB each.
+    static_assert(TILE >= 4 * 16 * 512, "four 16-row x 256-dim stages per buffer");
+    const int nsteps = kv_end > t_first ? (kv_end - t_first + BN - 1) / BN : 0;
+    const int fb = wave_uniform(nsteps % 2);
+    store_rows_staged16<M>(acc, inv, ((wave >> 2) ? vl[fb] : kl[fb]) + (wave & 3) * 16 * 512,
+                           obase, a.o_tok, wq0, qe, lane);
+    return;
+  }
+  if (my_q >= qe) return;
   const int oes = dtype_size((sp_dtype)a.out_dtype);
   char* op = obase + (int64_t)my_q * a.o_tok * oes;
 #pragma unroll
