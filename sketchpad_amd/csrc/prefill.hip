@@ -32,6 +32,9 @@
 // Only tiles that cross the causal diagonal, the window edge or the sequence end are masked.
 // Workgroups are ordered with the KV head fastest (all query heads of one KV head share an XCD's
 // L2) and the heaviest causal query blocks first.
+// Outputs in the input type leave through LDS: each wave stages its block in a tile buffer that
+// no wave needs any more and stores whole rows (store_rows_staged), where a store from the O^T
+// registers would write 16 bytes into each of 32 rows.
 #include "prefill.hpp"
 
 #include <math.h>
