@@ -45,7 +45,10 @@ def load_kernels(d: Path) -> dict:
     intermediate files go to the directory d."""
     t = _tools()
     fatbin = d / "fatbin.bin"
-    subprocess.run([t["objcopy"], "--dump-section", f".hip_fatbin={fatbin}", str(LIB)], check=True)
+    # input and output both named: objcopy given one file rewrites it, here a library that
+    # this test process (or another test in it) may have mapped
+    subprocess.run([t["objcopy"], "-O", "binary", "--only-section=.hip_fatbin", str(LIB),
+                    str(fatbin)], check=True)
     data = fatbin.read_bytes()
     starts = [m.start() for m in re.finditer(re.escape(BUNDLE_MAGIC), data)] + [len(data)]
     assert len(starts) > 1, "no offload bundle in .hip_fatbin"
