@@ -173,7 +173,8 @@ size_t sp_paged_decode_workspace_size(int32_t num_seqs, int32_t num_q_heads,
  * followed by repeat_kv + softmax((q k^T) * scale) v (transformer.rs:227-243). Decode applies
  * no mask in the reference (llama.rs:255-260); window_left >= 0 restricts sequence s to keys
  * [context_lens[s]-1-window_left, context_lens[s]) (Mistral window: window_left = W).
- *   q, out         : [num_seqs, num_q_heads, D] contiguous, dtype
+ *   q, out         : [num_seqs, num_q_heads, D] contiguous, dtype; q, out, the pools and the
+ *                    workspace 16-byte aligned (else SP_EINVAL)
  *   block_tables   : [num_seqs, max_blocks_per_seq] int32 (device)
  *   context_lens   : [num_seqs] int32 (device), each in [0, max_context_len]; the count
  *                    includes the token just appended. A zero-length context yields zeros.

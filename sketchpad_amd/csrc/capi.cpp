@@ -271,8 +271,9 @@ static int decode_setup(const char* fn, void* out, const void* q, const void* k_
   if (p.ws_bytes > 0 && (!workspace || workspace_bytes < p.ws_bytes))
     return fail(SP_ENOSPACE, "%s: workspace of %zu bytes, %zu required", fn, workspace_bytes,
                 p.ws_bytes);
-  if (((uintptr_t)q | (uintptr_t)k_pool | (uintptr_t)v_pool | (uintptr_t)workspace) & 15)
-    return fail(SP_EINVAL, "%s: q, pools and workspace must be 16-byte aligned", fn);
+  if (((uintptr_t)out | (uintptr_t)q | (uintptr_t)k_pool | (uintptr_t)v_pool |
+       (uintptr_t)workspace) & 15)
+    return fail(SP_EINVAL, "%s: out, q, pools and workspace must be 16-byte aligned", fn);
   a->out = out;
   a->q = q;
   a->kpool = (const char*)k_pool;

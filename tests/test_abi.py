@@ -108,8 +108,9 @@ def test_append_decode_validation(sp_lib):
     f = sp_lib.sp_paged_append_decode
     fake = ctypes.c_void_p(0x1000)
 
-    def call(lay, kn=fake, vn=fake, ts=256, hs=64, hq=4, max_ctx=32, mbs=2, seqs=3, dtype=1):
-        return f(fake, fake, fake, fake, ctypes.byref(lay), kn, vn, ts, hs, fake, mbs, fake,
+    def call(lay, kn=fake, vn=fake, ts=256, hs=64, hq=4, max_ctx=32, mbs=2, seqs=3, dtype=1,
+             out=fake):
+        return f(out, fake, fake, fake, ctypes.byref(lay), kn, vn, ts, hs, fake, mbs, fake,
                  max_ctx, seqs, hq, 0.125, -1, dtype, None, 0, None)
 
     # the decode's own checks come first
@@ -121,6 +122,7 @@ def test_append_decode_validation(sp_lib):
     _expect(_lib.SP_EINVAL, call(_lay(), ts=-1), "negative stride")
     _expect(_lib.SP_EINVAL, call(_lay(), hs=4), "16-byte aligned")         # 8 bytes (bf16)
     _expect(_lib.SP_EINVAL, call(_lay(), kn=ctypes.c_void_p(0x1008)), "16-byte aligned")
+    _expect(_lib.SP_EINVAL, call(_lay(), out=ctypes.c_void_p(0x1008)), "16-byte aligned")
     assert call(_lay(), seqs=0) == 0  # an empty batch enqueues nothing
 
 
