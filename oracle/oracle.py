@@ -7,12 +7,15 @@ item it restates; sp_oracle.h lists the check that pins it.
 from __future__ import annotations
 
 import ctypes
+import os
 from ctypes import POINTER, c_double, c_float, c_int, c_int32, c_int64, c_void_p
 from pathlib import Path
 
 import numpy as np
 
-LIB_PATH = Path(__file__).resolve().parent / "build" / "libsp_oracle.so"
+# SP_ORACLE_LIB: another build of the same source (oracle/sanitize.sh loads its instrumented one)
+LIB_PATH = Path(os.environ.get("SP_ORACLE_LIB") or
+                Path(__file__).resolve().parent / "build" / "libsp_oracle.so")
 
 F32, BF16, F16 = 0, 1, 2
 
